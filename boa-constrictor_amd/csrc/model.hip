@@ -1,0 +1,888 @@
+// Model kernels and the model context of libboa_hip.so: BoaBytePredictor (embedding, L blocks of
+// LayerNorm -> Mamba mixer -> LayerNorm -> GELU feed-forward with a block residual, Linear-ReLU-Linear head)
+// for many chunk lanes at once, plus the fused compress / decompress drivers.
+//
+// Row layout: a launch processes B lanes x Tc positions; row m = b * Tc + t.  The same kernels serve the
+// compress path (Tc = tile length, model parallel in time) and the decompress path (Tc = 1, one recurrent
+// step).  Per-element arithmetic never depends on Tc or on a row's position in a tile:
+//   - GEMMs accumulate each output over K in a fixed order (16-wide K groups, 4 MFMA steps each), with
+//     no split-K, so the result of a row does not depend on M or on the tile it falls in;
+//   - LayerNorm statistics are wave reductions over the row only;
+//   - the conv and selective-scan kernels run the same per-position code whether the state comes from
+//     registers (previous position in the same tile) or from HBM (previous launch).
+// This is what makes the encoder's and decoder's logits bit-identical.
+#include "boa_common.h"
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+#include <algorithm>
+#include <string>
+#include <vector>
+
+#include "../../include/boa_hip.h"
+
+using namespace boa;
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// ================================================================================================
+// Errors (thread-local last message)
+static thread_local std::string g_last_error;
+
+int boa_fail(int code, const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int boa_fail_hip(hipError_t e, const char* what, const char* file, int line) {
+    return boa_fail(BOA_ERR_HIP, "HIP error %d (%s) in %s at %s:%d", (int)e, hipGetErrorString(e), what, file, line);
+}
+
+extern "C" const char* boa_last_error(void) { return g_last_error.c_str(); }
+extern "C" int boa_abi_version(void) { return 1; }
+
+extern "C" int boa_is_device_pointer(const void* p) {
+    hipPointerAttribute_t a;
+    if (hipPointerGetAttributes(&a, p) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return a.type == hipMemoryTypeDevice ? 1 : 0;
+}
+
+// ================================================================================================
+// GEMM: C[M,N] = epilogue( prologue(A)[M,K] * W[N,K]^T )  on MFMA v_mfma_f32_16x16x4_f32.
+//   A row-major (lda), W row-major [N][K] (PyTorch Linear layout, K contiguous), C row-major (ldc).
+//   prologue: optional LayerNorm of each A row (K == LN width; eps 1e-5, biased variance).
+//   epilogue: none | +bias | +bias,GELU(erf) | +bias,ReLU | residual + (acc + bias).
+// Tiling: BM x BN per 256-thread workgroup (2 x 2 waves), BK = 32 per LDS stage, double buffered.
+// Within a 16-wide K group, lane group g = lane/16 supplies k = 4g + s to MFMA step s, so each lane reads
+// one float4 per fragment from LDS.  Rows of the LDS tiles are padded to 36 floats (conflict-free b128
+// reads for the 16 rows a quarter-wave touches).
+enum { EPI_NONE = 0, EPI_BIAS = 1, EPI_GELU = 2, EPI_RELU = 3, EPI_RESID = 4 };
+
+struct GemmArgs {
+    const float* A;
+    int64_t lda;
+    const float* W;
+    const float* bias;
+    const float* R;
+    int64_t ldr;
+    float* C;
+    int64_t ldc;
+    const float* ln_w;
+    const float* ln_b;
+    int64_t M;
+    int N;
+    int K;
+    int mtiles;
+    int ntiles;
+    int per_xcd;
+};
+
+__device__ __forceinline__ float gelu_erf(float v) { return (v * 0.5f) * (1.0f + erff(v * 0.70710678118654752f)); }
+
+template <int BM, int BN, int LNV, int EPI>
+__global__ void __launch_bounds__(256, 2) k_gemm(GemmArgs g) {
+    constexpr int BK = 32, LDK = BK + 4;
+    constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 16, FN = WN / 16;
+    constexpr int A_LD = BM * BK / 4 / 256;
+    constexpr int B_LD = BN * BK / 4 / 256;
+    __shared__ __attribute__((aligned(16))) float sA[2][BM * LDK];
+    __shared__ __attribute__((aligned(16))) float sB[2][BN * LDK];
+    __shared__ float sMu[LNV ? BM : 1];
+    __shared__ float sRs[LNV ? BM : 1];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    // XCD-aware tile order: workgroup i runs on XCD i % 8; give each XCD a contiguous range of tiles,
+    // N-tiles fastest, so concurrently resident workgroups of one XCD share A rows and W in its L2.
+    const int bid = blockIdx.x;
+    const int tile = (bid & 7) * g.per_xcd + (bid >> 3);
+    if (tile >= g.mtiles * g.ntiles) return;
+    const int mt = tile / g.ntiles;
+    const int nt = tile - mt * g.ntiles;
+    const int64_t m0 = (int64_t)mt * BM;
+    const int n0 = nt * BN;
+    const int64_t M = g.M;
+    const int N = g.N, K = g.K;
+
+    if constexpr (LNV > 0) {
+        for (int r = wave; r < BM; r += 4) {
+            const int64_t m = m0 + r;
+            float mu = 0.0f, rs = 0.0f;
+            if (m < M) {
+                const float* row = g.A + m * g.lda;
+                float v[4 * LNV];
+#pragma unroll
+                for (int i = 0; i < LNV; ++i) {
+                    const float4 q = *reinterpret_cast<const float4*>(row + 256 * i + 4 * lane);
+                    v[4 * i + 0] = q.x; v[4 * i + 1] = q.y; v[4 * i + 2] = q.z; v[4 * i + 3] = q.w;
+                }
+                float s = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4 * LNV; ++i) s = s + v[i];
+                s = wave_sum(s);
+                mu = s / (float)(256 * LNV);
+                float sq = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4 * LNV; ++i) {
+                    const float d = v[i] - mu;
+                    sq = sq + d * d;
+                }
+                sq = wave_sum(sq);
+                const float var = sq / (float)(256 * LNV);
+                rs = 1.0f / sqrtf(var + 1e-5f);
+            }
+            if (lane == 0) { sMu[r] = mu; sRs[r] = rs; }
+        }
+        __syncthreads();
+    }
+
+    float4 ra[A_LD], rb[B_LD];
+    auto load_tiles = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < A_LD; ++i) {
+            const int q = tid + 256 * i;
+            const int r = q >> 3, c = (q & 7) * 4;
+            const int64_t m = m0 + r;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (m < M) {
+                v = *reinterpret_cast<const float4*>(g.A + m * g.lda + k0 + c);
+                if constexpr (LNV > 0) {
+                    const float mu = sMu[r], rs = sRs[r];
+                    const float4 w = *reinterpret_cast<const float4*>(g.ln_w + k0 + c);
+                    const float4 b = *reinterpret_cast<const float4*>(g.ln_b + k0 + c);
+                    v.x = ((v.x - mu) * rs) * w.x + b.x;
+                    v.y = ((v.y - mu) * rs) * w.y + b.y;
+                    v.z = ((v.z - mu) * rs) * w.z + b.z;
+                    v.w = ((v.w - mu) * rs) * w.w + b.w;
+                }
+            }
+            ra[i] = v;
+        }
+#pragma unroll
+        for (int i = 0; i < B_LD; ++i) {
+            const int q = tid + 256 * i;
+            const int r = q >> 3, c = (q & 7) * 4;
+            const int n = n0 + r;
+            rb[i] = (n < N) ? *reinterpret_cast<const float4*>(g.W + (int64_t)n * K + k0 + c)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    auto store_tiles = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < A_LD; ++i) {
+            const int q = tid + 256 * i;
+            *reinterpret_cast<float4*>(&sA[buf][(q >> 3) * LDK + (q & 7) * 4]) = ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < B_LD; ++i) {
+            const int q = tid + 256 * i;
+            *reinterpret_cast<float4*>(&sB[buf][(q >> 3) * LDK + (q & 7) * 4]) = rb[i];
+        }
+    };
+
+    floatx4 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    const int KT = K / BK;
+    load_tiles(0);
+    store_tiles(0);
+    __syncthreads();
+    const int arow = wm * WM + (lane & 15);
+    const int brow = wn * WN + (lane & 15);
+    const int kq = 4 * (lane >> 4);
+    for (int kt = 0; kt < KT; ++kt) {
+        const int cur = kt & 1;
+        if (kt + 1 < KT) load_tiles((kt + 1) * BK);
+#pragma unroll
+        for (int kg = 0; kg < 2; ++kg) {
+            float4 a[FM], b[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+                a[i] = *reinterpret_cast<const float4*>(&sA[cur][(arow + 16 * i) * LDK + 16 * kg + kq]);
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                b[j] = *reinterpret_cast<const float4*>(&sB[cur][(brow + 16 * j) * LDK + 16 * kg + kq]);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].x, b[j].x, acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].y, b[j].y, acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].z, b[j].z, acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].w, b[j].w, acc[i][j], 0, 0, 0);
+                }
+        }
+        if (kt + 1 < KT) store_tiles(cur ^ 1);
+        __syncthreads();
+    }
+
+    // epilogue: lane holds rows 4*(lane/16)+r, column lane%16 of each 16x16 output fragment
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int col = n0 + wn * WN + 16 * j + (lane & 15);
+            if (col >= N) continue;
+            float bias = 0.0f;
+            if constexpr (EPI != EPI_NONE) bias = g.bias[col];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t row = m0 + wm * WM + 16 * i + 4 * (lane >> 4) + r;
+                if (row >= M) continue;
+                float v = acc[i][j][r];
+                if constexpr (EPI != EPI_NONE) v = v + bias;
+                if constexpr (EPI == EPI_GELU) v = gelu_erf(v);
+                if constexpr (EPI == EPI_RELU) v = fmaxf(v, 0.0f);
+                if constexpr (EPI == EPI_RESID) v = g.R[row * g.ldr + col] + v;
+                g.C[row * g.ldc + col] = v;
+            }
+        }
+}
+
+template <int BM, int BN, int LNV, int EPI>
+static int launch_gemm_cfg(GemmArgs g, hipStream_t s) {
+    g.mtiles = (int)((g.M + BM - 1) / BM);
+    g.ntiles = (g.N + BN - 1) / BN;
+    const int64_t tiles = (int64_t)g.mtiles * g.ntiles;
+    g.per_xcd = (int)((tiles + 7) / 8);
+    const int64_t grid = (int64_t)g.per_xcd * 8;
+    hipLaunchKernelGGL((k_gemm<BM, BN, LNV, EPI>), dim3((unsigned)grid), dim3(256), 0, s, g);
+    return BOA_OK;
+}
+
+// Picks the tile shape: 128x128 when that still gives >= 2 workgroups per CU, else 64x64.
+template <int LNV, int EPI>
+static int launch_gemm(const GemmArgs& g, hipStream_t s) {
+    const int64_t big = ((g.M + 127) / 128) * (int64_t)((g.N + 127) / 128);
+    if (g.N >= 128 && big >= 512) return launch_gemm_cfg<128, 128, LNV, EPI>(g, s);
+    return launch_gemm_cfg<64, 64, LNV, EPI>(g, s);
+}
+
+static GemmArgs gemm_args(const float* A, int64_t lda, const float* W, const float* bias, float* C, int64_t ldc,
+                          int64_t M, int N, int K) {
+    GemmArgs g;
+    memset(&g, 0, sizeof(g));
+    g.A = A; g.lda = lda; g.W = W; g.bias = bias; g.C = C; g.ldc = ldc; g.M = M; g.N = N; g.K = K;
+    return g;
+}
+
+// ================================================================================================
+// Embedding gathers.  One wavefront per row; lane j copies elements 4j.. of each 256-wide slab.
+__global__ void __launch_bounds__(256) k_embed_bytes(const uint8_t* __restrict__ bytes, int64_t stride,
+                                                    const int32_t* __restrict__ lens, int t0, int Tc,
+                                                    int64_t rows, const float* __restrict__ emb, int d, int V,
+                                                    float* __restrict__ x) {
+    const int64_t m = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int lane = threadIdx.x & 63;
+    if (m >= rows) return;
+    const int64_t b = m / Tc;
+    const int t = (int)(m - b * Tc);
+    const int p = t0 + t;
+    int tok = (p < lens[b]) ? (int)bytes[b * stride + p] : 0;
+    tok = tok < V ? tok : V - 1;  // bytes >= vocab are not codable; keep the gather in bounds
+    for (int c = 4 * lane; c < d; c += 256)
+        *reinterpret_cast<float4*>(x + m * d + c) = *reinterpret_cast<const float4*>(emb + (int64_t)tok * d + c);
+}
+
+__global__ void __launch_bounds__(256) k_embed_tokens(const int32_t* __restrict__ tokens, int64_t tok_stride,
+                                                     int t0, int Tc, int64_t rows, const float* __restrict__ emb,
+                                                     int d, int V, float* __restrict__ x) {
+    const int64_t m = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int lane = threadIdx.x & 63;
+    if (m >= rows) return;
+    const int64_t b = m / Tc;
+    const int t = (int)(m - b * Tc);
+    int tok = tokens[b * tok_stride + t0 + t];
+    tok = tok < 0 ? 0 : (tok >= V ? V - 1 : tok);
+    for (int c = 4 * lane; c < d; c += 256)
+        *reinterpret_cast<float4*>(x + m * d + c) = *reinterpret_cast<const float4*>(emb + (int64_t)tok * d + c);
+}
+
+// ================================================================================================
+// Depthwise causal conv (d_conv = 4) + bias + SiLU, per (lane, channel), sequential over the Tc positions
+// of the launch.  History = the 3 previous x values of the channel, [lane][3][di] in HBM between launches
+// (oldest first, model.py:72 / App. A: xc = b + w0*x[t-3] + w1*x[t-2] + w2*x[t-1] + w3*x[t]).
+__global__ void __launch_bounds__(256) k_conv_silu(const float* __restrict__ xz, int64_t ldxz,
+                                                  float* __restrict__ hist, const float* __restrict__ w,
+                                                  const float* __restrict__ bias, float* __restrict__ xs,
+                                                  int di, int Tc) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t b = blockIdx.y;
+    if (c >= di) return;
+    float* hb = hist + b * 3 * di;
+    float h0 = hb[c], h1 = hb[di + c], h2 = hb[2 * di + c];
+    const float4 wv = *reinterpret_cast<const float4*>(w + 4 * c);
+    const float bb = bias[c];
+    for (int t = 0; t < Tc; ++t) {
+        const int64_t m = b * Tc + t;
+        const float x = xz[m * ldxz + c];
+        float v = bb;
+        v = v + wv.x * h0;
+        v = v + wv.y * h1;
+        v = v + wv.z * h2;
+        v = v + wv.w * x;
+        xs[m * di + c] = v / (1.0f + expf(-v));
+        h0 = h1; h1 = h2; h2 = x;
+    }
+    hb[c] = h0; hb[di + c] = h1; hb[2 * di + c] = h2;
+}
+
+// ================================================================================================
+// Selective scan, fused with dt_proj + softplus, the D skip and the SiLU(z) gate (App. A of the mixer):
+//   dt = softplus(W_dt . dr + b_dt)                  (torch threshold 20)
+//   h_n <- exp(dt * A_n) * h_n + (dt * B_n) * x      A = -exp(A_log), precomputed
+//   y = sum_n h_n * C_n + D * x ;  y <- y * SiLU(z)
+// One thread per (lane, channel), h[16] in registers across the Tc positions; the [dr | B | C] rows of the
+// lane's positions are staged in LDS (uniform across the workgroup).  State [lane][di][NS] in HBM between
+// launches.  y overwrites x in place.
+template <int NS, int R>
+__global__ void __launch_bounds__(256) k_scan(float* __restrict__ xs_y, const float* __restrict__ dbc, int ldd,
+                                             const float* __restrict__ xz, int64_t ldxz,
+                                             const float* __restrict__ dt_w, const float* __restrict__ dt_b,
+                                             const float* __restrict__ Aneg, const float* __restrict__ Dp,
+                                             float* __restrict__ ssm, int di, int Tc) {
+    extern __shared__ float s_dbc[];
+    constexpr int W = R + 2 * NS;
+    const int64_t b = blockIdx.y;
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t row0 = b * Tc;
+    for (int i = threadIdx.x; i < Tc * W; i += blockDim.x) {
+        const int t = i / W, k = i - t * W;
+        s_dbc[i] = dbc[(row0 + t) * ldd + k];
+    }
+    __syncthreads();
+    if (c >= di) return;
+    float h[NS], a[NS], wr[R];
+    float* hp = ssm + (b * di + c) * NS;
+#pragma unroll
+    for (int n = 0; n < NS; n += 4) {
+        const float4 q = *reinterpret_cast<const float4*>(hp + n);
+        h[n] = q.x; h[n + 1] = q.y; h[n + 2] = q.z; h[n + 3] = q.w;
+        const float4 p = *reinterpret_cast<const float4*>(Aneg + (int64_t)c * NS + n);
+        a[n] = p.x; a[n + 1] = p.y; a[n + 2] = p.z; a[n + 3] = p.w;
+    }
+#pragma unroll
+    for (int r = 0; r < R; r += 4) {
+        const float4 q = *reinterpret_cast<const float4*>(dt_w + (int64_t)c * R + r);
+        wr[r] = q.x; wr[r + 1] = q.y; wr[r + 2] = q.z; wr[r + 3] = q.w;
+    }
+    const float bdt = dt_b[c], Dc = Dp[c];
+    for (int t = 0; t < Tc; ++t) {
+        const float* row = s_dbc + t * W;
+        float dt = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) dt = dt + row[r] * wr[r];
+        dt = dt + bdt;
+        dt = (dt > 20.0f) ? dt : log1pf(expf(dt));
+        const int64_t m = row0 + t;
+        const float x = xs_y[m * di + c];
+        const float z = xz[m * ldxz + di + c];
+        float y = 0.0f;
+#pragma unroll
+        for (int n = 0; n < NS; ++n) {
+            const float dA = expf(dt * a[n]);
+            const float dBx = (dt * row[R + n]) * x;
+            h[n] = dA * h[n] + dBx;
+            y = y + h[n] * row[R + NS + n];
+        }
+        y = y + Dc * x;
+        y = y * (z / (1.0f + expf(-z)));
+        xs_y[m * di + c] = y;
+    }
+#pragma unroll
+    for (int n = 0; n < NS; n += 4)
+        *reinterpret_cast<float4*>(hp + n) = make_float4(h[n], h[n + 1], h[n + 2], h[n + 3]);
+}
+
+// ================================================================================================
+// Fused coder kernels (quantiser XQ at PRECISION 24), one wavefront per chunk lane.
+static constexpr int CODER_P = 24;
+
+__global__ void k_enc_init(EncState* st, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) enc_init(st[i]);
+}
+
+// cumulative of symbol s and its weight, from the owner lane (s uniform across the wave)
+__device__ __forceinline__ void xq_sym(const XQ& q, int s, uint32_t& c_s, uint32_t& f_s) {
+    const int j = s & 3;
+    uint32_t cl = q.base, fl = q.f[0];
+    if (j >= 1) { cl += q.f[0]; fl = q.f[1]; }
+    if (j >= 2) { cl += q.f[1]; fl = q.f[2]; }
+    if (j >= 3) { cl += q.f[2]; fl = q.f[3]; }
+    c_s = wave_bcast(cl, s >> 2);
+    f_s = wave_bcast(fl, s >> 2);
+}
+
+// Encodes the symbols predicted by the Tc positions of this launch: the logits of position p (absolute
+// t0 + t) code byte p + 1 of the chunk (codec.py:56-76: step(byte t-1) -> probabilities of byte t).
+__global__ void __launch_bounds__(64) k_encode_tile(const float* __restrict__ logits, int V, int Tc, int t0,
+                                                   const uint8_t* __restrict__ bytes, int64_t stride,
+                                                   const int32_t* __restrict__ lens, EncState* __restrict__ states,
+                                                   uint32_t* __restrict__ words, int64_t pitch) {
+    const int64_t b = blockIdx.x;
+    const int lane = threadIdx.x;
+    const int L = lens[b];
+    if (t0 + 1 >= L) return;
+    EncState st = states[b];
+    const WordSink sink{words + b * pitch, pitch, lane == 0};
+    const uint8_t* src = bytes + b * stride;
+    for (int t = 0; t < Tc; ++t) {
+        const int p = t0 + t;
+        if (p + 1 >= L) break;
+        const int s = src[p + 1];
+        if (s >= V) continue;  // as gpu_range_coder.py:97: symbols outside [0, K) are skipped
+        const float* row = logits + (b * Tc + t) * V;
+        float4 l4 = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (4 * lane + 3 < V) l4 = *reinterpret_cast<const float4*>(row + 4 * lane);
+        else {
+            if (4 * lane + 0 < V) l4.x = row[4 * lane + 0];
+            if (4 * lane + 1 < V) l4.y = row[4 * lane + 1];
+            if (4 * lane + 2 < V) l4.z = row[4 * lane + 2];
+        }
+        XQ q;
+        xq_build(q, l4, lane, V, CODER_P);
+        uint32_t c_s, f_s;
+        xq_sym(q, s, c_s, f_s);
+        const uint32_t lo = xq_cdf_at(q, c_s, s);
+        const uint32_t hi = (s + 1 < V) ? xq_cdf_at(q, c_s + f_s, s + 1) : (1u << CODER_P);
+        enc_push(st, CODER_P, lo, hi - lo, sink);
+    }
+    if (lane == 0) states[b] = st;
+}
+
+__global__ void k_enc_finish(EncState* states, uint32_t* words, int64_t pitch, int32_t* nwords, int32_t* overflow,
+                             int n) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= n) return;
+    EncState st = states[b];
+    const WordSink sink{words + (int64_t)b * pitch, pitch, true};
+    enc_finish(st, sink);
+    states[b] = st;
+    nwords[b] = st.overflow ? 0 : st.nwords;
+    if (st.overflow) overflow[0] = 1;
+}
+
+__global__ void k_dec_init(DecState* states, const uint32_t* payload, const int64_t* off, const int32_t* nwords,
+                           const uint8_t* first, const int32_t* lens, int32_t* tokens, uint8_t* out,
+                           int64_t out_stride, int n) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= n) return;
+    DecState st;
+    dec_init(st, payload + off[b], nwords[b]);
+    states[b] = st;
+    tokens[b] = first[b];
+    if (lens[b] >= 1) out[(int64_t)b * out_stride] = first[b];
+}
+
+// One decode step at position t for every lane with t < len: quantise the logits, find the symbol the
+// coder state points into, advance the state, emit the byte and feed it back as the next token.
+__global__ void __launch_bounds__(64) k_decode_step(const float* __restrict__ logits, int V, int t,
+                                                   const int32_t* __restrict__ lens, DecState* __restrict__ states,
+                                                   const uint32_t* __restrict__ payload,
+                                                   const int64_t* __restrict__ off, const int32_t* __restrict__ nwords,
+                                                   int32_t* __restrict__ tokens, uint8_t* __restrict__ out,
+                                                   int64_t out_stride) {
+    const int64_t b = blockIdx.x;
+    const int lane = threadIdx.x;
+    if (t >= lens[b]) return;
+    DecState st = states[b];
+    const uint32_t* in = payload + off[b];
+    const int32_t nw = nwords[b];
+    const float* row = logits + b * V;
+    float4 l4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (4 * lane + 3 < V) l4 = *reinterpret_cast<const float4*>(row + 4 * lane);
+    else {
+        if (4 * lane + 0 < V) l4.x = row[4 * lane + 0];
+        if (4 * lane + 1 < V) l4.y = row[4 * lane + 1];
+        if (4 * lane + 2 < V) l4.z = row[4 * lane + 2];
+    }
+    XQ q;
+    xq_build(q, l4, lane, V, CODER_P);
+    uint32_t e[4];
+    uint32_t c = q.base;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int k = 4 * lane + j;
+        e[j] = (k < V) ? xq_cdf_at(q, c, k) : (1u << CODER_P);
+        c += q.f[j];
+    }
+    const uint32_t qv = dec_target(st, CODER_P);
+    uint32_t lo, hi;
+    const int s = wave_find_symbol<CODER_P>(e, V, qv, lane, lo, hi);
+    dec_advance(st, CODER_P, lo, hi - lo, in, nw);
+    if (lane == 0) {
+        states[b] = st;
+        tokens[b] = s;
+        out[b * out_stride + t] = (uint8_t)s;
+    }
+}
+
+// Scatter of a tile's logits [B*Tc][V] into [B][len][V] at positions t0..t0+Tc-1.
+__global__ void __launch_bounds__(256) k_scatter_logits(const float* __restrict__ src, int V, int Tc, int t0,
+                                                       int len, int64_t rows, float* __restrict__ dst) {
+    const int64_t m = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int lane = threadIdx.x & 63;
+    if (m >= rows) return;
+    const int64_t b = m / Tc;
+    const int t = (int)(m - b * Tc);
+    const float* s = src + m * V;
+    float* d = dst + (b * len + t0 + t) * V;
+    for (int c = lane; c < V; c += 64) d[c] = s[c];
+}
+
+// ================================================================================================
+// Context
+
+struct LayerW {
+    const float *ln1_w, *ln1_b, *in_w, *in_b, *conv_w, *conv_b, *x_w, *dt_w, *dt_b, *A_log, *D, *out_w, *out_b,
+        *ln2_w, *ln2_b, *ff1_w, *ff1_b, *ff2_w, *ff2_b;
+    float* Aneg;
+};
+
+struct boa_ctx {
+    boa_model_cfg cfg;
+    int d, di, NS, R, V, L, DC;
+    hipStream_t stream = nullptr;
+    int32_t max_lanes = 0, tile_len = 0;
+    int64_t max_rows = 0;
+    float* wblob = nullptr;
+    float* aneg = nullptr;
+    const float *emb = nullptr, *h1_w = nullptr, *h1_b = nullptr, *h2_w = nullptr, *h2_b = nullptr;
+    std::vector<LayerW> layers;
+    float* conv_hist = nullptr;  // [L][max_lanes][3][di]
+    float* ssm = nullptr;        // [L][max_lanes][di][NS]
+    float *x = nullptr, *xz = nullptr, *xs = nullptr, *dbc = nullptr, *mm = nullptr, *logits = nullptr;
+    int32_t* tokens = nullptr;
+    EncState* enc = nullptr;
+    DecState* dec = nullptr;
+    int32_t* flag = nullptr;
+    int64_t device_bytes = 0;
+};
+
+static int64_t weights_floats(const boa_model_cfg& c, int R) {
+    const int64_t d = c.d_model, di = (int64_t)c.expand * c.d_model, NS = c.d_state, V = c.vocab, DC = c.d_conv;
+    const int64_t per = 2 * d + 2 * di * d + 2 * di + di * DC + di + (R + 2 * NS) * di + di * R + di + di * NS + di +
+                        d * di + d + 2 * d + 4 * d * d + 4 * d + d * 4 * d + d;
+    return V * d + c.n_layers * per + d * d + d + V * d + V;
+}
+
+static int resolve_cfg(const boa_model_cfg* in, boa_model_cfg& c, int& R) {
+    if (!in) return boa_fail(BOA_ERR_ARG, "null model config");
+    c = *in;
+    if (c.d_state == 0) c.d_state = 16;
+    if (c.d_conv == 0) c.d_conv = 4;
+    if (c.expand == 0) c.expand = 2;
+    R = c.dt_rank > 0 ? c.dt_rank : (c.d_model + 15) / 16;
+    c.dt_rank = R;
+    if (c.d_model != 256 && c.d_model != 512)
+        return boa_fail(BOA_ERR_ARG, "d_model must be 256 or 512 (got %d)", c.d_model);
+    if (c.n_layers < 1 || c.n_layers > 64) return boa_fail(BOA_ERR_ARG, "n_layers out of range (%d)", c.n_layers);
+    if (c.vocab < 2 || c.vocab > 256) return boa_fail(BOA_ERR_ARG, "vocab must be in [2, 256] (got %d)", c.vocab);
+    if (c.d_state != 16) return boa_fail(BOA_ERR_ARG, "d_state must be 16 (got %d)", c.d_state);
+    if (c.d_conv != 4) return boa_fail(BOA_ERR_ARG, "d_conv must be 4 (got %d)", c.d_conv);
+    if (c.expand != 2) return boa_fail(BOA_ERR_ARG, "expand must be 2 (got %d)", c.expand);
+    if (R != 16 && R != 32) return boa_fail(BOA_ERR_ARG, "dt_rank must be 16 or 32 (got %d)", R);
+    if (c.vocab % 4 != 0) return boa_fail(BOA_ERR_ARG, "vocab must be a multiple of 4 (got %d)", c.vocab);
+    return BOA_OK;
+}
+
+extern "C" int64_t boa_weights_nbytes(const boa_model_cfg* cfg) {
+    boa_model_cfg c;
+    int R;
+    if (resolve_cfg(cfg, c, R) != BOA_OK) return -1;
+    return weights_floats(c, R) * 4;
+}
+
+extern "C" int64_t boa_ctx_device_bytes(const boa_ctx* ctx) { return ctx ? ctx->device_bytes : 0; }
+
+extern "C" int boa_ctx_destroy(boa_ctx* ctx) {
+    if (!ctx) return BOA_OK;
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    else (void)hipDeviceSynchronize();
+    void* ptrs[] = {ctx->wblob, ctx->aneg, ctx->conv_hist, ctx->ssm, ctx->x, ctx->xz, ctx->xs, ctx->dbc,
+                    ctx->mm, ctx->logits, ctx->tokens, ctx->enc, ctx->dec, ctx->flag};
+    for (void* p : ptrs)
+        if (p) (void)hipFree(p);
+    delete ctx;
+    return BOA_OK;
+}
+
+template <typename T>
+static hipError_t dmalloc(boa_ctx* c, T** p, int64_t count) {
+    const int64_t bytes = std::max<int64_t>(count, 1) * (int64_t)sizeof(T);
+    c->device_bytes += bytes;
+    return hipMalloc((void**)p, (size_t)bytes);
+}
+
+extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, int64_t nbytes, int weight_dtype,
+                              int32_t max_lanes, int32_t tile_len, void* stream, boa_ctx** out) {
+    if (!out) return boa_fail(BOA_ERR_ARG, "boa_ctx_create: null output");
+    *out = nullptr;
+    boa_model_cfg c;
+    int R;
+    int rc = resolve_cfg(cfg, c, R);
+    if (rc != BOA_OK) return rc;
+    if (weight_dtype != BOA_WEIGHTS_F32)
+        return boa_fail(BOA_ERR_ARG, "boa_ctx_create: weight dtype %d not supported", weight_dtype);
+    const int64_t nf = weights_floats(c, R);
+    if (!h_weights || nbytes != nf * 4)
+        return boa_fail(BOA_ERR_ARG, "weight blob must be %lld bytes (got %lld)", (long long)(nf * 4), (long long)nbytes);
+    if (max_lanes < 1 || tile_len < 1 || tile_len > 256)
+        return boa_fail(BOA_ERR_ARG, "need max_lanes >= 1 and 1 <= tile_len <= 256 (got %d, %d)", max_lanes, tile_len);
+    const int64_t max_rows = (int64_t)max_lanes * tile_len;
+    if (max_rows > (int64_t)1 << 31) return boa_fail(BOA_ERR_ARG, "max_lanes * tile_len too large");
+
+    boa_ctx* x = new boa_ctx();
+    x->cfg = c;
+    x->d = c.d_model; x->di = c.expand * c.d_model; x->NS = c.d_state; x->R = R; x->V = c.vocab;
+    x->L = c.n_layers; x->DC = c.d_conv;
+    x->stream = reinterpret_cast<hipStream_t>(stream);
+    x->max_lanes = max_lanes; x->tile_len = tile_len; x->max_rows = max_rows;
+    const int d = x->d, di = x->di, NS = x->NS, V = x->V, L = x->L;
+
+    hipError_t e = hipSuccess;
+#define TRY_ALLOC(p, n) do { if (e == hipSuccess) e = dmalloc(x, &(p), (n)); } while (0)
+    TRY_ALLOC(x->wblob, nf);
+    TRY_ALLOC(x->aneg, (int64_t)L * di * NS);
+    TRY_ALLOC(x->conv_hist, (int64_t)L * max_lanes * 3 * di);
+    TRY_ALLOC(x->ssm, (int64_t)L * max_lanes * di * NS);
+    TRY_ALLOC(x->x, max_rows * d);
+    TRY_ALLOC(x->xz, max_rows * std::max(2 * di, 4 * d));
+    TRY_ALLOC(x->xs, max_rows * di);
+    TRY_ALLOC(x->dbc, max_rows * (R + 2 * NS));
+    TRY_ALLOC(x->mm, max_rows * d);
+    TRY_ALLOC(x->logits, max_rows * V);
+    TRY_ALLOC(x->tokens, (int64_t)max_lanes);
+    TRY_ALLOC(x->enc, (int64_t)max_lanes);
+    TRY_ALLOC(x->dec, (int64_t)max_lanes);
+    TRY_ALLOC(x->flag, 1);
+#undef TRY_ALLOC
+    if (e != hipSuccess) {
+        boa_ctx_destroy(x);
+        return boa_fail_hip(e, "boa_ctx_create allocation", __FILE__, __LINE__);
+    }
+    // weight pointers in the flat blob (convert_boa_weights.py:22-133 order)
+    const float* hw = static_cast<const float*>(h_weights);
+    int64_t o = 0;
+    auto take = [&](int64_t n) { const float* p = x->wblob + o; o += n; return p; };
+    x->emb = take((int64_t)V * d);
+    std::vector<float> aneg_host((size_t)L * di * NS);
+    for (int l = 0; l < L; ++l) {
+        LayerW w;
+        w.ln1_w = take(d); w.ln1_b = take(d);
+        w.in_w = take((int64_t)2 * di * d); w.in_b = take(2 * di);
+        w.conv_w = take((int64_t)di * x->DC); w.conv_b = take(di);
+        w.x_w = take((int64_t)(R + 2 * NS) * di);
+        w.dt_w = take((int64_t)di * R); w.dt_b = take(di);
+        const int64_t a_off = o;
+        w.A_log = take((int64_t)di * NS);
+        w.D = take(di);
+        w.out_w = take((int64_t)d * di); w.out_b = take(d);
+        w.ln2_w = take(d); w.ln2_b = take(d);
+        w.ff1_w = take((int64_t)4 * d * d); w.ff1_b = take(4 * d);
+        w.ff2_w = take((int64_t)d * 4 * d); w.ff2_b = take(d);
+        w.Aneg = x->aneg + (int64_t)l * di * NS;
+        for (int64_t i = 0; i < (int64_t)di * NS; ++i)
+            aneg_host[(size_t)l * di * NS + i] = (float)(-exp((double)hw[a_off + i]));  // A = -exp(A_log)
+        x->layers.push_back(w);
+    }
+    x->h1_w = take((int64_t)d * d); x->h1_b = take(d);
+    x->h2_w = take((int64_t)V * d); x->h2_b = take(V);
+    if (o != nf) {
+        boa_ctx_destroy(x);
+        return boa_fail(BOA_ERR_ARG, "internal: weight layout mismatch (%lld vs %lld)", (long long)o, (long long)nf);
+    }
+    e = hipMemcpyAsync(x->wblob, h_weights, (size_t)nbytes, hipMemcpyHostToDevice, x->stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(x->aneg, aneg_host.data(), aneg_host.size() * 4, hipMemcpyHostToDevice, x->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(x->stream);
+    if (e != hipSuccess) {
+        boa_ctx_destroy(x);
+        return boa_fail_hip(e, "boa_ctx_create upload", __FILE__, __LINE__);
+    }
+    *out = x;
+    return BOA_OK;
+}
+
+extern "C" int boa_state_reset(boa_ctx* x, int32_t lanes) {
+    if (!x || lanes < 0 || lanes > x->max_lanes) return boa_fail(BOA_ERR_ARG, "boa_state_reset: bad lanes");
+    for (int l = 0; l < x->L; ++l) {
+        BOA_HIP_TRY(hipMemsetAsync(x->conv_hist + (int64_t)l * x->max_lanes * 3 * x->di, 0,
+                                   sizeof(float) * (size_t)lanes * 3 * x->di, x->stream));
+        BOA_HIP_TRY(hipMemsetAsync(x->ssm + (int64_t)l * x->max_lanes * x->di * x->NS, 0,
+                                   sizeof(float) * (size_t)lanes * x->di * x->NS, x->stream));
+    }
+    return BOA_OK;
+}
+
+// One block of the model over B lanes x Tc positions, in place on ctx->x.
+static int run_layer(boa_ctx* x, int l, int B, int Tc) {
+    const LayerW& w = x->layers[l];
+    const int d = x->d, di = x->di, NS = x->NS, R = x->R;
+    const int64_t M = (int64_t)B * Tc;
+    hipStream_t s = x->stream;
+    int rc;
+    // LN1 + in_proj -> xz [M][2di]
+    {
+        GemmArgs g = gemm_args(x->x, d, w.in_w, w.in_b, x->xz, 2 * di, M, 2 * di, d);
+        g.ln_w = w.ln1_w; g.ln_b = w.ln1_b;
+        rc = (d == 256) ? launch_gemm<1, EPI_BIAS>(g, s) : launch_gemm<2, EPI_BIAS>(g, s);
+        if (rc) return rc;
+    }
+    // conv + SiLU -> xs
+    hipLaunchKernelGGL(k_conv_silu, dim3((di + 255) / 256, B), dim3(256), 0, s, x->xz, (int64_t)2 * di,
+                       x->conv_hist + (int64_t)l * x->max_lanes * 3 * di, w.conv_w, w.conv_b, x->xs, di, Tc);
+    // x_proj -> dbc [M][R+2NS]
+    {
+        GemmArgs g = gemm_args(x->xs, di, w.x_w, nullptr, x->dbc, R + 2 * NS, M, R + 2 * NS, di);
+        rc = launch_gemm_cfg<64, 64, 0, EPI_NONE>(g, s);
+        if (rc) return rc;
+    }
+    // dt_proj + softplus + scan + D + gate, y in place of xs
+    {
+        const size_t lds = sizeof(float) * (size_t)Tc * (R + 2 * NS);
+        float* ssm = x->ssm + (int64_t)l * x->max_lanes * di * NS;
+        if (R == 16)
+            hipLaunchKernelGGL((k_scan<16, 16>), dim3((di + 255) / 256, B), dim3(256), lds, s, x->xs, x->dbc,
+                               R + 2 * NS, x->xz, (int64_t)2 * di, w.dt_w, w.dt_b, w.Aneg, w.D, ssm, di, Tc);
+        else
+            hipLaunchKernelGGL((k_scan<16, 32>), dim3((di + 255) / 256, B), dim3(256), lds, s, x->xs, x->dbc,
+                               R + 2 * NS, x->xz, (int64_t)2 * di, w.dt_w, w.dt_b, w.Aneg, w.D, ssm, di, Tc);
+    }
+    // out_proj -> mm [M][d]
+    {
+        GemmArgs g = gemm_args(x->xs, di, w.out_w, w.out_b, x->mm, d, M, d, di);
+        rc = launch_gemm<0, EPI_BIAS>(g, s);
+        if (rc) return rc;
+    }
+    // LN2 + FF1 + GELU -> g [M][4d] (reuses xz)
+    {
+        GemmArgs g = gemm_args(x->mm, d, w.ff1_w, w.ff1_b, x->xz, 4 * d, M, 4 * d, d);
+        g.ln_w = w.ln2_w; g.ln_b = w.ln2_b;
+        rc = (d == 256) ? launch_gemm<1, EPI_GELU>(g, s) : launch_gemm<2, EPI_GELU>(g, s);
+        if (rc) return rc;
+    }
+    // FF2 + bias + block residual -> x
+    {
+        GemmArgs g = gemm_args(x->xz, 4 * d, w.ff2_w, w.ff2_b, x->x, d, M, d, 4 * d);
+        g.R = x->x; g.ldr = d;
+        rc = launch_gemm<0, EPI_RESID>(g, s);
+        if (rc) return rc;
+    }
+    return BOA_OK;
+}
+
+// Full model over B x Tc rows already embedded in ctx->x; logits to `out` (ld V).
+static int run_model(boa_ctx* x, int B, int Tc, float* out) {
+    const int d = x->d, V = x->V;
+    const int64_t M = (int64_t)B * Tc;
+    for (int l = 0; l < x->L; ++l) {
+        int rc = run_layer(x, l, B, Tc);
+        if (rc) return rc;
+    }
+    GemmArgs g1 = gemm_args(x->x, d, x->h1_w, x->h1_b, x->mm, d, M, d, d);
+    int rc = launch_gemm<0, EPI_RELU>(g1, x->stream);
+    if (rc) return rc;
+    GemmArgs g2 = gemm_args(x->mm, d, x->h2_w, x->h2_b, out, V, M, V, d);
+    rc = launch_gemm<0, EPI_BIAS>(g2, x->stream);
+    if (rc) return rc;
+    BOA_HIP_TRY(hipGetLastError());
+    return BOA_OK;
+}
+
+static unsigned row_blocks(int64_t rows) { return (unsigned)((rows + 3) / 4); }  // 4 waves per 256-thread block
+
+extern "C" int boa_model_step(boa_ctx* x, const int32_t* d_tokens, int32_t lanes, float* d_logits) {
+    if (!x || !d_tokens || !d_logits || lanes < 1 || lanes > x->max_lanes)
+        return boa_fail(BOA_ERR_ARG, "boa_model_step: bad arguments");
+    hipLaunchKernelGGL(k_embed_tokens, dim3(row_blocks(lanes)), dim3(256), 0, x->stream, d_tokens, (int64_t)1, 0, 1,
+                       (int64_t)lanes, x->emb, x->d, x->V, x->x);
+    return run_model(x, lanes, 1, d_logits);
+}
+
+extern "C" int boa_model_forward(boa_ctx* x, const int32_t* d_tokens, int64_t tok_stride, int32_t lanes, int32_t len,
+                                 float* d_logits) {
+    if (!x || !d_tokens || !d_logits || lanes < 1 || lanes > x->max_lanes || len < 0 || tok_stride < len)
+        return boa_fail(BOA_ERR_ARG, "boa_model_forward: bad arguments");
+    for (int t0 = 0; t0 < len; t0 += x->tile_len) {
+        const int Tc = std::min(x->tile_len, len - t0);
+        const int64_t rows = (int64_t)lanes * Tc;
+        hipLaunchKernelGGL(k_embed_tokens, dim3(row_blocks(rows)), dim3(256), 0, x->stream, d_tokens, tok_stride, t0,
+                           Tc, rows, x->emb, x->d, x->V, x->x);
+        int rc = run_model(x, lanes, Tc, x->logits);
+        if (rc) return rc;
+        hipLaunchKernelGGL(k_scatter_logits, dim3(row_blocks(rows)), dim3(256), 0, x->stream, x->logits, x->V, Tc, t0,
+                           len, rows, d_logits);
+    }
+    BOA_HIP_TRY(hipGetLastError());
+    return BOA_OK;
+}
+
+extern "C" int boa_compress(boa_ctx* x, const uint8_t* d_bytes, int64_t byte_stride, const int32_t* d_lens,
+                            int32_t lanes, int32_t max_len, uint32_t* d_words, int64_t pitch_words, int32_t* d_nwords) {
+    if (!x || !d_bytes || !d_lens || !d_words || !d_nwords || lanes < 1 || lanes > x->max_lanes || max_len < 1 ||
+        byte_stride < max_len || pitch_words < 1)
+        return boa_fail(BOA_ERR_ARG, "boa_compress: bad arguments");
+    hipStream_t s = x->stream;
+    int rc = boa_state_reset(x, lanes);
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_enc_init, dim3((lanes + 255) / 256), dim3(256), 0, s, x->enc, lanes);
+    BOA_HIP_TRY(hipMemsetAsync(x->flag, 0, sizeof(int32_t), s));
+    const int positions = max_len - 1;  // model inputs 0..max_len-2 predict bytes 1..max_len-1
+    for (int t0 = 0; t0 < positions; t0 += x->tile_len) {
+        const int Tc = std::min(x->tile_len, positions - t0);
+        const int64_t rows = (int64_t)lanes * Tc;
+        hipLaunchKernelGGL(k_embed_bytes, dim3(row_blocks(rows)), dim3(256), 0, s, d_bytes, byte_stride, d_lens, t0, Tc,
+                           rows, x->emb, x->d, x->V, x->x);
+        rc = run_model(x, lanes, Tc, x->logits);
+        if (rc) return rc;
+        hipLaunchKernelGGL(k_encode_tile, dim3(lanes), dim3(64), 0, s, x->logits, x->V, Tc, t0, d_bytes, byte_stride,
+                           d_lens, x->enc, d_words, pitch_words);
+    }
+    hipLaunchKernelGGL(k_enc_finish, dim3((lanes + 255) / 256), dim3(256), 0, s, x->enc, d_words, pitch_words, d_nwords,
+                       x->flag, lanes);
+    BOA_HIP_TRY(hipGetLastError());
+    int32_t flag = 0;
+    BOA_HIP_TRY(hipMemcpyAsync(&flag, x->flag, sizeof(int32_t), hipMemcpyDeviceToHost, s));
+    BOA_HIP_TRY(hipStreamSynchronize(s));
+    if (flag) return boa_fail(BOA_ERR_OVERFLOW, "boa_compress: a stream exceeded pitch_words=%lld", (long long)pitch_words);
+    return BOA_OK;
+}
+
+extern "C" int boa_decompress(boa_ctx* x, const uint32_t* d_payload, const int64_t* d_word_off, const int32_t* d_nwords,
+                              const uint8_t* d_first, const int32_t* d_lens, int32_t lanes, int32_t max_len,
+                              uint8_t* d_out, int64_t out_stride) {
+    if (!x || !d_payload || !d_word_off || !d_nwords || !d_first || !d_lens || !d_out || lanes < 1 ||
+        lanes > x->max_lanes || max_len < 1 || out_stride < max_len)
+        return boa_fail(BOA_ERR_ARG, "boa_decompress: bad arguments");
+    hipStream_t s = x->stream;
+    int rc = boa_state_reset(x, lanes);
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_dec_init, dim3((lanes + 255) / 256), dim3(256), 0, s, x->dec, d_payload, d_word_off, d_nwords,
+                       d_first, d_lens, x->tokens, d_out, out_stride, lanes);
+    for (int t = 1; t < max_len; ++t) {
+        hipLaunchKernelGGL(k_embed_tokens, dim3(row_blocks(lanes)), dim3(256), 0, s, x->tokens, (int64_t)1, 0, 1,
+                           (int64_t)lanes, x->emb, x->d, x->V, x->x);
+        rc = run_model(x, lanes, 1, x->logits);
+        if (rc) return rc;
+        hipLaunchKernelGGL(k_decode_step, dim3(lanes), dim3(64), 0, s, x->logits, x->V, t, d_lens, x->dec, d_payload,
+                           d_word_off, d_nwords, x->tokens, d_out, out_stride);
+    }
+    BOA_HIP_TRY(hipGetLastError());
+    BOA_HIP_TRY(hipStreamSynchronize(s));
+    return BOA_OK;
+}

@@ -1,0 +1,588 @@
+// Range-coder kernels of libboa_hip.so: the coder on precomputed tables (range coder alone), the per-step
+// batch coder with the reference's Q2 quantiser (drop-in for gpu.queue.RangeCoderBatch), bitstream
+// compaction, and the fused quantiser's table export used by the parity tests.
+//
+// One chunk lane per stream throughout.  Wave-parallel work (table search, Q2 prefix sums, quantiser
+// scans) is done by one 64-wide wavefront per lane; the coder state itself is uniform across the wave.
+#include "boa_common.h"
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+#include <string>
+#include <vector>
+
+#include "../../include/boa_hip.h"
+
+using namespace boa;
+
+// ================================================================================================
+// Coder on precomputed tables.  Table row = cdf[0..K-1] of one step (cdf[K] = 2^P implied).
+
+template <int P, typename TC>
+__global__ void __launch_bounds__(256) k_rc_encode_tables(const TC* __restrict__ cdf, int K,
+                                                         const uint8_t* __restrict__ syms, int streams,
+                                                         int len, uint32_t* __restrict__ words,
+                                                         int64_t pitch, int32_t* __restrict__ nwords) {
+    const int n = blockIdx.x * blockDim.x + threadIdx.x;
+    if (n >= streams) return;
+    EncState st;
+    enc_init(st);
+    const WordSink sink{words + (int64_t)n * pitch, pitch, true};
+    const TC* c = cdf + (int64_t)n * len * K;
+    const uint8_t* s = syms + (int64_t)n * len;
+    for (int t = 0; t < len; ++t) {
+        const int sym = s[t];
+        if (sym >= K) continue;  // gpu_range_coder.py:97: symbols outside [0, K) are skipped
+        const uint32_t lo = (uint32_t)c[(int64_t)t * K + sym];
+        const uint32_t hi = (sym + 1 < K) ? (uint32_t)c[(int64_t)t * K + sym + 1] : (1u << P);
+        enc_push(st, P, lo, hi - lo, sink);
+    }
+    enc_finish(st, sink);
+    nwords[n] = st.nwords;  // > pitch signals overflow (nothing past the pitch was written)
+}
+
+template <int P, typename TC>
+__global__ void __launch_bounds__(64) k_rc_decode_tables(const TC* __restrict__ cdf, int K,
+                                                        const uint32_t* __restrict__ words, int64_t pitch,
+                                                        const int32_t* __restrict__ nwords, int streams,
+                                                        int len, uint8_t* __restrict__ syms) {
+    const int n = blockIdx.x;
+    const int lane = threadIdx.x;
+    if (n >= streams) return;
+    const uint32_t* in = words + (int64_t)n * pitch;
+    int32_t nw = nwords[n];
+    if (nw > pitch) nw = (int32_t)pitch;
+    DecState st;
+    dec_init(st, in, nw);
+    const TC* c = cdf + (int64_t)n * len * K;
+    uint32_t cur[4], nxt[4];
+    if (len > 0) load_row4<P>(c, K, lane, cur);
+    for (int t = 0; t < len; ++t) {
+        if (t + 1 < len) load_row4<P>(c + (int64_t)(t + 1) * K, K, lane, nxt);
+        const uint32_t q = dec_target(st, P);
+        uint32_t lo, hi;
+        const int s = wave_find_symbol<P>(cur, K, q, lane, lo, hi);
+        if (lane == 0) syms[(int64_t)n * len + t] = (uint8_t)s;
+        dec_advance(st, P, lo, hi - lo, in, nw);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) cur[j] = nxt[j];
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Synthetic tables: counter-based generator (SplitMix64 finaliser, Steele/Lea/Flood 2014) keyed by
+// (seed, stream, step, index), Box-Muller normals, fused quantiser, inverse-CDF symbol draw.
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+template <int P, typename TC>
+__global__ void __launch_bounds__(256) k_rc_synth_tables(uint64_t seed, float sigma, int K, int streams,
+                                                        int len, TC* __restrict__ cdf,
+                                                        uint8_t* __restrict__ syms) {
+    const int lane = threadIdx.x & 63;
+    const int64_t rows = (int64_t)streams * len;
+    const int64_t wave0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+    for (int64_t r = wave0; r < rows; r += nwaves) {
+        const uint64_t key = mix64(seed ^ mix64((uint64_t)r));
+        float l[4];
+#pragma unroll
+        for (int j = 0; j < 4; j += 2) {
+            const uint64_t h = mix64(key + (uint64_t)(4 * lane + j));
+            const float u1 = ((float)(uint32_t)(h >> 40) + 1.0f) * 0x1p-24f;      // (0, 1]
+            const float u2 = (float)(uint32_t)(h & 0xFFFFFFu) * 0x1p-24f;         // [0, 1)
+            const float rad = sqrtf(-2.0f * logf(u1));
+            l[j] = sigma * rad * cosf(6.28318530718f * u2);
+            l[j + 1] = sigma * rad * sinf(6.28318530718f * u2);
+        }
+        XQ q;
+        xq_build(q, make_float4(l[0], l[1], l[2], l[3]), lane, K, P);
+        uint32_t e[4];
+        uint32_t c = q.base;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int k = 4 * lane + j;
+            e[j] = (k < K) ? xq_cdf_at(q, c, k) : (1u << P);
+            c += q.f[j];
+        }
+        TC* row = cdf + r * K;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int k = 4 * lane + j;
+            if (k < K) row[k] = (TC)e[j];
+        }
+        const uint32_t u = (uint32_t)(mix64(key ^ 0x5851F42D4C957F2Dull) >> 20) & ((1u << P) - 1u);
+        uint32_t lo, hi;
+        const int s = wave_find_symbol<P>(e, K, u, lane, lo, hi);
+        if (lane == 0) syms[r] = (uint8_t)s;
+    }
+}
+
+// ================================================================================================
+// Per-step batch coder, Q2 quantiser (gpu_range_coder.py:57-79) at PRECISION 24.
+
+static constexpr int RCB_P = 24;
+static constexpr int RCB_KMAX = 1024;  // the reference's per-thread table holds K+1 <= 1025 entries
+
+__global__ void k_rcb_init(EncState* st, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) enc_init(st[i]);
+}
+
+// gpu_range_coder.py:88-141, one wavefront per lane: the probabilities are staged through LDS with
+// coalesced loads, then lane 0 runs the sequential double accumulation of build_cdf_fast (the same
+// additions in the same order, so the prefix values equal the reference's cumulative_float).
+__global__ void __launch_bounds__(64) k_rcb_encode_step(const int32_t* __restrict__ syms,
+                                                       const float* __restrict__ probs,
+                                                       const uint8_t* __restrict__ mask, int n, int K,
+                                                       EncState* __restrict__ states,
+                                                       uint32_t* __restrict__ words, int64_t pitch) {
+    __shared__ float sp[RCB_KMAX];
+    const int b = blockIdx.x;
+    const int lane = threadIdx.x;
+    if (b >= n) return;
+    if (mask && mask[b] == 0) return;
+    const int s = syms[b];
+    if (s < 0 || s >= K) return;
+    const float* row = probs + (int64_t)b * K;
+    for (int i = lane; i < K; i += 64) sp[i] = row[i];
+    __syncthreads();
+    if (lane != 0) return;
+    const uint32_t TOTAL = 1u << RCB_P;
+    const uint32_t free_weight = TOTAL - (uint32_t)K;
+    double norm = 0.0, cum_s = 0.0, cum_s1 = 0.0;
+    for (int i = 0; i < K; ++i) {
+        if (i == s) cum_s = norm;
+        if (i == s + 1) cum_s1 = norm;
+        norm += (double)sp[i];
+    }
+    uint32_t lo, hi;
+    if (!(norm > 0.0) || !__builtin_isfinite(norm)) {
+        const uint32_t step = free_weight / (uint32_t)K + 1u;
+        lo = (uint32_t)s * step;
+        hi = (s + 1 < K) ? (uint32_t)(s + 1) * step : TOTAL;
+    } else {
+        const double scale = (double)free_weight / norm;
+        lo = (uint32_t)(cum_s * scale) + (uint32_t)s;
+        hi = (s + 1 < K) ? (uint32_t)(cum_s1 * scale) + (uint32_t)(s + 1) : TOTAL;
+    }
+    EncState st = states[b];
+    const WordSink sink{words + (int64_t)b * pitch, pitch, true};
+    enc_push(st, RCB_P, lo, hi - lo, sink);
+    states[b] = st;
+}
+
+__global__ void k_rcb_finalize(EncState* states, uint32_t* words, int64_t pitch, int32_t* sizes, int n) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= n) return;
+    EncState st = states[b];
+    const WordSink sink{words + (int64_t)b * pitch, pitch, true};
+    enc_finish(st, sink);
+    states[b] = st;
+    sizes[b] = st.overflow ? -st.nwords : st.nwords;  // negative: the stream needed more than the pitch
+}
+
+__global__ void k_rcb_init_dec(DecState* states, const uint32_t* words, int64_t pitch,
+                               const int32_t* sizes, int n) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= n) return;
+    DecState st;
+    dec_init(st, words + (int64_t)b * pitch, sizes[b]);
+    states[b] = st;
+}
+
+// gpu_range_coder.py:182-210.  Lane 0 writes the sequential Q2 prefix sums to LDS; the wave then
+// evaluates every cdf entry in parallel and finds the reference's linear-search answer with ballots.
+__global__ void __launch_bounds__(64) k_rcb_decode_step(const float* __restrict__ probs,
+                                                       const uint8_t* __restrict__ mask, int n, int K,
+                                                       DecState* __restrict__ states,
+                                                       const uint32_t* __restrict__ words, int64_t pitch,
+                                                       const int32_t* __restrict__ sizes,
+                                                       int32_t* __restrict__ out_syms) {
+    __shared__ float sp[RCB_KMAX];
+    __shared__ double scum[RCB_KMAX + 1];
+    __shared__ double s_scale;
+    __shared__ int s_uniform;
+    const int b = blockIdx.x;
+    const int lane = threadIdx.x;
+    if (b >= n) return;
+    if (mask && mask[b] == 0) return;
+    const float* row = probs + (int64_t)b * K;
+    for (int i = lane; i < K; i += 64) sp[i] = row[i];
+    __syncthreads();
+    const uint32_t TOTAL = 1u << RCB_P;
+    const uint32_t free_weight = TOTAL - (uint32_t)K;
+    if (lane == 0) {
+        double norm = 0.0;
+        for (int i = 0; i < K; ++i) {
+            scum[i] = norm;
+            norm += (double)sp[i];
+        }
+        scum[K] = norm;
+        const int uni = (!(norm > 0.0) || !__builtin_isfinite(norm)) ? 1 : 0;
+        s_uniform = uni;
+        s_scale = uni ? 0.0 : (double)free_weight / norm;
+    }
+    __syncthreads();
+    const uint32_t* in = words + (int64_t)b * pitch;
+    const int32_t nw = sizes[b];
+    DecState st = states[b];
+    const uint32_t q = dec_target(st, RCB_P);
+    const bool uni = s_uniform != 0;
+    const double scale = s_scale;
+    const uint32_t ustep = free_weight / (uint32_t)K + 1u;
+    auto cdf_at = [&](int i) -> uint32_t {
+        if (i >= K) return TOTAL;
+        if (uni) return (uint32_t)i * ustep;
+        return (uint32_t)(scum[i] * scale) + (uint32_t)i;
+    };
+    // smallest i in [1, K] with cdf[i] > q
+    int first = K;
+    for (int base = 0; base < K; base += 64) {
+        const int i = base + lane;
+        const bool pred = (i >= 1) && (i < K) && (cdf_at(i) > q);
+        const uint64_t m = __ballot(pred);
+        if (m) { first = base + __builtin_ctzll(m); break; }
+    }
+    int s = first - 1;
+    if (s < 0) s = 0;
+    if (s >= K) s = K - 1;
+    const uint32_t lo = cdf_at(s), hi = cdf_at(s + 1);
+    dec_advance(st, RCB_P, lo, hi - lo, in, nw);
+    if (lane == 0) {
+        out_syms[b] = s;
+        states[b] = st;
+    }
+}
+
+// ================================================================================================
+// Compaction: exclusive scan of stream sizes (one workgroup) + gather into a contiguous payload.
+
+__global__ void __launch_bounds__(1024) k_scan_sizes(const int32_t* __restrict__ nwords, int n,
+                                                    int64_t* __restrict__ off, int64_t* __restrict__ total) {
+    __shared__ int64_t part[1024];
+    const int tid = threadIdx.x;
+    const int per = (n + 1023) / 1024;
+    const int lo = tid * per;
+    const int hi = min(n, lo + per);
+    int64_t s = 0;
+    for (int i = lo; i < hi; ++i) s += (int64_t)max(nwords[i], 0);
+    part[tid] = s;
+    __syncthreads();
+    for (int o = 1; o < 1024; o <<= 1) {  // Hillis-Steele inclusive scan over the 1024 partials
+        const int64_t v = (tid >= o) ? part[tid - o] : 0;
+        __syncthreads();
+        part[tid] += v;
+        __syncthreads();
+    }
+    int64_t run = part[tid] - s;
+    for (int i = lo; i < hi; ++i) {
+        off[i] = run;
+        run += (int64_t)max(nwords[i], 0);
+    }
+    if (tid == 1023) *total = part[1023];
+}
+
+__global__ void __launch_bounds__(256) k_gather_words(const uint32_t* __restrict__ words, int64_t pitch,
+                                                     const int32_t* __restrict__ nwords,
+                                                     const int64_t* __restrict__ off,
+                                                     uint32_t* __restrict__ payload) {
+    const int b = blockIdx.x;
+    const int32_t nw = max(nwords[b], 0);
+    const uint32_t* src = words + (int64_t)b * pitch;
+    uint32_t* dst = payload + off[b];
+    for (int i = threadIdx.x; i < nw; i += blockDim.x) dst[i] = src[i];
+}
+
+// Fused-quantiser tables for parity tests: one wavefront per row.
+__global__ void __launch_bounds__(256) k_xq_cdf(const float* __restrict__ logits, int64_t rows, int V, int P,
+                                               uint32_t* __restrict__ cdf) {
+    const int lane = threadIdx.x & 63;
+    const int64_t r = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    if (r >= rows) return;
+    const float* row = logits + r * V;
+    float l[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) l[j] = (4 * lane + j < V) ? row[4 * lane + j] : 0.0f;
+    XQ q;
+    xq_build(q, make_float4(l[0], l[1], l[2], l[3]), lane, V, P);
+    uint32_t c = q.base;
+    uint32_t* out = cdf + r * (V + 1);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int k = 4 * lane + j;
+        if (k < V) out[k] = xq_cdf_at(q, c, k);
+        c += q.f[j];
+    }
+    if (lane == 0) out[V] = 1u << P;
+}
+
+// ================================================================================================
+// Host side
+
+static hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+extern "C" int rc_encode_tables(int32_t precision, int32_t cdf_bytes, const void* d_cdf, int32_t K,
+                                const uint8_t* d_syms, int32_t streams, int32_t len, uint32_t* d_words,
+                                int64_t pitch_words, int32_t* d_nwords, void* stream) {
+    if (!d_cdf || !d_syms || !d_words || !d_nwords || streams < 0 || len < 0 || K < 2 || K > 256 ||
+        pitch_words < 1)
+        return boa_fail(BOA_ERR_ARG, "rc_encode_tables: bad arguments");
+    if (streams == 0) return BOA_OK;
+    const dim3 grid((streams + 255) / 256), block(256);
+    hipStream_t s = as_stream(stream);
+    if (precision == 16 && cdf_bytes == 2)
+        hipLaunchKernelGGL((k_rc_encode_tables<16, uint16_t>), grid, block, 0, s, (const uint16_t*)d_cdf, K,
+                           d_syms, streams, len, d_words, pitch_words, d_nwords);
+    else if (precision == 16 && cdf_bytes == 4)
+        hipLaunchKernelGGL((k_rc_encode_tables<16, uint32_t>), grid, block, 0, s, (const uint32_t*)d_cdf, K,
+                           d_syms, streams, len, d_words, pitch_words, d_nwords);
+    else if (precision == 24 && cdf_bytes == 4)
+        hipLaunchKernelGGL((k_rc_encode_tables<24, uint32_t>), grid, block, 0, s, (const uint32_t*)d_cdf, K,
+                           d_syms, streams, len, d_words, pitch_words, d_nwords);
+    else
+        return boa_fail(BOA_ERR_ARG, "rc_encode_tables: precision %d with %d-byte tables unsupported",
+                        precision, cdf_bytes);
+    BOA_HIP_TRY(hipGetLastError());
+    return BOA_OK;
+}
+
+extern "C" int rc_decode_tables(int32_t precision, int32_t cdf_bytes, const void* d_cdf, int32_t K,
+                                const uint32_t* d_words, int64_t pitch_words, const int32_t* d_nwords,
+                                int32_t streams, int32_t len, uint8_t* d_syms, void* stream) {
+    if (!d_cdf || !d_syms || !d_words || !d_nwords || streams < 0 || len < 0 || K < 2 || K > 256 ||
+        pitch_words < 1)
+        return boa_fail(BOA_ERR_ARG, "rc_decode_tables: bad arguments");
+    if (streams == 0) return BOA_OK;
+    const dim3 grid(streams), block(64);
+    hipStream_t s = as_stream(stream);
+    if (precision == 16 && cdf_bytes == 2)
+        hipLaunchKernelGGL((k_rc_decode_tables<16, uint16_t>), grid, block, 0, s, (const uint16_t*)d_cdf, K,
+                           d_words, pitch_words, d_nwords, streams, len, d_syms);
+    else if (precision == 16 && cdf_bytes == 4)
+        hipLaunchKernelGGL((k_rc_decode_tables<16, uint32_t>), grid, block, 0, s, (const uint32_t*)d_cdf, K,
+                           d_words, pitch_words, d_nwords, streams, len, d_syms);
+    else if (precision == 24 && cdf_bytes == 4)
+        hipLaunchKernelGGL((k_rc_decode_tables<24, uint32_t>), grid, block, 0, s, (const uint32_t*)d_cdf, K,
+                           d_words, pitch_words, d_nwords, streams, len, d_syms);
+    else
+        return boa_fail(BOA_ERR_ARG, "rc_decode_tables: precision %d with %d-byte tables unsupported",
+                        precision, cdf_bytes);
+    BOA_HIP_TRY(hipGetLastError());
+    return BOA_OK;
+}
+
+extern "C" int rc_synth_tables(uint64_t seed, float sigma, int32_t precision, int32_t cdf_bytes, int32_t K,
+                               int32_t streams, int32_t len, void* d_cdf, uint8_t* d_syms, void* stream) {
+    if (!d_cdf || !d_syms || streams < 0 || len < 0 || K < 2 || K > 256)
+        return boa_fail(BOA_ERR_ARG, "rc_synth_tables: bad arguments");
+    const int64_t rows = (int64_t)streams * len;
+    if (rows == 0) return BOA_OK;
+    const int64_t waves = rows < (int64_t)65536 * 4 ? rows : (int64_t)65536 * 4;
+    const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+    hipStream_t s = as_stream(stream);
+    if (precision == 16 && cdf_bytes == 2)
+        hipLaunchKernelGGL((k_rc_synth_tables<16, uint16_t>), grid, block, 0, s, seed, sigma, K, streams, len,
+                           (uint16_t*)d_cdf, d_syms);
+    else if (precision == 16 && cdf_bytes == 4)
+        hipLaunchKernelGGL((k_rc_synth_tables<16, uint32_t>), grid, block, 0, s, seed, sigma, K, streams, len,
+                           (uint32_t*)d_cdf, d_syms);
+    else if (precision == 24 && cdf_bytes == 4)
+        hipLaunchKernelGGL((k_rc_synth_tables<24, uint32_t>), grid, block, 0, s, seed, sigma, K, streams, len,
+                           (uint32_t*)d_cdf, d_syms);
+    else
+        return boa_fail(BOA_ERR_ARG, "rc_synth_tables: precision %d with %d-byte tables unsupported",
+                        precision, cdf_bytes);
+    BOA_HIP_TRY(hipGetLastError());
+    return BOA_OK;
+}
+
+extern "C" int boa_xq_cdf(const float* d_logits, int64_t rows, int32_t vocab, int32_t precision,
+                          uint32_t* d_cdf, void* stream) {
+    if (!d_logits || !d_cdf || rows < 0 || vocab < 2 || vocab > 256 || precision < 16 || precision > 24)
+        return boa_fail(BOA_ERR_ARG, "boa_xq_cdf: bad arguments");
+    if (rows == 0) return BOA_OK;
+    const int64_t blocks = (rows + 3) / 4;
+    hipLaunchKernelGGL(k_xq_cdf, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), d_logits, rows, vocab,
+                       precision, d_cdf);
+    BOA_HIP_TRY(hipGetLastError());
+    return BOA_OK;
+}
+
+extern "C" int boa_compact(const uint32_t* d_words, int64_t pitch_words, const int32_t* d_nwords, int32_t lanes,
+                           int64_t* d_word_off, uint32_t* d_payload, int64_t payload_cap, int64_t* h_total_words,
+                           void* stream) {
+    if (!d_words || !d_nwords || !d_word_off || lanes < 0 || !h_total_words)
+        return boa_fail(BOA_ERR_ARG, "boa_compact: bad arguments");
+    *h_total_words = 0;
+    if (lanes == 0) return BOA_OK;
+    hipStream_t s = as_stream(stream);
+    int64_t* d_total = nullptr;
+    BOA_HIP_TRY(hipMalloc((void**)&d_total, sizeof(int64_t)));
+    hipLaunchKernelGGL(k_scan_sizes, dim3(1), dim3(1024), 0, s, d_nwords, lanes, d_word_off, d_total);
+    hipError_t e = hipGetLastError();
+    int64_t total = 0;
+    if (e == hipSuccess) e = hipMemcpyAsync(&total, d_total, sizeof(int64_t), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    (void)hipFree(d_total);
+    if (e != hipSuccess) return boa_fail_hip(e, "boa_compact scan", __FILE__, __LINE__);
+    *h_total_words = total;
+    if (total > payload_cap) return boa_fail(BOA_ERR_OVERFLOW, "boa_compact: payload needs %lld words, capacity %lld",
+                                             (long long)total, (long long)payload_cap);
+    if (total > 0) {
+        if (!d_payload) return boa_fail(BOA_ERR_ARG, "boa_compact: null payload");
+        hipLaunchKernelGGL(k_gather_words, dim3(lanes), dim3(256), 0, s, d_words, pitch_words, d_nwords, d_word_off,
+                           d_payload);
+        BOA_HIP_TRY(hipGetLastError());
+    }
+    BOA_HIP_TRY(hipStreamSynchronize(s));
+    return BOA_OK;
+}
+
+// ------------------------------------------------------------------------------------------------
+// RangeCoderBatch holder (gpu_range_coder.py:212-306): owns states, the pitched word buffer and sizes.
+struct rcb {
+    int32_t n = 0, k = 0;
+    int64_t pitch = 0;
+    hipStream_t stream = nullptr;
+    EncState* enc = nullptr;
+    DecState* dec = nullptr;
+    uint32_t* words = nullptr;
+    int32_t* sizes = nullptr;
+    int64_t* off = nullptr;
+    uint32_t* payload = nullptr;
+    bool finalized = false;
+    bool dec_ready = false;
+};
+
+extern "C" int rcb_destroy(rcb* b) {
+    if (!b) return BOA_OK;
+    if (b->stream) (void)hipStreamSynchronize(b->stream);
+    else (void)hipDeviceSynchronize();
+    void* ptrs[] = {b->enc, b->dec, b->words, b->sizes, b->off, b->payload};
+    for (void* p : ptrs)
+        if (p) (void)hipFree(p);
+    delete b;
+    return BOA_OK;
+}
+
+extern "C" int rcb_create(int32_t n, int32_t k, int64_t pitch_words, void* stream, rcb** out) {
+    if (!out || n < 1 || k < 1 || k > RCB_KMAX || pitch_words < 1)
+        return boa_fail(BOA_ERR_ARG, "rcb_create: need N >= 1, 1 <= K <= %d, pitch >= 1 (got %d, %d, %lld)",
+                        RCB_KMAX, n, k, (long long)pitch_words);
+    *out = nullptr;
+    rcb* b = new rcb();
+    b->n = n;
+    b->k = k;
+    b->pitch = pitch_words;
+    b->stream = as_stream(stream);
+    hipError_t e = hipSuccess;
+    if (e == hipSuccess) e = hipMalloc((void**)&b->enc, sizeof(EncState) * n);
+    if (e == hipSuccess) e = hipMalloc((void**)&b->dec, sizeof(DecState) * n);
+    if (e == hipSuccess) e = hipMalloc((void**)&b->words, sizeof(uint32_t) * (size_t)n * (size_t)pitch_words);
+    if (e == hipSuccess) e = hipMalloc((void**)&b->sizes, sizeof(int32_t) * n);
+    if (e == hipSuccess) e = hipMalloc((void**)&b->off, sizeof(int64_t) * n);
+    if (e == hipSuccess) e = hipMemsetAsync(b->sizes, 0, sizeof(int32_t) * n, b->stream);
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(k_rcb_init, dim3((n + 255) / 256), dim3(256), 0, b->stream, b->enc, n);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(b->stream);
+    if (e != hipSuccess) {
+        rcb_destroy(b);
+        return boa_fail_hip(e, "rcb_create", __FILE__, __LINE__);
+    }
+    *out = b;
+    return BOA_OK;
+}
+
+extern "C" int rcb_encode_step(rcb* b, const int32_t* d_syms, const float* d_probs, const uint8_t* d_mask) {
+    if (!b || !d_syms || !d_probs) return boa_fail(BOA_ERR_ARG, "rcb_encode_step: null argument");
+    if (b->finalized) return boa_fail(BOA_ERR_STATE, "rcb_encode_step: batch already finalized");
+    hipLaunchKernelGGL(k_rcb_encode_step, dim3(b->n), dim3(64), 0, b->stream, d_syms, d_probs, d_mask, b->n, b->k,
+                       b->enc, b->words, b->pitch);
+    BOA_HIP_TRY(hipGetLastError());
+    return BOA_OK;
+}
+
+extern "C" int rcb_finalize(rcb* b) {
+    if (!b) return boa_fail(BOA_ERR_ARG, "rcb_finalize: null batch");
+    hipLaunchKernelGGL(k_rcb_finalize, dim3((b->n + 255) / 256), dim3(256), 0, b->stream, b->enc, b->words, b->pitch,
+                       b->sizes, b->n);
+    BOA_HIP_TRY(hipGetLastError());
+    b->finalized = true;
+    std::vector<int32_t> h(b->n);
+    BOA_HIP_TRY(hipMemcpyAsync(h.data(), b->sizes, sizeof(int32_t) * b->n, hipMemcpyDeviceToHost, b->stream));
+    BOA_HIP_TRY(hipStreamSynchronize(b->stream));
+    for (int i = 0; i < b->n; ++i)
+        if (h[i] < 0)
+            return boa_fail(BOA_ERR_OVERFLOW, "Compressed stream %d needs %d words, exceeds pitch %lld; increase pitch",
+                            i, -h[i], (long long)b->pitch);
+    return BOA_OK;
+}
+
+extern "C" int rcb_get_sizes(rcb* b, int32_t* h_sizes) {
+    if (!b || !h_sizes) return boa_fail(BOA_ERR_ARG, "rcb_get_sizes: null argument");
+    BOA_HIP_TRY(hipMemcpyAsync(h_sizes, b->sizes, sizeof(int32_t) * b->n, hipMemcpyDeviceToHost, b->stream));
+    BOA_HIP_TRY(hipStreamSynchronize(b->stream));
+    return BOA_OK;
+}
+
+extern "C" int rcb_get_words(rcb* b, uint32_t* h_words, int64_t cap_words, int64_t* h_total) {
+    if (!b || !h_total) return boa_fail(BOA_ERR_ARG, "rcb_get_words: null argument");
+    int64_t total = 0;
+    // the compacted payload is at most n * pitch words; gather into a scratch buffer owned by the batch
+    if (!b->payload) BOA_HIP_TRY(hipMalloc((void**)&b->payload, sizeof(uint32_t) * (size_t)b->n * (size_t)b->pitch));
+    int rc = boa_compact(b->words, b->pitch, b->sizes, b->n, b->off, b->payload, (int64_t)b->n * b->pitch, &total,
+                         b->stream);
+    if (rc != BOA_OK) return rc;
+    *h_total = total;
+    if (total > cap_words) return boa_fail(BOA_ERR_OVERFLOW, "rcb_get_words: host buffer too small");
+    if (total > 0) {
+        if (!h_words) return boa_fail(BOA_ERR_ARG, "rcb_get_words: null host buffer");
+        BOA_HIP_TRY(hipMemcpyAsync(h_words, b->payload, sizeof(uint32_t) * total, hipMemcpyDeviceToHost, b->stream));
+    }
+    BOA_HIP_TRY(hipStreamSynchronize(b->stream));
+    return BOA_OK;
+}
+
+extern "C" int rcb_load(rcb* b, const uint32_t* h_words, const int32_t* h_sizes) {
+    if (!b || !h_sizes) return boa_fail(BOA_ERR_ARG, "rcb_load: null argument");
+    std::vector<uint32_t> buf((size_t)b->n * (size_t)b->pitch, 0u);
+    int64_t pos = 0;
+    for (int i = 0; i < b->n; ++i) {
+        const int32_t nw = h_sizes[i];
+        if (nw < 0) return boa_fail(BOA_ERR_ARG, "rcb_load: negative size for stream %d", i);
+        if (nw > b->pitch) return boa_fail(BOA_ERR_OVERFLOW, "Compressed stream exceeds pitch; increase pitch");
+        if (nw > 0) memcpy(buf.data() + (size_t)i * (size_t)b->pitch, h_words + pos, sizeof(uint32_t) * nw);
+        pos += nw;
+    }
+    BOA_HIP_TRY(hipMemcpyAsync(b->words, buf.data(), sizeof(uint32_t) * buf.size(), hipMemcpyHostToDevice, b->stream));
+    BOA_HIP_TRY(hipMemcpyAsync(b->sizes, h_sizes, sizeof(int32_t) * b->n, hipMemcpyHostToDevice, b->stream));
+    BOA_HIP_TRY(hipStreamSynchronize(b->stream));
+    b->dec_ready = false;
+    return BOA_OK;
+}
+
+extern "C" int rcb_init_decoder(rcb* b) {
+    if (!b) return boa_fail(BOA_ERR_ARG, "rcb_init_decoder: null batch");
+    hipLaunchKernelGGL(k_rcb_init_dec, dim3((b->n + 255) / 256), dim3(256), 0, b->stream, b->dec, b->words, b->pitch,
+                       b->sizes, b->n);
+    BOA_HIP_TRY(hipGetLastError());
+    b->dec_ready = true;
+    return BOA_OK;
+}
+
+extern "C" int rcb_decode_step(rcb* b, const float* d_probs, int32_t* d_out_syms, const uint8_t* d_mask) {
+    if (!b || !d_probs || !d_out_syms) return boa_fail(BOA_ERR_ARG, "rcb_decode_step: null argument");
+    if (!b->dec_ready) return boa_fail(BOA_ERR_STATE, "rcb_decode_step: call init_decoder first");
+    hipLaunchKernelGGL(k_rcb_decode_step, dim3(b->n), dim3(64), 0, b->stream, d_probs, d_mask, b->n, b->k, b->dec,
+                       b->words, b->pitch, b->sizes, d_out_syms);
+    BOA_HIP_TRY(hipGetLastError());
+    return BOA_OK;
+}

@@ -1,0 +1,104 @@
+"""Fused compress/decompress on the GPU: byte-exact round trips, ragged and edge-case chunks, BOA2 files,
+and compressed size within 0.5% of the oracle pipeline (CPU fp32 model -> softmax -> Q2 -> coder)."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import model_ref, weights_ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _model(n_layers=2, seed=0):
+    from boa_amd import weights as W
+
+    import model as M
+
+    blob = W.seeded_blob(W.Cfg(n_layers=n_layers), seed)
+    return M.BoaConstrictor(256, n_layers, 256).load_blob(blob), blob
+
+
+def _markov(n, seed=0, alpha=0.1):
+    rng = np.random.default_rng(seed)
+    P = rng.dirichlet([alpha] * 256, size=256)
+    C = np.cumsum(P, axis=1)
+    out = np.empty(n, dtype=np.uint8)
+    x = 0
+    u = rng.random(n)
+    for i in range(n):
+        out[i] = x
+        x = min(int(np.searchsorted(C[x], u[i], side="right")), 255)
+    return out
+
+
+def test_round_trip_ragged(gpu):
+    import codec
+
+    m, _ = _model(2)
+    rng = np.random.default_rng(1)
+    lens = [1, 2, 3, 64, 65, 129, 200, 1, 77]
+    chunks = [rng.integers(0, 256, L).astype(np.uint8) for L in lens]
+    payload, nw, fb, Ls = codec.compress_payload(m, chunks)
+    assert Ls == lens and fb == [int(c[0]) for c in chunks]
+    assert nw[0] == 0 and nw[7] == 0  # length-1 chunks code nothing
+    out = codec.decompress_payload(m, payload, nw, lens, fb)
+    for i, c in enumerate(chunks):
+        assert (out[i, :lens[i]] == c).all(), i
+
+
+def test_round_trip_api_8_layers(gpu):
+    import codec
+
+    m, _ = _model(8)
+    data = _markov(40 * 300, seed=2)
+    x_list = [torch.from_numpy(data[i * 300:(i + 1) * 300]).unsqueeze(0) for i in range(40)]
+    comp, fb, Ls = codec.compress_GPU(m, x_list)
+    assert all(c.dtype == np.uint32 for c in comp)
+    dec = codec.decompress_GPU(m, comp, Ls, fb)
+    assert all(d.shape == (1, L) for d, L in zip(dec, Ls))
+    assert np.array_equal(np.concatenate([d.reshape(-1) for d in dec]), data)
+
+
+def test_compressed_size_vs_oracle_pipeline(gpu, ora):
+    """Sizes within 0.5% of the reference protocol run on the CPU oracle (Q2 on torch softmax probs)."""
+    import codec
+
+    n_layers, B, L = 2, 32, 1500
+    m, blob = _model(n_layers, seed=4)
+    data = _markov(B * L, seed=3)
+    chunks = [data[i * L:(i + 1) * L] for i in range(B)]
+    payload, nw, fb, Ls = codec.compress_payload(m, chunks)
+    ref = model_ref.RefModel(blob, weights_ref.Cfg(n_layers=n_layers))
+    X = torch.from_numpy(np.stack(chunks).astype(np.int64))
+    logits = ref.forward(X[:, :-1])                       # [B, L-1, V]
+    probs = torch.softmax(logits, dim=-1).to(torch.float32).numpy()
+    ref_words = sum(len(ora.encode_probs_q2(24, probs[b], X[b, 1:].numpy().astype(np.int32))) for b in range(B))
+    gpu_words = int(nw.sum())
+    print(f"gpu words {gpu_words}  oracle words {ref_words}", flush=True)
+    assert abs(gpu_words - ref_words) <= 0.005 * ref_words
+    out = codec.decompress_payload(m, payload, nw, Ls, fb)
+    assert np.array_equal(out.reshape(-1), data)
+
+
+def test_boa_file_round_trip(gpu, tmp_path):
+    import boa
+
+    m, _ = _model(2)
+    data = _markov(5000, seed=5).tobytes()
+    src = tmp_path / "in.bin"
+    src.write_bytes(data)
+    f = boa.BOA("cuda", str(tmp_path / "x.boa"), m)
+    f.compress(str(src), chunks_count=7, progress=False)
+    meta = f.get_metadata()
+    assert meta == {"chunk_len": 715, "n_chunks": 7, "uncompressed_len": 5000, "last_chunk_len": 710}
+    g = boa.BOA("cuda", str(tmp_path / "x.boa"), m)
+    assert g.decompress(progress=False) == data
+    # seq_size chunking, and a wave size smaller than the chunk count
+    os.environ["BOA_GPU_STREAMS"] = "3"
+    try:
+        f.compress(str(src), seq_size=1024, progress=False)
+        assert boa.BOA("cuda", str(tmp_path / "x.boa"), m).decompress(progress=False) == data
+    finally:
+        del os.environ["BOA_GPU_STREAMS"]

@@ -1,0 +1,185 @@
+"""GPU range coder vs the oracle: bit-exact words on identical CDF tables, drop-in RangeCoderBatch parity."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import bigint_check
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _sample(cdf, rng, P):
+    # symbol with cdf[s] <= u < cdf[s+1] for a uniform u in [0, 2^P)
+    u = rng.integers(0, 1 << P, cdf.shape[:-1])
+    return (np.sum(cdf[..., 1:] <= u[..., None], axis=-1)).astype(np.int64)
+
+
+def _encode_gpu(lib, P, cb, tables, syms, pitch):
+    from boa_amd import _native as N
+
+    S, T, K = tables.shape
+    d_cdf = _dev(tables)
+    d_syms = _dev(syms.astype(np.uint8))
+    d_words = torch.zeros((S, pitch), dtype=torch.int32, device="cuda")
+    d_n = torch.zeros(S, dtype=torch.int32, device="cuda")
+    N.check(lib.rc_encode_tables(P, cb, N.ptr(d_cdf), K, N.ptr(d_syms), S, T, N.ptr(d_words), pitch, N.ptr(d_n),
+                                 N.stream_ptr()))
+    torch.cuda.synchronize()
+    return d_cdf, d_words, d_n
+
+
+@pytest.mark.parametrize("P,cb,K", [(16, 2, 256), (16, 4, 256), (24, 4, 256), (16, 2, 100), (24, 4, 7)])
+def test_tables_bit_exact(gpu, ora, P, cb, K):
+    from boa_amd import _native as N
+
+    rng = np.random.default_rng(P * 1000 + cb * 100 + K)
+    S, T = 48, 257
+    logits = rng.normal(0, 3, (S, T, K)).astype(np.float32)
+    cdf = ora.xq_cdf(logits, P)
+    syms = _sample(cdf, rng, P)
+    tables = cdf[..., :K].astype(np.uint16 if cb == 2 else np.uint32)
+    pitch = T + 8
+    d_cdf, d_words, d_n = _encode_gpu(gpu, P, cb, tables, syms, pitch)
+    words = d_words.cpu().numpy().view(np.uint32)
+    nw = d_n.cpu().numpy()
+    for s in range(S):
+        ref = ora.encode_tables(P, cdf[s], syms[s])
+        assert nw[s] == len(ref), s
+        assert (words[s, :nw[s]] == ref).all(), s
+    d_out = torch.zeros((S, T), dtype=torch.uint8, device="cuda")
+    N.check(gpu.rc_decode_tables(P, cb, N.ptr(d_cdf), K, N.ptr(d_words), pitch, N.ptr(d_n), S, T, N.ptr(d_out),
+                                 N.stream_ptr()))
+    assert (d_out.cpu().numpy() == syms).all()
+
+
+def test_tables_empty_and_skipped_symbols(gpu, ora):
+    P, K, S, T = 16, 16, 8, 40
+    rng = np.random.default_rng(3)
+    cdf = ora.xq_cdf(rng.normal(0, 2, (S, T, K)).astype(np.float32), P)
+    syms = _sample(cdf, rng, P)
+    syms[0, :] = 255          # every symbol outside [0, K): skipped -> empty stream
+    syms[1, ::3] = 200        # some skipped (gpu_range_coder.py:97)
+    _, d_words, d_n = _encode_gpu(gpu, P, 4, cdf[..., :K].astype(np.uint32), syms, T + 8)
+    nw = d_n.cpu().numpy()
+    words = d_words.cpu().numpy().view(np.uint32)
+    assert nw[0] == 0
+    for s in range(S):
+        keep = syms[s] < K
+        ref = ora.encode_tables(P, cdf[s][keep], syms[s][keep])
+        assert (words[s, :nw[s]] == ref).all()
+
+
+def test_synth_tables_round_trip(gpu, ora):
+    from boa_amd import _native as N
+
+    P, cb, K, S, T = 16, 2, 256, 256, 512
+    d_cdf = torch.empty((S, T, K), dtype=torch.int16, device="cuda")
+    d_syms = torch.empty((S, T), dtype=torch.uint8, device="cuda")
+    N.check(gpu.rc_synth_tables(12345, 3.0, P, cb, K, S, T, N.ptr(d_cdf), N.ptr(d_syms), N.stream_ptr()))
+    pitch = T + 8
+    d_words = torch.zeros((S, pitch), dtype=torch.int32, device="cuda")
+    d_n = torch.zeros(S, dtype=torch.int32, device="cuda")
+    N.check(gpu.rc_encode_tables(P, cb, N.ptr(d_cdf), K, N.ptr(d_syms), S, T, N.ptr(d_words), pitch, N.ptr(d_n),
+                                 N.stream_ptr()))
+    d_out = torch.zeros((S, T), dtype=torch.uint8, device="cuda")
+    N.check(gpu.rc_decode_tables(P, cb, N.ptr(d_cdf), K, N.ptr(d_words), pitch, N.ptr(d_n), S, T, N.ptr(d_out),
+                                 N.stream_ptr()))
+    torch.cuda.synchronize()
+    syms = d_syms.cpu().numpy()
+    assert (d_out.cpu().numpy() == syms).all()
+    tables = d_cdf.cpu().numpy().view(np.uint16).astype(np.uint32)
+    full = np.concatenate([tables, np.full((S, T, 1), 1 << P, np.uint32)], axis=-1)
+    assert (full[..., 0] == 0).all() and (np.diff(full.astype(np.int64), axis=-1) >= 1).all()
+    words = d_words.cpu().numpy().view(np.uint32)
+    nw = d_n.cpu().numpy()
+    for s in range(0, S, 37):
+        ref = ora.encode_tables(P, full[s], syms[s].astype(np.int32))
+        assert (words[s, :nw[s]] == ref).all()
+        steps = [(int(full[s, t, v]), int(full[s, t, v + 1] - full[s, t, v])) for t, v in enumerate(syms[s])]
+        bigint_check.check(ref, steps, P)
+
+
+def _softmax(x):
+    e = np.exp(x - x.max(-1, keepdims=True))
+    return (e / e.sum(-1, keepdims=True)).astype(np.float32)
+
+
+@pytest.mark.parametrize("K", [256, 1000, 3])
+def test_range_coder_batch_matches_q2_oracle(gpu, ora, K):
+    import gpu_range_coder as gr
+
+    rng = np.random.default_rng(K)
+    N, T = 40, 150
+    probs = _softmax(rng.normal(0, 3, (T, N, K)))
+    syms = np.array([[rng.choice(K, p=probs[t, i].astype(np.float64) / probs[t, i].sum()) for i in range(N)]
+                     for t in range(T)], dtype=np.int32)
+    lens = rng.integers(0, T + 1, N)
+    lens[0], lens[1] = 0, T
+    b = gr.gpu.queue.RangeCoderBatch(N, K, T)
+    for t in range(T):
+        b.encode_step(_dev(syms[t]), _dev(probs[t]), mask=_dev(lens > t))
+    b.finalize()
+    comp = b.get_compressed_list()
+    assert b.get_sizes_list() == [len(c) for c in comp]
+    for i in range(N):
+        ref = ora.encode_probs_q2(24, probs[:lens[i], i], syms[:lens[i], i])
+        assert comp[i].dtype == np.uint32 and (comp[i] == ref).all(), i
+    d = gr.gpu.queue.RangeCoderBatch(N, K, T)
+    d.load_compressed_list(comp)
+    d.init_decoder()
+    out = torch.full((N,), -1, dtype=torch.int32, device="cuda")
+    got = np.zeros((T, N), dtype=np.int32)
+    for t in range(T):
+        d.decode_step(_dev(probs[t]), out, mask=_dev(lens > t))
+        got[t] = out.cpu().numpy()
+    for i in range(N):
+        assert (got[:lens[i], i] == syms[:lens[i], i]).all(), i
+
+
+def test_range_coder_batch_errors(gpu):
+    import gpu_range_coder as gr
+
+    N, K = 4, 256
+    b = gr.gpu.queue.RangeCoderBatch(N, K, 4, pitch_bytes=8)  # 2 words per stream
+    rng = np.random.default_rng(0)
+    probs = _softmax(rng.normal(0, 0.1, (N, K)))
+    for _ in range(8):  # ~8 bits per symbol: overflows 2 words
+        b.encode_step(_dev(rng.integers(0, K, N).astype(np.int32)), _dev(probs))
+    with pytest.raises(RuntimeError, match="pitch"):
+        b.finalize()
+    with pytest.raises(RuntimeError, match="length must equal N"):
+        b.load_compressed_list([np.zeros(1, np.uint32)])
+    with pytest.raises(RuntimeError, match="uint32"):
+        b.load_compressed_list([np.zeros(1, np.int64)] * N)
+    with pytest.raises(RuntimeError, match="exceeds pitch"):
+        b.load_compressed_list([np.zeros(5, np.uint32)] * N)
+
+
+def test_compaction(gpu):
+    from boa_amd import _native as N
+
+    rng = np.random.default_rng(9)
+    lanes, pitch = 3000, 64
+    nw = rng.integers(0, pitch + 1, lanes).astype(np.int32)
+    words = rng.integers(0, 1 << 31, (lanes, pitch)).astype(np.int32)
+    d_words, d_nw = _dev(words), _dev(nw)
+    d_off = torch.empty(lanes, dtype=torch.int64, device="cuda")
+    total = int(nw.sum())
+    d_pl = torch.empty(total, dtype=torch.int32, device="cuda")
+    got = ctypes.c_int64(0)
+    N.check(gpu.boa_compact(N.ptr(d_words), pitch, N.ptr(d_nw), lanes, N.ptr(d_off), N.ptr(d_pl), total,
+                            ctypes.byref(got), N.stream_ptr()))
+    assert got.value == total
+    ref = np.concatenate([words[i, :nw[i]] for i in range(lanes)])
+    assert (d_pl.cpu().numpy() == ref).all()
+    assert (d_off.cpu().numpy() == np.concatenate([[0], np.cumsum(nw)[:-1]])).all()
+    small = torch.empty(max(total - 1, 1), dtype=torch.int32, device="cuda")
+    with pytest.raises(N.BoaError):
+        N.check(gpu.boa_compact(N.ptr(d_words), pitch, N.ptr(d_nw), lanes, N.ptr(d_off), N.ptr(small), total - 1,
+                                ctypes.byref(got), N.stream_ptr()))

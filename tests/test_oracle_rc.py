@@ -1,0 +1,151 @@
+"""Pins the oracle's range coder and quantisers (CPU only).
+
+Checks that do not restate the oracle's own code: hand-derived known answers, the independent big-integer
+interval check, closed-form tables, code-length bounds and round trips.
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+from oracle import bigint_check
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def _uniform256():
+    return np.array([[65536 * i for i in range(257)]], dtype=np.uint32)
+
+
+def test_known_answers(ora):
+    spec = json.load(open(os.path.join(HERE, "golden", "rc_known_answers.json")))
+    for case in spec["cases"]:
+        P = case["P"]
+        syms = np.array(case["syms"], dtype=np.int32)
+        if case["cdf"] == "uniform256":
+            cdf = np.repeat(_uniform256(), len(syms), axis=0)
+        elif len(case["cdf"]) == 0:
+            cdf = np.zeros((0, 3), dtype=np.uint32)
+        else:
+            cdf = np.array(case["cdf"], dtype=np.uint32)
+        words = ora.encode_tables(P, cdf, syms)
+        assert [int(w) for w in words] == case["words"], case["name"]
+        if len(syms):
+            assert (ora.decode_tables(P, cdf, words) == syms).all(), case["name"]
+
+
+def test_bigint_detects_mistakes():
+    # the checker must reject a dropped word and flipped bits (a trailing extra word can still decode
+    # correctly, so it is not a violation)
+    steps = [(0, 32768), (32768, 32768)] * 100
+    from oracle import ora
+
+    cdf = np.array([[0, 32768, 65536]] * 200, dtype=np.uint32)
+    syms = np.array([0, 1] * 100, dtype=np.int32)
+    w = ora.encode_tables(16, cdf, syms)
+    bigint_check.check(w, steps, 16)
+    assert len(w) >= 3
+    flip0 = w.copy(); flip0[0] ^= np.uint32(1 << 31)
+    flip1 = w.copy(); flip1[1] ^= np.uint32(1 << 31)
+    for bad in (w[:-1], flip0, flip1):
+        with pytest.raises(AssertionError):
+            bigint_check.check(bad, steps, 16)
+
+
+@pytest.mark.parametrize("P", [16, 24])
+def test_random_streams_bigint(ora, P):
+    rng = np.random.default_rng(P)
+    for trial in range(40):
+        T = int(rng.integers(0, 400))
+        K = int(rng.integers(2, 257))
+        logits = rng.normal(0, 3 if trial % 2 else 12, (T, K)).astype(np.float32)
+        cdf = ora.xq_cdf(logits, P)
+        syms = rng.integers(0, K, T).astype(np.int32)
+        words = ora.encode_tables(P, cdf, syms)
+        steps = [(int(cdf[t, s]), int(cdf[t, s + 1] - cdf[t, s])) for t, s in enumerate(syms)]
+        bigint_check.check(words, steps, P)
+        assert (ora.decode_tables(P, cdf, words) == syms).all()
+        # code length bound: at most information content + 64 bits + rounding loss per symbol
+        bits = -sum(math.log2(f / (1 << P)) for _, f in steps)
+        assert 32 * len(words) <= bits + 64 + 32 + T * 0.01
+
+
+def test_carry_heavy_streams(ora):
+    # tables concentrated near the top of the range force long runs of inverted (carry-pending) words
+    P = 16
+    rng = np.random.default_rng(5)
+    for trial in range(30):
+        T = 300
+        cdf = np.zeros((T, 3), dtype=np.uint32)
+        cdf[:, 1] = rng.integers(65000, 65535, T)
+        cdf[:, 2] = 65536
+        syms = (rng.random(T) < 0.97).astype(np.int32) ^ 1
+        syms = np.where(rng.random(T) < 0.5, 0, 1).astype(np.int32) if trial % 3 == 0 else syms
+        words = ora.encode_tables(P, cdf, syms)
+        steps = [(int(cdf[t, s]), int(cdf[t, s + 1] - cdf[t, s])) for t, s in enumerate(syms)]
+        bigint_check.check(words, steps, P)
+        assert (ora.decode_tables(P, cdf, words) == syms).all()
+
+
+def test_q2_closed_forms(ora):
+    P = 24
+    u = np.full((1, 256), 1 / 256, dtype=np.float32)
+    assert (ora.q2_cdf(u, P) == _uniform256()).all()          # norm = 1 exactly: cdf[i] = i*(2^24-256)/256 + i
+    z = np.zeros((1, 256), dtype=np.float32)                  # degenerate norm: uniform fallback
+    assert (ora.q2_cdf(z, P) == _uniform256()).all()
+    n = np.full((1, 256), np.nan, dtype=np.float32)
+    assert (ora.q2_cdf(n, P) == _uniform256()).all()
+    one = np.zeros((1, 4), dtype=np.float32)
+    one[0, 2] = 1.0                                           # K=4: free = 2^24-4, point mass on symbol 2
+    c = ora.q2_cdf(one, P)[0]
+    assert list(c) == [0, 1, 2, (1 << 24) - 1, 1 << 24]
+
+
+def test_xq_closed_forms(ora):
+    P = 24
+    flat = np.zeros((1, 256), dtype=np.float32)
+    assert (ora.xq_cdf(flat, P) == _uniform256()).all()       # equal logits: f_i = 2^23 for all i
+    peak = np.full((1, 256), -200.0, dtype=np.float32)
+    peak[0, 0] = 0.0                                          # one symbol: f_0 = 2^23, others 0
+    c = ora.xq_cdf(peak, P)[0].astype(np.int64)
+    assert c[0] == 0 and all(c[i] == (1 << 24) - 256 + i for i in range(1, 257))
+    nan = np.full((1, 256), np.nan, dtype=np.float32)
+    assert (ora.xq_cdf(nan, P) == _uniform256()).all()
+
+
+@pytest.mark.parametrize("P", [16, 24])
+def test_table_invariants(ora, P):
+    rng = np.random.default_rng(7)
+    logits = rng.normal(0, 5, (500, 256)).astype(np.float32)
+    for cdf in (ora.xq_cdf(logits, P),
+                ora.q2_cdf(np.exp(logits - logits.max(1, keepdims=True)).astype(np.float32), P)):
+        c = cdf.astype(np.int64)
+        assert (c[:, 0] == 0).all() and (c[:, -1] == 1 << P).all()
+        assert (np.diff(c, axis=1) >= 1).all()
+
+
+def test_expf_accuracy(ora):
+    x = np.concatenate([np.linspace(-87, 0, 200001), np.linspace(0, 88, 1001)]).astype(np.float32)
+    y = ora.expf(x).astype(np.float64)
+    ref = np.exp(x.astype(np.float64))
+    ulp = np.spacing(ref.astype(np.float32)).astype(np.float64)
+    assert (np.abs(y - ref) <= 3 * ulp).all()
+    assert ora.expf(np.array([0.0], np.float32))[0] == 1.0
+    assert ora.expf(np.array([np.nan, -90.0], np.float32)).tolist() == [0.0, 0.0]
+
+
+def test_q2_and_xq_round_trip_from_model_outputs(ora):
+    rng = np.random.default_rng(11)
+    T, K = 300, 256
+    logits = rng.normal(0, 3, (T, K)).astype(np.float32)
+    probs = np.exp(logits - logits.max(1, keepdims=True))
+    probs = (probs / probs.sum(1, keepdims=True)).astype(np.float32)
+    syms = np.array([rng.choice(K, p=p / p.sum()) for p in probs.astype(np.float64)], dtype=np.int32)
+    w2 = ora.encode_probs_q2(24, probs, syms)
+    assert (ora.decode_probs_q2(24, probs, w2) == syms).all()
+    wx = ora.encode_logits_xq(24, logits, syms)
+    assert (ora.decode_logits_xq(24, logits, wx) == syms).all()
+    # both quantisers code within 0.5% of each other on the same distributions
+    assert abs(len(w2) - len(wx)) <= max(2, 0.005 * len(w2))
