@@ -48,6 +48,17 @@ class ModelCfg(ctypes.Structure):
     ]
 
 
+class ProfEntry(ctypes.Structure):
+    _fields_ = [
+        ("name", ctypes.c_char * 32),
+        ("launches", ctypes.c_int64),
+        ("sampled", ctypes.c_int64),
+        ("ms", ctypes.c_double),
+        ("flops", ctypes.c_double),
+        ("bytes", ctypes.c_double),
+    ]
+
+
 # (name, restype, argtypes); every declaration of include/boa_hip.h appears here
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
@@ -65,6 +76,8 @@ SIGNATURES = [
     ("boa_state_reset", ctypes.c_int, [_P, _I32]),
     ("boa_model_step", ctypes.c_int, [_P, _P, _I32, _P]),
     ("boa_model_forward", ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P]),
+    ("boa_profile", ctypes.c_int, [_P, ctypes.c_int]),
+    ("boa_profile_read", ctypes.c_int, [_P, _P, _I32, ctypes.POINTER(_I32)]),
     ("boa_compress", ctypes.c_int, [_P, _P, _I64, _P, _I32, _I32, _P, _I64, _P]),
     ("boa_decompress", ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I32, _I32, _P, _I64]),
     ("boa_xq_cdf", ctypes.c_int, [_P, _I64, _I32, _I32, _P, _P]),

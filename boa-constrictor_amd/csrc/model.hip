@@ -79,6 +79,7 @@ struct GemmArgs {
     int64_t ldc;
     const float* ln_w;
     const float* ln_b;
+    const float2* ln_stats;  // per-row (mean, rstd) from k_ln_stats
     int64_t M;
     int N;
     int K;
@@ -97,8 +98,6 @@ __global__ void __launch_bounds__(256, 2) k_gemm(GemmArgs g) {
     constexpr int B_LD = BN * BK / 4 / 256;
     __shared__ __attribute__((aligned(16))) float sA[2][BM * LDK];
     __shared__ __attribute__((aligned(16))) float sB[2][BN * LDK];
-    __shared__ float sMu[LNV ? BM : 1];
-    __shared__ float sRs[LNV ? BM : 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
@@ -114,38 +113,6 @@ __global__ void __launch_bounds__(256, 2) k_gemm(GemmArgs g) {
     const int64_t M = g.M;
     const int N = g.N, K = g.K;
 
-    if constexpr (LNV > 0) {
-        for (int r = wave; r < BM; r += 4) {
-            const int64_t m = m0 + r;
-            float mu = 0.0f, rs = 0.0f;
-            if (m < M) {
-                const float* row = g.A + m * g.lda;
-                float v[4 * LNV];
-#pragma unroll
-                for (int i = 0; i < LNV; ++i) {
-                    const float4 q = *reinterpret_cast<const float4*>(row + 256 * i + 4 * lane);
-                    v[4 * i + 0] = q.x; v[4 * i + 1] = q.y; v[4 * i + 2] = q.z; v[4 * i + 3] = q.w;
-                }
-                float s = 0.0f;
-#pragma unroll
-                for (int i = 0; i < 4 * LNV; ++i) s = s + v[i];
-                s = wave_sum(s);
-                mu = s / (float)(256 * LNV);
-                float sq = 0.0f;
-#pragma unroll
-                for (int i = 0; i < 4 * LNV; ++i) {
-                    const float d = v[i] - mu;
-                    sq = sq + d * d;
-                }
-                sq = wave_sum(sq);
-                const float var = sq / (float)(256 * LNV);
-                rs = 1.0f / sqrtf(var + 1e-5f);
-            }
-            if (lane == 0) { sMu[r] = mu; sRs[r] = rs; }
-        }
-        __syncthreads();
-    }
-
     float4 ra[A_LD], rb[B_LD];
     auto load_tiles = [&](int k0) {
 #pragma unroll
@@ -157,7 +124,8 @@ __global__ void __launch_bounds__(256, 2) k_gemm(GemmArgs g) {
             if (m < M) {
                 v = *reinterpret_cast<const float4*>(g.A + m * g.lda + k0 + c);
                 if constexpr (LNV > 0) {
-                    const float mu = sMu[r], rs = sRs[r];
+                    const float2 st = g.ln_stats[m];
+                    const float mu = st.x, rs = st.y;
                     const float4 w = *reinterpret_cast<const float4*>(g.ln_w + k0 + c);
                     const float4 b = *reinterpret_cast<const float4*>(g.ln_b + k0 + c);
                     v.x = ((v.x - mu) * rs) * w.x + b.x;
@@ -280,6 +248,40 @@ static GemmArgs gemm_args(const float* A, int64_t lda, const float* W, const flo
 }
 
 // ================================================================================================
+// LayerNorm row statistics (model.py:45,51: nn.LayerNorm, eps 1e-5, biased variance): one wavefront per
+// row, lane j holding elements 4j.. of each 256-wide slab; sum and sum of squared deviations by butterfly
+// reduction (fixed order, identical in every lane).  The consuming GEMM applies ((x - mean) * rstd) * w + b
+// while staging A.
+template <int LNV>
+__global__ void __launch_bounds__(256) k_ln_stats(const float* __restrict__ A, int64_t lda, int64_t M,
+                                                 float2* __restrict__ stats) {
+    const int lane = threadIdx.x & 63;
+    const int64_t m = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    if (m >= M) return;
+    const float* row = A + m * lda;
+    float v[4 * LNV];
+#pragma unroll
+    for (int i = 0; i < LNV; ++i) {
+        const float4 q = *reinterpret_cast<const float4*>(row + 256 * i + 4 * lane);
+        v[4 * i + 0] = q.x; v[4 * i + 1] = q.y; v[4 * i + 2] = q.z; v[4 * i + 3] = q.w;
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4 * LNV; ++i) s = s + v[i];
+    s = wave_sum(s);
+    const float mu = s / (float)(256 * LNV);
+    float sq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4 * LNV; ++i) {
+        const float d = v[i] - mu;
+        sq = sq + d * d;
+    }
+    sq = wave_sum(sq);
+    const float var = sq / (float)(256 * LNV);
+    if (lane == 0) stats[m] = make_float2(mu, 1.0f / sqrtf(var + 1e-5f));
+}
+
+// ================================================================================================
 // Embedding gathers.  One wavefront per row; lane j copies elements 4j.. of each 256-wide slab.
 __global__ void __launch_bounds__(256) k_embed_bytes(const uint8_t* __restrict__ bytes, int64_t stride,
                                                     const int32_t* __restrict__ lens, int t0, int Tc,
@@ -343,11 +345,59 @@ __global__ void __launch_bounds__(256) k_conv_silu(const float* __restrict__ xz,
 // ================================================================================================
 // Selective scan, fused with dt_proj + softplus, the D skip and the SiLU(z) gate (App. A of the mixer):
 //   dt = softplus(W_dt . dr + b_dt)                  (torch threshold 20)
-//   h_n <- exp(dt * A_n) * h_n + (dt * B_n) * x      A = -exp(A_log), precomputed
+//   h_n <- exp(dt * A_n) * h_n + (dt * B_n) * x      A = -exp(A_log), precomputed as A * log2(e) so the
+//                                                    16 exponentials per position are exp2 (v_exp_f32)
 //   y = sum_n h_n * C_n + D * x ;  y <- y * SiLU(z)
 // One thread per (lane, channel), h[16] in registers across the Tc positions; the [dr | B | C] rows of the
 // lane's positions are staged in LDS (uniform across the workgroup).  State [lane][di][NS] in HBM between
 // launches.  y overwrites x in place.
+// One position of one channel: the arithmetic shared by the tile kernel and the step kernel (this shared
+// function is what makes the two produce identical bits).  row = [dr (R) | B (NS) | C (NS)] of the position.
+template <int NS, int R>
+__device__ __forceinline__ float scan_position(const float* row, const float (&wr)[R], float bdt, const float (&a)[NS],
+                                               float Dc, float x, float z, float (&h)[NS]) {
+    float dt = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) dt = dt + row[r] * wr[r];
+    dt = dt + bdt;
+    dt = (dt > 20.0f) ? dt : log1pf(expf(dt));
+    float y = 0.0f;
+#pragma unroll
+    for (int n = 0; n < NS; ++n) {
+        const float dA = exp2f(dt * a[n]);
+        const float dBx = (dt * row[R + n]) * x;
+        h[n] = dA * h[n] + dBx;
+        y = y + h[n] * row[R + NS + n];
+    }
+    y = y + Dc * x;
+    return y * (z / (1.0f + expf(-z)));
+}
+
+template <int NS, int R>
+__device__ __forceinline__ void scan_load_channel(int c, const float* hp, const float* Aneg, const float* dt_w,
+                                                  float (&h)[NS], float (&a)[NS], float (&wr)[R]) {
+#pragma unroll
+    for (int n = 0; n < NS; n += 4) {
+        const float4 q = *reinterpret_cast<const float4*>(hp + n);
+        h[n] = q.x; h[n + 1] = q.y; h[n + 2] = q.z; h[n + 3] = q.w;
+        const float4 p = *reinterpret_cast<const float4*>(Aneg + (int64_t)c * NS + n);
+        a[n] = p.x; a[n + 1] = p.y; a[n + 2] = p.z; a[n + 3] = p.w;
+    }
+#pragma unroll
+    for (int r = 0; r < R; r += 4) {
+        const float4 q = *reinterpret_cast<const float4*>(dt_w + (int64_t)c * R + r);
+        wr[r] = q.x; wr[r + 1] = q.y; wr[r + 2] = q.z; wr[r + 3] = q.w;
+    }
+}
+
+template <int NS>
+__device__ __forceinline__ void scan_store_channel(float* hp, const float (&h)[NS]) {
+#pragma unroll
+    for (int n = 0; n < NS; n += 4)
+        *reinterpret_cast<float4*>(hp + n) = make_float4(h[n], h[n + 1], h[n + 2], h[n + 3]);
+}
+
+// Tile kernel (compress path): Tc positions per lane, h in registers across them.
 template <int NS, int R>
 __global__ void __launch_bounds__(256) k_scan(float* __restrict__ xs_y, const float* __restrict__ dbc, int ldd,
                                              const float* __restrict__ xz, int64_t ldxz,
@@ -367,44 +417,35 @@ __global__ void __launch_bounds__(256) k_scan(float* __restrict__ xs_y, const fl
     if (c >= di) return;
     float h[NS], a[NS], wr[R];
     float* hp = ssm + (b * di + c) * NS;
-#pragma unroll
-    for (int n = 0; n < NS; n += 4) {
-        const float4 q = *reinterpret_cast<const float4*>(hp + n);
-        h[n] = q.x; h[n + 1] = q.y; h[n + 2] = q.z; h[n + 3] = q.w;
-        const float4 p = *reinterpret_cast<const float4*>(Aneg + (int64_t)c * NS + n);
-        a[n] = p.x; a[n + 1] = p.y; a[n + 2] = p.z; a[n + 3] = p.w;
-    }
-#pragma unroll
-    for (int r = 0; r < R; r += 4) {
-        const float4 q = *reinterpret_cast<const float4*>(dt_w + (int64_t)c * R + r);
-        wr[r] = q.x; wr[r + 1] = q.y; wr[r + 2] = q.z; wr[r + 3] = q.w;
-    }
+    scan_load_channel<NS, R>(c, hp, Aneg, dt_w, h, a, wr);
     const float bdt = dt_b[c], Dc = Dp[c];
     for (int t = 0; t < Tc; ++t) {
-        const float* row = s_dbc + t * W;
-        float dt = 0.0f;
-#pragma unroll
-        for (int r = 0; r < R; ++r) dt = dt + row[r] * wr[r];
-        dt = dt + bdt;
-        dt = (dt > 20.0f) ? dt : log1pf(expf(dt));
         const int64_t m = row0 + t;
         const float x = xs_y[m * di + c];
         const float z = xz[m * ldxz + di + c];
-        float y = 0.0f;
-#pragma unroll
-        for (int n = 0; n < NS; ++n) {
-            const float dA = expf(dt * a[n]);
-            const float dBx = (dt * row[R + n]) * x;
-            h[n] = dA * h[n] + dBx;
-            y = y + h[n] * row[R + NS + n];
-        }
-        y = y + Dc * x;
-        y = y * (z / (1.0f + expf(-z)));
-        xs_y[m * di + c] = y;
+        xs_y[m * di + c] = scan_position<NS, R>(s_dbc + t * W, wr, bdt, a, Dc, x, z, h);
     }
-#pragma unroll
-    for (int n = 0; n < NS; n += 4)
-        *reinterpret_cast<float4*>(hp + n) = make_float4(h[n], h[n + 1], h[n + 2], h[n + 3]);
+    scan_store_channel<NS>(hp, h);
+}
+
+// Step kernel (decompress path): one position per lane; the [dr | B | C] row is uniform across the
+// workgroup and read straight from memory.
+template <int NS, int R>
+__global__ void __launch_bounds__(256) k_scan_step(float* __restrict__ xs_y, const float* __restrict__ dbc, int ldd,
+                                                  const float* __restrict__ xz, int64_t ldxz,
+                                                  const float* __restrict__ dt_w, const float* __restrict__ dt_b,
+                                                  const float* __restrict__ Aneg, const float* __restrict__ Dp,
+                                                  float* __restrict__ ssm, int di) {
+    const int64_t b = blockIdx.y;
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= di) return;
+    float h[NS], a[NS], wr[R];
+    float* hp = ssm + (b * di + c) * NS;
+    scan_load_channel<NS, R>(c, hp, Aneg, dt_w, h, a, wr);
+    const float x = xs_y[b * di + c];
+    const float z = xz[b * ldxz + di + c];
+    xs_y[b * di + c] = scan_position<NS, R>(dbc + b * ldd, wr, dt_b[c], a, Dp[c], x, z, h);
+    scan_store_channel<NS>(hp, h);
 }
 
 // ================================================================================================
@@ -553,6 +594,22 @@ struct LayerW {
     float* Aneg;
 };
 
+// Per-kernel-class event timing (boa_profile / boa_profile_read).
+enum ProfClass {
+    PC_EMBED, PC_IN, PC_CONV, PC_XPROJ, PC_SCAN, PC_OUT, PC_FF1, PC_FF2, PC_HEAD1, PC_HEAD2, PC_ENCODE, PC_DECODE,
+    PC_LN, PC_COUNT
+};
+static const char* kProfNames[PC_COUNT] = {"embed",    "gemm_in_proj", "conv",     "gemm_x_proj",
+                                           "scan",     "gemm_out_proj", "gemm_ff1", "gemm_ff2",
+                                           "gemm_head1", "gemm_head2", "encode",   "decode",
+                                           "ln_stats"};
+struct ProfClassState {
+    int64_t launches = 0;
+    int64_t used = 0;
+    double flops = 0.0, bytes = 0.0;
+    std::vector<hipEvent_t> ev;  // 2 per sampled launch, created on first use and reused
+};
+
 struct boa_ctx {
     boa_model_cfg cfg;
     int d, di, NS, R, V, L, DC;
@@ -566,12 +623,81 @@ struct boa_ctx {
     float* conv_hist = nullptr;  // [L][max_lanes][3][di]
     float* ssm = nullptr;        // [L][max_lanes][di][NS]
     float *x = nullptr, *xz = nullptr, *xs = nullptr, *dbc = nullptr, *mm = nullptr, *logits = nullptr;
+    float2* stats = nullptr;
     int32_t* tokens = nullptr;
     EncState* enc = nullptr;
     DecState* dec = nullptr;
     int32_t* flag = nullptr;
     int64_t device_bytes = 0;
+    bool prof_on = false;
+    ProfClassState prof[PC_COUNT];
 };
+
+// Returns the event-pair index of this launch, or -1 when not sampled.
+static int64_t prof_start(boa_ctx* x, int cls) {
+    if (!x->prof_on) return -1;
+    ProfClassState& p = x->prof[cls];
+    if (p.used >= BOA_PROF_SAMPLES) return -1;
+    const int64_t i = p.used;
+    if ((int64_t)p.ev.size() < 2 * (i + 1)) {
+        hipEvent_t a, b;
+        if (hipEventCreate(&a) != hipSuccess) return -1;
+        if (hipEventCreate(&b) != hipSuccess) { (void)hipEventDestroy(a); return -1; }
+        p.ev.push_back(a);
+        p.ev.push_back(b);
+    }
+    if (hipEventRecord(p.ev[2 * i], x->stream) != hipSuccess) return -1;
+    return i;
+}
+
+static void prof_stop(boa_ctx* x, int cls, int64_t i, double flops, double bytes) {
+    if (!x->prof_on) return;
+    ProfClassState& p = x->prof[cls];
+    p.launches++;
+    if (i < 0) return;
+    if (hipEventRecord(p.ev[2 * i + 1], x->stream) != hipSuccess) return;
+    p.used = i + 1;
+    p.flops += flops;
+    p.bytes += bytes;
+}
+
+extern "C" int boa_profile(boa_ctx* x, int enable) {
+    if (!x) return boa_fail(BOA_ERR_ARG, "boa_profile: null context");
+    if (enable) {
+        for (auto& p : x->prof) { p.launches = 0; p.used = 0; p.flops = 0.0; p.bytes = 0.0; }
+    }
+    x->prof_on = enable != 0;
+    return BOA_OK;
+}
+
+extern "C" int boa_profile_read(boa_ctx* x, boa_prof_entry* out, int32_t cap, int32_t* n) {
+    if (!x || !n || (cap > 0 && !out)) return boa_fail(BOA_ERR_ARG, "boa_profile_read: bad arguments");
+    BOA_HIP_TRY(hipStreamSynchronize(x->stream));
+    int32_t k = 0;
+    for (int c = 0; c < PC_COUNT; ++c) {
+        const ProfClassState& p = x->prof[c];
+        if (p.launches == 0) continue;
+        if (k < cap) {
+            boa_prof_entry& e = out[k];
+            memset(&e, 0, sizeof(e));
+            snprintf(e.name, sizeof(e.name), "%s", kProfNames[c]);
+            e.launches = p.launches;
+            e.sampled = p.used;
+            double ms = 0.0;
+            for (int64_t i = 0; i < p.used; ++i) {
+                float t = 0.0f;
+                BOA_HIP_TRY(hipEventElapsedTime(&t, p.ev[2 * i], p.ev[2 * i + 1]));
+                ms += t;
+            }
+            e.ms = ms;
+            e.flops = p.flops;
+            e.bytes = p.bytes;
+        }
+        ++k;
+    }
+    *n = k;
+    return BOA_OK;
+}
 
 static int64_t weights_floats(const boa_model_cfg& c, int R) {
     const int64_t d = c.d_model, di = (int64_t)c.expand * c.d_model, NS = c.d_state, V = c.vocab, DC = c.d_conv;
@@ -614,9 +740,11 @@ extern "C" int boa_ctx_destroy(boa_ctx* ctx) {
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     else (void)hipDeviceSynchronize();
     void* ptrs[] = {ctx->wblob, ctx->aneg, ctx->conv_hist, ctx->ssm, ctx->x, ctx->xz, ctx->xs, ctx->dbc,
-                    ctx->mm, ctx->logits, ctx->tokens, ctx->enc, ctx->dec, ctx->flag};
+                    ctx->mm, ctx->logits, ctx->stats, ctx->tokens, ctx->enc, ctx->dec, ctx->flag};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
+    for (auto& p : ctx->prof)
+        for (hipEvent_t e : p.ev) (void)hipEventDestroy(e);
     delete ctx;
     return BOA_OK;
 }
@@ -666,6 +794,7 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
     TRY_ALLOC(x->dbc, max_rows * (R + 2 * NS));
     TRY_ALLOC(x->mm, max_rows * d);
     TRY_ALLOC(x->logits, max_rows * V);
+    TRY_ALLOC(x->stats, max_rows);
     TRY_ALLOC(x->tokens, (int64_t)max_lanes);
     TRY_ALLOC(x->enc, (int64_t)max_lanes);
     TRY_ALLOC(x->dec, (int64_t)max_lanes);
@@ -697,7 +826,8 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
         w.ff2_w = take((int64_t)d * 4 * d); w.ff2_b = take(d);
         w.Aneg = x->aneg + (int64_t)l * di * NS;
         for (int64_t i = 0; i < (int64_t)di * NS; ++i)
-            aneg_host[(size_t)l * di * NS + i] = (float)(-exp((double)hw[a_off + i]));  // A = -exp(A_log)
+            // A = -exp(A_log), stored pre-scaled by log2(e) so that exp(dt * A) = exp2(dt * A2)
+            aneg_host[(size_t)l * di * NS + i] = (float)(-exp((double)hw[a_off + i]) * 1.4426950408889634);
         x->layers.push_back(w);
     }
     x->h1_w = take((int64_t)d * d); x->h1_b = take(d);
@@ -729,58 +859,99 @@ extern "C" int boa_state_reset(boa_ctx* x, int32_t lanes) {
     return BOA_OK;
 }
 
+// Launch wrappers that record per-class timing when profiling is on.
+#define PROF(cls, flops, bytes, ...)                                \
+    do {                                                            \
+        const int64_t _pi = prof_start(x, (cls));                   \
+        __VA_ARGS__;                                                \
+        prof_stop(x, (cls), _pi, (double)(flops), (double)(bytes)); \
+    } while (0)
+
+static double gemm_flops(int64_t M, int N, int K) { return 2.0 * (double)M * N * K; }
+static double gemm_bytes(int64_t M, int N, int K) { return 4.0 * ((double)M * K + (double)N * K + (double)M * N); }
+
+static void launch_ln_stats(boa_ctx* x, const float* A, int64_t lda, int64_t M) {
+    const unsigned blocks = (unsigned)((M + 3) / 4);
+    if (x->d == 256)
+        PROF(PC_LN, 0.0, 4.0 * M * x->d + 8.0 * M,
+             hipLaunchKernelGGL((k_ln_stats<1>), dim3(blocks), dim3(256), 0, x->stream, A, lda, M, x->stats));
+    else
+        PROF(PC_LN, 0.0, 4.0 * M * x->d + 8.0 * M,
+             hipLaunchKernelGGL((k_ln_stats<2>), dim3(blocks), dim3(256), 0, x->stream, A, lda, M, x->stats));
+}
+
 // One block of the model over B lanes x Tc positions, in place on ctx->x.
 static int run_layer(boa_ctx* x, int l, int B, int Tc) {
     const LayerW& w = x->layers[l];
     const int d = x->d, di = x->di, NS = x->NS, R = x->R;
     const int64_t M = (int64_t)B * Tc;
     hipStream_t s = x->stream;
-    int rc;
+    int rc = 0;
     // LN1 + in_proj -> xz [M][2di]
     {
+        launch_ln_stats(x, x->x, d, M);
         GemmArgs g = gemm_args(x->x, d, w.in_w, w.in_b, x->xz, 2 * di, M, 2 * di, d);
-        g.ln_w = w.ln1_w; g.ln_b = w.ln1_b;
-        rc = (d == 256) ? launch_gemm<1, EPI_BIAS>(g, s) : launch_gemm<2, EPI_BIAS>(g, s);
+        g.ln_w = w.ln1_w; g.ln_b = w.ln1_b; g.ln_stats = x->stats;
+        PROF(PC_IN, gemm_flops(M, 2 * di, d), gemm_bytes(M, 2 * di, d),
+             rc = (d == 256) ? launch_gemm<1, EPI_BIAS>(g, s) : launch_gemm<2, EPI_BIAS>(g, s));
         if (rc) return rc;
     }
     // conv + SiLU -> xs
-    hipLaunchKernelGGL(k_conv_silu, dim3((di + 255) / 256, B), dim3(256), 0, s, x->xz, (int64_t)2 * di,
-                       x->conv_hist + (int64_t)l * x->max_lanes * 3 * di, w.conv_w, w.conv_b, x->xs, di, Tc);
+    PROF(PC_CONV, 8.0 * M * di, 4.0 * (2.0 * M * di + 6.0 * B * di),
+         hipLaunchKernelGGL(k_conv_silu, dim3((di + 255) / 256, B), dim3(256), 0, s, x->xz, (int64_t)2 * di,
+                            x->conv_hist + (int64_t)l * x->max_lanes * 3 * di, w.conv_w, w.conv_b, x->xs, di, Tc));
     // x_proj -> dbc [M][R+2NS]
     {
         GemmArgs g = gemm_args(x->xs, di, w.x_w, nullptr, x->dbc, R + 2 * NS, M, R + 2 * NS, di);
-        rc = launch_gemm_cfg<64, 64, 0, EPI_NONE>(g, s);
+        PROF(PC_XPROJ, gemm_flops(M, R + 2 * NS, di), gemm_bytes(M, R + 2 * NS, di),
+             rc = (launch_gemm_cfg<64, 64, 0, EPI_NONE>(g, s)));
         if (rc) return rc;
     }
     // dt_proj + softplus + scan + D + gate, y in place of xs
     {
         const size_t lds = sizeof(float) * (size_t)Tc * (R + 2 * NS);
         float* ssm = x->ssm + (int64_t)l * x->max_lanes * di * NS;
-        if (R == 16)
-            hipLaunchKernelGGL((k_scan<16, 16>), dim3((di + 255) / 256, B), dim3(256), lds, s, x->xs, x->dbc,
-                               R + 2 * NS, x->xz, (int64_t)2 * di, w.dt_w, w.dt_b, w.Aneg, w.D, ssm, di, Tc);
+        const double flops = (double)M * di * (2.0 * R + 6.0 * NS + 8.0);
+        const double bytes = 4.0 * ((double)M * (3.0 * di + R + 2 * NS) + 2.0 * B * di * NS);
+        const dim3 grid((di + 255) / 256, B);
+        if (Tc == 1 && R == 16)
+            PROF(PC_SCAN, flops, bytes,
+                 hipLaunchKernelGGL((k_scan_step<16, 16>), grid, dim3(256), 0, s, x->xs, x->dbc, R + 2 * NS, x->xz,
+                                    (int64_t)2 * di, w.dt_w, w.dt_b, w.Aneg, w.D, ssm, di));
+        else if (Tc == 1)
+            PROF(PC_SCAN, flops, bytes,
+                 hipLaunchKernelGGL((k_scan_step<16, 32>), grid, dim3(256), 0, s, x->xs, x->dbc, R + 2 * NS, x->xz,
+                                    (int64_t)2 * di, w.dt_w, w.dt_b, w.Aneg, w.D, ssm, di));
+        else if (R == 16)
+            PROF(PC_SCAN, flops, bytes,
+                 hipLaunchKernelGGL((k_scan<16, 16>), grid, dim3(256), lds, s, x->xs, x->dbc, R + 2 * NS, x->xz,
+                                    (int64_t)2 * di, w.dt_w, w.dt_b, w.Aneg, w.D, ssm, di, Tc));
         else
-            hipLaunchKernelGGL((k_scan<16, 32>), dim3((di + 255) / 256, B), dim3(256), lds, s, x->xs, x->dbc,
-                               R + 2 * NS, x->xz, (int64_t)2 * di, w.dt_w, w.dt_b, w.Aneg, w.D, ssm, di, Tc);
+            PROF(PC_SCAN, flops, bytes,
+                 hipLaunchKernelGGL((k_scan<16, 32>), grid, dim3(256), lds, s, x->xs, x->dbc, R + 2 * NS, x->xz,
+                                    (int64_t)2 * di, w.dt_w, w.dt_b, w.Aneg, w.D, ssm, di, Tc));
     }
     // out_proj -> mm [M][d]
     {
         GemmArgs g = gemm_args(x->xs, di, w.out_w, w.out_b, x->mm, d, M, d, di);
-        rc = launch_gemm<0, EPI_BIAS>(g, s);
+        PROF(PC_OUT, gemm_flops(M, d, di), gemm_bytes(M, d, di), rc = (launch_gemm<0, EPI_BIAS>(g, s)));
         if (rc) return rc;
     }
     // LN2 + FF1 + GELU -> g [M][4d] (reuses xz)
     {
+        launch_ln_stats(x, x->mm, d, M);
         GemmArgs g = gemm_args(x->mm, d, w.ff1_w, w.ff1_b, x->xz, 4 * d, M, 4 * d, d);
-        g.ln_w = w.ln2_w; g.ln_b = w.ln2_b;
-        rc = (d == 256) ? launch_gemm<1, EPI_GELU>(g, s) : launch_gemm<2, EPI_GELU>(g, s);
+        g.ln_w = w.ln2_w; g.ln_b = w.ln2_b; g.ln_stats = x->stats;
+        PROF(PC_FF1, gemm_flops(M, 4 * d, d), gemm_bytes(M, 4 * d, d),
+             rc = (d == 256) ? launch_gemm<1, EPI_GELU>(g, s) : launch_gemm<2, EPI_GELU>(g, s));
         if (rc) return rc;
     }
     // FF2 + bias + block residual -> x
     {
         GemmArgs g = gemm_args(x->xz, 4 * d, w.ff2_w, w.ff2_b, x->x, d, M, d, 4 * d);
         g.R = x->x; g.ldr = d;
-        rc = launch_gemm<0, EPI_RESID>(g, s);
+        PROF(PC_FF2, gemm_flops(M, d, 4 * d), gemm_bytes(M, d, 4 * d) + 4.0 * M * d,
+             rc = (launch_gemm<0, EPI_RESID>(g, s)));
         if (rc) return rc;
     }
     return BOA_OK;
@@ -790,15 +961,16 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc) {
 static int run_model(boa_ctx* x, int B, int Tc, float* out) {
     const int d = x->d, V = x->V;
     const int64_t M = (int64_t)B * Tc;
+    int rc = 0;
     for (int l = 0; l < x->L; ++l) {
-        int rc = run_layer(x, l, B, Tc);
+        rc = run_layer(x, l, B, Tc);
         if (rc) return rc;
     }
     GemmArgs g1 = gemm_args(x->x, d, x->h1_w, x->h1_b, x->mm, d, M, d, d);
-    int rc = launch_gemm<0, EPI_RELU>(g1, x->stream);
+    PROF(PC_HEAD1, gemm_flops(M, d, d), gemm_bytes(M, d, d), rc = (launch_gemm<0, EPI_RELU>(g1, x->stream)));
     if (rc) return rc;
     GemmArgs g2 = gemm_args(x->mm, d, x->h2_w, x->h2_b, out, V, M, V, d);
-    rc = launch_gemm<0, EPI_BIAS>(g2, x->stream);
+    PROF(PC_HEAD2, gemm_flops(M, V, d), gemm_bytes(M, V, d), rc = (launch_gemm<0, EPI_BIAS>(g2, x->stream)));
     if (rc) return rc;
     BOA_HIP_TRY(hipGetLastError());
     return BOA_OK;
@@ -806,11 +978,16 @@ static int run_model(boa_ctx* x, int B, int Tc, float* out) {
 
 static unsigned row_blocks(int64_t rows) { return (unsigned)((rows + 3) / 4); }  // 4 waves per 256-thread block
 
+static void launch_embed_tokens(boa_ctx* x, const int32_t* tokens, int64_t tok_stride, int t0, int Tc, int64_t rows) {
+    PROF(PC_EMBED, 0.0, 4.0 * rows * x->d,
+         hipLaunchKernelGGL(k_embed_tokens, dim3(row_blocks(rows)), dim3(256), 0, x->stream, tokens, tok_stride, t0,
+                            Tc, rows, x->emb, x->d, x->V, x->x));
+}
+
 extern "C" int boa_model_step(boa_ctx* x, const int32_t* d_tokens, int32_t lanes, float* d_logits) {
     if (!x || !d_tokens || !d_logits || lanes < 1 || lanes > x->max_lanes)
         return boa_fail(BOA_ERR_ARG, "boa_model_step: bad arguments");
-    hipLaunchKernelGGL(k_embed_tokens, dim3(row_blocks(lanes)), dim3(256), 0, x->stream, d_tokens, (int64_t)1, 0, 1,
-                       (int64_t)lanes, x->emb, x->d, x->V, x->x);
+    launch_embed_tokens(x, d_tokens, 1, 0, 1, lanes);
     return run_model(x, lanes, 1, d_logits);
 }
 
@@ -821,8 +998,7 @@ extern "C" int boa_model_forward(boa_ctx* x, const int32_t* d_tokens, int64_t to
     for (int t0 = 0; t0 < len; t0 += x->tile_len) {
         const int Tc = std::min(x->tile_len, len - t0);
         const int64_t rows = (int64_t)lanes * Tc;
-        hipLaunchKernelGGL(k_embed_tokens, dim3(row_blocks(rows)), dim3(256), 0, x->stream, d_tokens, tok_stride, t0,
-                           Tc, rows, x->emb, x->d, x->V, x->x);
+        launch_embed_tokens(x, d_tokens, tok_stride, t0, Tc, rows);
         int rc = run_model(x, lanes, Tc, x->logits);
         if (rc) return rc;
         hipLaunchKernelGGL(k_scatter_logits, dim3(row_blocks(rows)), dim3(256), 0, x->stream, x->logits, x->V, Tc, t0,
@@ -846,12 +1022,14 @@ extern "C" int boa_compress(boa_ctx* x, const uint8_t* d_bytes, int64_t byte_str
     for (int t0 = 0; t0 < positions; t0 += x->tile_len) {
         const int Tc = std::min(x->tile_len, positions - t0);
         const int64_t rows = (int64_t)lanes * Tc;
-        hipLaunchKernelGGL(k_embed_bytes, dim3(row_blocks(rows)), dim3(256), 0, s, d_bytes, byte_stride, d_lens, t0, Tc,
-                           rows, x->emb, x->d, x->V, x->x);
+        PROF(PC_EMBED, 0.0, 4.0 * rows * x->d,
+             hipLaunchKernelGGL(k_embed_bytes, dim3(row_blocks(rows)), dim3(256), 0, s, d_bytes, byte_stride, d_lens,
+                                t0, Tc, rows, x->emb, x->d, x->V, x->x));
         rc = run_model(x, lanes, Tc, x->logits);
         if (rc) return rc;
-        hipLaunchKernelGGL(k_encode_tile, dim3(lanes), dim3(64), 0, s, x->logits, x->V, Tc, t0, d_bytes, byte_stride,
-                           d_lens, x->enc, d_words, pitch_words);
+        PROF(PC_ENCODE, 0.0, 4.0 * rows * x->V + (double)rows,
+             hipLaunchKernelGGL(k_encode_tile, dim3(lanes), dim3(64), 0, s, x->logits, x->V, Tc, t0, d_bytes,
+                                byte_stride, d_lens, x->enc, d_words, pitch_words));
     }
     hipLaunchKernelGGL(k_enc_finish, dim3((lanes + 255) / 256), dim3(256), 0, s, x->enc, d_words, pitch_words, d_nwords,
                        x->flag, lanes);
@@ -875,12 +1053,12 @@ extern "C" int boa_decompress(boa_ctx* x, const uint32_t* d_payload, const int64
     hipLaunchKernelGGL(k_dec_init, dim3((lanes + 255) / 256), dim3(256), 0, s, x->dec, d_payload, d_word_off, d_nwords,
                        d_first, d_lens, x->tokens, d_out, out_stride, lanes);
     for (int t = 1; t < max_len; ++t) {
-        hipLaunchKernelGGL(k_embed_tokens, dim3(row_blocks(lanes)), dim3(256), 0, s, x->tokens, (int64_t)1, 0, 1,
-                           (int64_t)lanes, x->emb, x->d, x->V, x->x);
+        launch_embed_tokens(x, x->tokens, 1, 0, 1, lanes);
         rc = run_model(x, lanes, 1, x->logits);
         if (rc) return rc;
-        hipLaunchKernelGGL(k_decode_step, dim3(lanes), dim3(64), 0, s, x->logits, x->V, t, d_lens, x->dec, d_payload,
-                           d_word_off, d_nwords, x->tokens, d_out, out_stride);
+        PROF(PC_DECODE, 0.0, 4.0 * lanes * x->V + (double)lanes,
+             hipLaunchKernelGGL(k_decode_step, dim3(lanes), dim3(64), 0, s, x->logits, x->V, t, d_lens, x->dec,
+                                d_payload, d_word_off, d_nwords, x->tokens, d_out, out_stride));
     }
     BOA_HIP_TRY(hipGetLastError());
     BOA_HIP_TRY(hipStreamSynchronize(s));

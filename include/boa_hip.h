@@ -81,6 +81,23 @@ int boa_model_step(boa_ctx* ctx, const int32_t* d_tokens, int32_t lanes, float* 
 int boa_model_forward(boa_ctx* ctx, const int32_t* d_tokens, int64_t tok_stride, int32_t lanes,
                       int32_t len, float* d_logits);
 
+/* Opt-in per-kernel-class timing with HIP events recorded on the context's stream around each launch
+ * (first BOA_PROF_SAMPLES launches of each class per profiling window).  No reference counterpart: it
+ * replaces the reference's cudaEvent forward/encode split (boa.cpp:366-380) for measurement.            */
+#define BOA_PROF_SAMPLES 4096
+typedef struct boa_prof_entry {
+    char name[32];        /* kernel class, e.g. "gemm_ff1"                                          */
+    int64_t launches;     /* launches in the window                                                 */
+    int64_t sampled;      /* launches that were timed                                               */
+    double ms;            /* summed duration of the timed launches                                  */
+    double flops;         /* algorithmic flops of the timed launches                                */
+    double bytes;         /* algorithmic HBM bytes of the timed launches                            */
+} boa_prof_entry;
+/* enable != 0 starts a fresh window; 0 stops recording. */
+int boa_profile(boa_ctx* ctx, int enable);
+/* Synchronizes, resolves the recorded events and copies up to cap entries; *n receives the count.      */
+int boa_profile_read(boa_ctx* ctx, boa_prof_entry* out, int32_t cap, int32_t* n);
+
 /* ------------------------------------------------------------------------------------------------ */
 /* Fused batched compress: chunk i is d_bytes[i*byte_stride .. +d_lens[i]).  Byte 0 of each chunk is not
  * coded (stored raw by the caller, codec.py:38); bytes 1..len-1 are range coded (PRECISION 24) under the

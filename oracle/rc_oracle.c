@@ -325,3 +325,24 @@ void ora_xq_cdf_rows(const float* logits, int64_t rows, int K, int P, uint32_t* 
 void ora_expf_rows(const float* x, int64_t n, float* y) {
     for (int64_t i = 0; i < n; ++i) y[i] = ora_expf(x[i]);
 }
+
+/* ---------------------------------------------------------------------------------------------- */
+/* Per-lane incremental calls, one symbol at a time (the CPU baseline calls these once per lane per step,
+ * as codec.py:201 calls constriction's encoder once per lane per step). */
+size_t ora_enc_sizeof(void) { return sizeof(ora_enc); }
+size_t ora_dec_sizeof(void) { return sizeof(ora_dec); }
+
+void ora_q2_encode_one(ora_enc* st, int P, const float* probs, int K, int sym, uint32_t* out, int64_t cap) {
+    uint32_t cdf[1025];
+    if (sym < 0 || sym >= K) return;
+    ora_q2_cdf(probs, K, P, cdf);
+    ora_enc_push(st, P, cdf[sym], cdf[sym + 1] - cdf[sym], out, cap);
+}
+
+int ora_q2_decode_one(ora_dec* st, int P, const float* probs, int K, const uint32_t* in, int64_t n) {
+    uint32_t cdf[1025];
+    ora_q2_cdf(probs, K, P, cdf);
+    int s = ora_find_symbol(cdf, K, ora_dec_target(st, P));
+    ora_dec_advance(st, P, cdf[s], cdf[s + 1] - cdf[s], in, n);
+    return s;
+}

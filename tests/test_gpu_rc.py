@@ -101,7 +101,7 @@ def test_synth_tables_round_trip(gpu, ora):
     for s in range(0, S, 37):
         ref = ora.encode_tables(P, full[s], syms[s].astype(np.int32))
         assert (words[s, :nw[s]] == ref).all()
-        steps = [(int(full[s, t, v]), int(full[s, t, v + 1] - full[s, t, v])) for t, v in enumerate(syms[s])]
+        steps = [(int(full[s, t, v]), int(full[s, t, v + 1]) - int(full[s, t, v])) for t, v in enumerate(syms[s].astype(np.int64))]
         bigint_check.check(ref, steps, P)
 
 
@@ -117,8 +117,9 @@ def test_range_coder_batch_matches_q2_oracle(gpu, ora, K):
     rng = np.random.default_rng(K)
     N, T = 40, 150
     probs = _softmax(rng.normal(0, 3, (T, N, K)))
-    syms = np.array([[rng.choice(K, p=probs[t, i].astype(np.float64) / probs[t, i].sum()) for i in range(N)]
-                     for t in range(T)], dtype=np.int32)
+    p64 = probs.astype(np.float64)
+    p64 /= p64.sum(-1, keepdims=True)
+    syms = np.array([[rng.choice(K, p=p64[t, i]) for i in range(N)] for t in range(T)], dtype=np.int32)
     lens = rng.integers(0, T + 1, N)
     lens[0], lens[1] = 0, T
     b = gr.gpu.queue.RangeCoderBatch(N, K, T)
