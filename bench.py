@@ -42,8 +42,8 @@ KERNEL_NAMES = {
     ("decompress", "gemm_ff1"): "k_gemm<64, 64, 1, 2>",
     ("decompress", "gemm_ff2"): "k_gemm<64, 64, 0, 4>",
     ("decompress", "gemm_out_proj"): "k_gemm<64, 64, 0, 1>",
-    ("compress", "scan"): "k_scan<16, 16>",
-    ("decompress", "scan"): "k_scan_step<16, 16>",
+    ("compress", "scan"): "k_scan<16, 16, true>",
+    ("decompress", "scan"): "k_scan_step<16, 16, true>",
 }
 
 

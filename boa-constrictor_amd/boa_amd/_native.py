@@ -24,8 +24,9 @@ BOA_ERR_HIP = 2
 BOA_ERR_OVERFLOW = 3
 BOA_ERR_STATE = 4
 
-BOA_WEIGHTS_F32 = 0
-BOA_WEIGHTS_BF16 = 1
+BOA_PREC_F32 = 0      # fp32 MFMA
+BOA_PREC_BF16X3 = 1   # split bf16 x3 products (fp32 weights)
+BOA_PREC_BF16W = 2    # bf16 weights, split activations
 
 
 class BoaError(RuntimeError):

@@ -72,6 +72,8 @@ struct GemmArgs {
     const float* A;
     int64_t lda;
     const float* W;
+    const uint16_t* Wh;  // bf16 bits of W (split precision modes)
+    const uint16_t* Wl;  // bf16 bits of W - Wh (bf16x3 mode only)
     const float* bias;
     const float* R;
     int64_t ldr;
@@ -80,6 +82,10 @@ struct GemmArgs {
     const float* ln_w;
     const float* ln_b;
     const float2* ln_stats;  // per-row (mean, rstd) from k_ln_stats
+    const uint16_t* Ah;      // pre-split A (bf16 hi / lo parts, row stride lda) instead of fp32 A
+    const uint16_t* Al;
+    uint16_t* Ch;            // split output (bf16 hi / lo parts, row stride ldc) instead of fp32 C
+    uint16_t* Cl;
     int64_t M;
     int N;
     int K;
@@ -220,31 +226,252 @@ __global__ void __launch_bounds__(256, 2) k_gemm(GemmArgs g) {
         }
 }
 
-template <int BM, int BN, int LNV, int EPI>
-static int launch_gemm_cfg(GemmArgs g, hipStream_t s) {
+// ------------------------------------------------------------------------------------------------
+// Split-precision GEMM on v_mfma_f32_16x16x32_bf16.  Each fp32 activation a is split while it is staged
+// into LDS as a = a_hi + a_lo (both bfloat16, round to nearest even; a - a_hi is exact in fp32), each
+// weight likewise once at context creation (w = w_hi + w_lo).  With NT = 3 the product is
+// a_lo*w_hi + a_hi*w_lo + a_hi*w_hi accumulated in fp32 (the a_lo*w_lo term, below 2^-16 of the product,
+// is dropped); with NT = 2 the weights are bfloat16 themselves (w_lo = 0).  Products of bfloat16 pairs are
+// exact in fp32, so the only losses are the dropped term and fp32 accumulation.  K order per output is
+// fixed (32 per MFMA step, steps ascending), independent of M: the encoder/decoder identity holds as in
+// the fp32 kernel.  LDS rows hold 32 bf16 + 8 pad (80 B: conflict-free b128 fragment reads).
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ uint32_t bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+__device__ __forceinline__ void split2(float f, uint32_t& hi, uint32_t& lo) {
+    hi = bf16_rne(f);
+    lo = bf16_rne(f - __uint_as_float(hi << 16));
+}
+
+template <int BM, int BN, int EPI, int NT, bool ASPLIT, bool OUTS>
+__global__ void __launch_bounds__(256, 2) k_gemm_bf(GemmArgs g) {
+    constexpr int BK = 32, LDK = BK + 8;
+    constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 16, FN = WN / 16;
+    constexpr int A_LD = ASPLIT ? BM * BK / 8 / 256 : BM * BK / 4 / 256;  // per thread: 8-bf16 or float4 loads
+    constexpr int B_LD = BN * BK / 8 / 256;
+    // one LDS block: double-buffered bf16 operand tiles, reused for the fp32 output tile after the K loop
+    constexpr int LDC = BN + 4;
+    constexpr int OPER = 2 * (2 * BM * LDK + (NT == 3 ? 2 : 1) * BN * LDK);  // uint16 elements
+    constexpr int OUTT = 2 * BM * LDC;                                      // uint16 elements (fp32 tile)
+    __shared__ __attribute__((aligned(16))) uint16_t smem[OPER > OUTT ? OPER : OUTT];
+    uint16_t (*sAh)[BM * LDK] = reinterpret_cast<uint16_t (*)[BM * LDK]>(smem);
+    uint16_t (*sAl)[BM * LDK] = reinterpret_cast<uint16_t (*)[BM * LDK]>(smem + 2 * BM * LDK);
+    uint16_t (*sBh)[BN * LDK] = reinterpret_cast<uint16_t (*)[BN * LDK]>(smem + 4 * BM * LDK);
+    uint16_t (*sBl)[BN * LDK] = reinterpret_cast<uint16_t (*)[BN * LDK]>(smem + 4 * BM * LDK + 2 * BN * LDK);
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int bid = blockIdx.x;
+    const int tile = (bid & 7) * g.per_xcd + (bid >> 3);
+    if (tile >= g.mtiles * g.ntiles) return;
+    const int mt = tile / g.ntiles;
+    const int nt = tile - mt * g.ntiles;
+    const int64_t m0 = (int64_t)mt * BM;
+    const int n0 = nt * BN;
+    const int64_t M = g.M;
+    const int N = g.N, K = g.K;
+
+    // A staging registers: pre-split (uint4 = 8 bf16 of each part) or fp32 split on load (uint2 = 4 bf16)
+    uint4 rah4[ASPLIT ? A_LD : 1], ral4[ASPLIT ? A_LD : 1];
+    uint2 rah2[ASPLIT ? 1 : A_LD], ral2[ASPLIT ? 1 : A_LD];
+    uint4 rbh[B_LD], rbl[NT == 3 ? B_LD : 1];
+    auto load_tiles = [&](int k0) {
+        if constexpr (ASPLIT) {
+#pragma unroll
+            for (int i = 0; i < A_LD; ++i) {
+                const int q = tid + 256 * i;
+                const int r = q >> 2, c = (q & 3) * 8;
+                const int64_t m = m0 + r;
+                const bool ok = m < M;
+                rah4[i] = ok ? *reinterpret_cast<const uint4*>(g.Ah + m * g.lda + k0 + c) : make_uint4(0, 0, 0, 0);
+                ral4[i] = ok ? *reinterpret_cast<const uint4*>(g.Al + m * g.lda + k0 + c) : make_uint4(0, 0, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < A_LD; ++i) {
+                const int q = tid + 256 * i;
+                const int r = q >> 3, c = (q & 7) * 4;
+                const int64_t m = m0 + r;
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (m < M) v = *reinterpret_cast<const float4*>(g.A + m * g.lda + k0 + c);
+                uint32_t h0, h1, h2, h3, l0, l1, l2, l3;
+                split2(v.x, h0, l0);
+                split2(v.y, h1, l1);
+                split2(v.z, h2, l2);
+                split2(v.w, h3, l3);
+                rah2[i] = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
+                ral2[i] = make_uint2(l0 | (l1 << 16), l2 | (l3 << 16));
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < B_LD; ++i) {
+            const int q = tid + 256 * i;
+            const int r = q >> 2, c = (q & 3) * 8;
+            const int n = n0 + r;
+            const bool ok = n < N;
+            rbh[i] = ok ? *reinterpret_cast<const uint4*>(g.Wh + (int64_t)n * K + k0 + c) : make_uint4(0, 0, 0, 0);
+            if constexpr (NT == 3)
+                rbl[i] = ok ? *reinterpret_cast<const uint4*>(g.Wl + (int64_t)n * K + k0 + c) : make_uint4(0, 0, 0, 0);
+        }
+    };
+    auto store_tiles = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < A_LD; ++i) {
+            const int q = tid + 256 * i;
+            if constexpr (ASPLIT) {
+                const int off = (q >> 2) * LDK + (q & 3) * 8;
+                *reinterpret_cast<uint4*>(&sAh[buf][off]) = rah4[i];
+                *reinterpret_cast<uint4*>(&sAl[buf][off]) = ral4[i];
+            } else {
+                const int off = (q >> 3) * LDK + (q & 7) * 4;
+                *reinterpret_cast<uint2*>(&sAh[buf][off]) = rah2[i];
+                *reinterpret_cast<uint2*>(&sAl[buf][off]) = ral2[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < B_LD; ++i) {
+            const int q = tid + 256 * i;
+            const int off = (q >> 2) * LDK + (q & 3) * 8;
+            *reinterpret_cast<uint4*>(&sBh[buf][off]) = rbh[i];
+            if constexpr (NT == 3) *reinterpret_cast<uint4*>(&sBl[buf][off]) = rbl[i];
+        }
+    };
+
+    floatx4 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    const int KT = K / BK;
+    load_tiles(0);
+    store_tiles(0);
+    __syncthreads();
+    const int arow = wm * WM + (lane & 15);
+    const int brow = wn * WN + (lane & 15);
+    const int kq = 8 * (lane >> 4);
+    for (int kt = 0; kt < KT; ++kt) {
+        const int cur = kt & 1;
+        if (kt + 1 < KT) load_tiles((kt + 1) * BK);
+        bf16x8 ah[FM], al[FM], bh[FN], bl[FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            ah[i] = *reinterpret_cast<const bf16x8*>(&sAh[cur][(arow + 16 * i) * LDK + kq]);
+            al[i] = *reinterpret_cast<const bf16x8*>(&sAl[cur][(arow + 16 * i) * LDK + kq]);
+        }
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            bh[j] = *reinterpret_cast<const bf16x8*>(&sBh[cur][(brow + 16 * j) * LDK + kq]);
+            if constexpr (NT == 3) bl[j] = *reinterpret_cast<const bf16x8*>(&sBl[cur][(brow + 16 * j) * LDK + kq]);
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bh[j], acc[i][j], 0, 0, 0);
+                if constexpr (NT == 3)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bl[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bh[j], acc[i][j], 0, 0, 0);
+            }
+        if (kt + 1 < KT) store_tiles(cur ^ 1);
+        __syncthreads();
+    }
+
+    // Epilogue through LDS (the operand buffers are free after the last barrier): fragments are written
+    // to an fp32 tile [BM][BN + 4] (bias and activation applied here), then rows leave in 16-byte pieces.
+    float* sC = reinterpret_cast<float*>(smem);
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int cl = wn * WN + 16 * j + (lane & 15);
+            const int col = n0 + cl;
+            float bias = 0.0f;
+            if constexpr (EPI != EPI_NONE) bias = (col < N) ? g.bias[col] : 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float v = acc[i][j][r];
+                if constexpr (EPI != EPI_NONE) v = v + bias;
+                if constexpr (EPI == EPI_GELU) v = gelu_erf(v);
+                if constexpr (EPI == EPI_RELU) v = fmaxf(v, 0.0f);
+                sC[(wm * WM + 16 * i + 4 * (lane >> 4) + r) * LDC + cl] = v;
+            }
+        }
+    __syncthreads();
+    constexpr int Q = BN / 4;  // float4 pieces per tile row
+#pragma unroll 4
+    for (int p = tid; p < BM * Q; p += 256) {
+        const int rl = p / Q, c4 = (p - rl * Q) * 4;
+        const int64_t row = m0 + rl;
+        const int col = n0 + c4;
+        if (row >= M || col >= N) continue;  // N is a multiple of 4: a piece is all in or all out
+        float4 v = *reinterpret_cast<const float4*>(&sC[rl * LDC + c4]);
+        if constexpr (EPI == EPI_RESID) {
+            const float4 rv = *reinterpret_cast<const float4*>(g.R + row * g.ldr + col);
+            v = make_float4(rv.x + v.x, rv.y + v.y, rv.z + v.z, rv.w + v.w);
+        }
+        if constexpr (OUTS) {
+            uint32_t h0, h1, h2, h3, l0, l1, l2, l3;
+            split2(v.x, h0, l0);
+            split2(v.y, h1, l1);
+            split2(v.z, h2, l2);
+            split2(v.w, h3, l3);
+            *reinterpret_cast<uint2*>(g.Ch + row * g.ldc + col) = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
+            *reinterpret_cast<uint2*>(g.Cl + row * g.ldc + col) = make_uint2(l0 | (l1 << 16), l2 | (l3 << 16));
+        } else {
+            *reinterpret_cast<float4*>(g.C + row * g.ldc + col) = v;
+        }
+    }
+}
+
+static void tile_grid(GemmArgs& g, int BM, int BN, int64_t& grid) {
     g.mtiles = (int)((g.M + BM - 1) / BM);
     g.ntiles = (g.N + BN - 1) / BN;
     const int64_t tiles = (int64_t)g.mtiles * g.ntiles;
     g.per_xcd = (int)((tiles + 7) / 8);
-    const int64_t grid = (int64_t)g.per_xcd * 8;
+    grid = (int64_t)g.per_xcd * 8;
+}
+
+// 128x128 when that still gives >= 2 workgroups per CU, else 64x64.
+static bool big_tiles(const GemmArgs& g) {
+    const int64_t big = ((g.M + 127) / 128) * (int64_t)((g.N + 127) / 128);
+    return g.N >= 128 && big >= 512;
+}
+
+template <int BM, int BN, int LNV, int EPI>
+static int launch_gemm_f32_cfg(GemmArgs g, hipStream_t s) {
+    int64_t grid;
+    tile_grid(g, BM, BN, grid);
     hipLaunchKernelGGL((k_gemm<BM, BN, LNV, EPI>), dim3((unsigned)grid), dim3(256), 0, s, g);
     return BOA_OK;
 }
 
-// Picks the tile shape: 128x128 when that still gives >= 2 workgroups per CU, else 64x64.
 template <int LNV, int EPI>
-static int launch_gemm(const GemmArgs& g, hipStream_t s) {
-    const int64_t big = ((g.M + 127) / 128) * (int64_t)((g.N + 127) / 128);
-    if (g.N >= 128 && big >= 512) return launch_gemm_cfg<128, 128, LNV, EPI>(g, s);
-    return launch_gemm_cfg<64, 64, LNV, EPI>(g, s);
+static int launch_gemm_f32(const GemmArgs& g, hipStream_t s) {
+    if (big_tiles(g)) return launch_gemm_f32_cfg<128, 128, LNV, EPI>(g, s);
+    return launch_gemm_f32_cfg<64, 64, LNV, EPI>(g, s);
 }
 
-static GemmArgs gemm_args(const float* A, int64_t lda, const float* W, const float* bias, float* C, int64_t ldc,
-                          int64_t M, int N, int K) {
-    GemmArgs g;
-    memset(&g, 0, sizeof(g));
-    g.A = A; g.lda = lda; g.W = W; g.bias = bias; g.C = C; g.ldc = ldc; g.M = M; g.N = N; g.K = K;
-    return g;
+template <int BM, int BN, int EPI, bool ASPLIT, bool OUTS>
+static int launch_gemm_bf_cfg(GemmArgs g, hipStream_t s) {
+    int64_t grid;
+    tile_grid(g, BM, BN, grid);
+    if (g.Wl)
+        hipLaunchKernelGGL((k_gemm_bf<BM, BN, EPI, 3, ASPLIT, OUTS>), dim3((unsigned)grid), dim3(256), 0, s, g);
+    else
+        hipLaunchKernelGGL((k_gemm_bf<BM, BN, EPI, 2, ASPLIT, OUTS>), dim3((unsigned)grid), dim3(256), 0, s, g);
+    return BOA_OK;
+}
+
+template <int EPI, bool ASPLIT, bool OUTS>
+static int launch_gemm_bf(const GemmArgs& g, hipStream_t s) {
+    if (big_tiles(g)) return launch_gemm_bf_cfg<128, 128, EPI, ASPLIT, OUTS>(g, s);
+    return launch_gemm_bf_cfg<64, 64, EPI, ASPLIT, OUTS>(g, s);
 }
 
 // ================================================================================================
@@ -279,6 +506,51 @@ __global__ void __launch_bounds__(256) k_ln_stats(const float* __restrict__ A, i
     sq = wave_sum(sq);
     const float var = sq / (float)(256 * LNV);
     if (lane == 0) stats[m] = make_float2(mu, 1.0f / sqrtf(var + 1e-5f));
+}
+
+// LayerNorm of a row, written as split bfloat16 parts (hi, lo) for the split-precision GEMMs: the same
+// statistics and the same ((x - mean) * rstd) * w + b expression as the fp32 path applies on load.
+template <int LNV>
+__global__ void __launch_bounds__(256) k_ln_split(const float* __restrict__ A, int64_t lda, int64_t M,
+                                                 const float* __restrict__ w, const float* __restrict__ bvec,
+                                                 uint16_t* __restrict__ Ah, uint16_t* __restrict__ Al) {
+    const int lane = threadIdx.x & 63;
+    const int64_t m = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    if (m >= M) return;
+    const float* row = A + m * lda;
+    float v[4 * LNV];
+#pragma unroll
+    for (int i = 0; i < LNV; ++i) {
+        const float4 q = *reinterpret_cast<const float4*>(row + 256 * i + 4 * lane);
+        v[4 * i + 0] = q.x; v[4 * i + 1] = q.y; v[4 * i + 2] = q.z; v[4 * i + 3] = q.w;
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4 * LNV; ++i) s = s + v[i];
+    s = wave_sum(s);
+    const float mu = s / (float)(256 * LNV);
+    float sq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4 * LNV; ++i) {
+        const float d = v[i] - mu;
+        sq = sq + d * d;
+    }
+    sq = wave_sum(sq);
+    const float var = sq / (float)(256 * LNV);
+    const float rs = 1.0f / sqrtf(var + 1e-5f);
+#pragma unroll
+    for (int i = 0; i < LNV; ++i) {
+        const int c = 256 * i + 4 * lane;
+        const float4 wv = *reinterpret_cast<const float4*>(w + c);
+        const float4 bv = *reinterpret_cast<const float4*>(bvec + c);
+        const float y[4] = {((v[4 * i + 0] - mu) * rs) * wv.x + bv.x, ((v[4 * i + 1] - mu) * rs) * wv.y + bv.y,
+                            ((v[4 * i + 2] - mu) * rs) * wv.z + bv.z, ((v[4 * i + 3] - mu) * rs) * wv.w + bv.w};
+        uint32_t h[4], l[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) split2(y[j], h[j], l[j]);
+        *reinterpret_cast<uint2*>(Ah + m * lda + c) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+        *reinterpret_cast<uint2*>(Al + m * lda + c) = make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
+    }
 }
 
 // ================================================================================================
@@ -374,13 +646,13 @@ __device__ __forceinline__ float scan_position(const float* row, const float (&w
 }
 
 template <int NS, int R>
-__device__ __forceinline__ void scan_load_channel(int c, const float* hp, const float* Aneg, const float* dt_w,
+__device__ __forceinline__ void scan_load_channel(int c, int di, const float* hp, const float* Aneg, const float* dt_w,
                                                   float (&h)[NS], float (&a)[NS], float (&wr)[R]) {
 #pragma unroll
     for (int n = 0; n < NS; n += 4) {
-        const float4 q = *reinterpret_cast<const float4*>(hp + n);
+        const float4 q = *reinterpret_cast<const float4*>(hp + (int64_t)(n / 4) * di * 4);
         h[n] = q.x; h[n + 1] = q.y; h[n + 2] = q.z; h[n + 3] = q.w;
-        const float4 p = *reinterpret_cast<const float4*>(Aneg + (int64_t)c * NS + n);
+        const float4 p = *reinterpret_cast<const float4*>(Aneg + ((int64_t)(n / 4) * di + c) * 4);
         a[n] = p.x; a[n + 1] = p.y; a[n + 2] = p.z; a[n + 3] = p.w;
     }
 #pragma unroll
@@ -391,19 +663,33 @@ __device__ __forceinline__ void scan_load_channel(int c, const float* hp, const 
 }
 
 template <int NS>
-__device__ __forceinline__ void scan_store_channel(float* hp, const float (&h)[NS]) {
+__device__ __forceinline__ void scan_store_channel(float* hp, int di, const float (&h)[NS]) {
 #pragma unroll
     for (int n = 0; n < NS; n += 4)
-        *reinterpret_cast<float4*>(hp + n) = make_float4(h[n], h[n + 1], h[n + 2], h[n + 3]);
+        *reinterpret_cast<float4*>(hp + (int64_t)(n / 4) * di * 4) = make_float4(h[n], h[n + 1], h[n + 2], h[n + 3]);
+}
+
+// Output of one position: fp32 in place of x (fp32 GEMM mode) or split bf16 parts (split modes).
+template <bool OUTS>
+__device__ __forceinline__ void scan_store_y(float* xs_y, uint16_t* yh, uint16_t* yl, int64_t idx, float y) {
+    if constexpr (OUTS) {
+        uint32_t h, l;
+        split2(y, h, l);
+        yh[idx] = (uint16_t)h;
+        yl[idx] = (uint16_t)l;
+    } else {
+        xs_y[idx] = y;
+    }
 }
 
 // Tile kernel (compress path): Tc positions per lane, h in registers across them.
-template <int NS, int R>
+template <int NS, int R, bool OUTS>
 __global__ void __launch_bounds__(256) k_scan(float* __restrict__ xs_y, const float* __restrict__ dbc, int ldd,
                                              const float* __restrict__ xz, int64_t ldxz,
                                              const float* __restrict__ dt_w, const float* __restrict__ dt_b,
                                              const float* __restrict__ Aneg, const float* __restrict__ Dp,
-                                             float* __restrict__ ssm, int di, int Tc) {
+                                             float* __restrict__ ssm, int di, int Tc, uint16_t* __restrict__ yh,
+                                             uint16_t* __restrict__ yl) {
     extern __shared__ float s_dbc[];
     constexpr int W = R + 2 * NS;
     const int64_t b = blockIdx.y;
@@ -416,36 +702,42 @@ __global__ void __launch_bounds__(256) k_scan(float* __restrict__ xs_y, const fl
     __syncthreads();
     if (c >= di) return;
     float h[NS], a[NS], wr[R];
-    float* hp = ssm + (b * di + c) * NS;
-    scan_load_channel<NS, R>(c, hp, Aneg, dt_w, h, a, wr);
+    float* hp = ssm + b * di * NS + 4 * c;
+    scan_load_channel<NS, R>(c, di, hp, Aneg, dt_w, h, a, wr);
     const float bdt = dt_b[c], Dc = Dp[c];
+    float xn = xs_y[row0 * di + c];
+    float zn = xz[row0 * ldxz + di + c];
     for (int t = 0; t < Tc; ++t) {
         const int64_t m = row0 + t;
-        const float x = xs_y[m * di + c];
-        const float z = xz[m * ldxz + di + c];
-        xs_y[m * di + c] = scan_position<NS, R>(s_dbc + t * W, wr, bdt, a, Dc, x, z, h);
+        const float x = xn, z = zn;
+        if (t + 1 < Tc) {  // next position's inputs in flight while this one computes
+            xn = xs_y[(m + 1) * di + c];
+            zn = xz[(m + 1) * ldxz + di + c];
+        }
+        scan_store_y<OUTS>(xs_y, yh, yl, m * di + c, scan_position<NS, R>(s_dbc + t * W, wr, bdt, a, Dc, x, z, h));
     }
-    scan_store_channel<NS>(hp, h);
+    scan_store_channel<NS>(hp, di, h);
 }
 
 // Step kernel (decompress path): one position per lane; the [dr | B | C] row is uniform across the
 // workgroup and read straight from memory.
-template <int NS, int R>
+template <int NS, int R, bool OUTS>
 __global__ void __launch_bounds__(256) k_scan_step(float* __restrict__ xs_y, const float* __restrict__ dbc, int ldd,
                                                   const float* __restrict__ xz, int64_t ldxz,
                                                   const float* __restrict__ dt_w, const float* __restrict__ dt_b,
                                                   const float* __restrict__ Aneg, const float* __restrict__ Dp,
-                                                  float* __restrict__ ssm, int di) {
+                                                  float* __restrict__ ssm, int di, uint16_t* __restrict__ yh,
+                                                  uint16_t* __restrict__ yl) {
     const int64_t b = blockIdx.y;
     const int c = blockIdx.x * blockDim.x + threadIdx.x;
     if (c >= di) return;
     float h[NS], a[NS], wr[R];
-    float* hp = ssm + (b * di + c) * NS;
-    scan_load_channel<NS, R>(c, hp, Aneg, dt_w, h, a, wr);
+    float* hp = ssm + b * di * NS + 4 * c;
+    scan_load_channel<NS, R>(c, di, hp, Aneg, dt_w, h, a, wr);
     const float x = xs_y[b * di + c];
     const float z = xz[b * ldxz + di + c];
-    xs_y[b * di + c] = scan_position<NS, R>(dbc + b * ldd, wr, dt_b[c], a, Dp[c], x, z, h);
-    scan_store_channel<NS>(hp, h);
+    scan_store_y<OUTS>(xs_y, yh, yl, b * di + c, scan_position<NS, R>(dbc + b * ldd, wr, dt_b[c], a, Dp[c], x, z, h));
+    scan_store_channel<NS>(hp, di, h);
 }
 
 // ================================================================================================
@@ -588,11 +880,29 @@ __global__ void __launch_bounds__(256) k_scatter_logits(const float* __restrict_
 // ================================================================================================
 // Context
 
+// A GEMM weight matrix [N][K]: fp32 values plus, in the split-precision modes, bf16 parts (hi, lo).
+struct MatW {
+    const float* f = nullptr;
+    const uint16_t* h = nullptr;
+    const uint16_t* l = nullptr;
+    int64_t n = 0;
+};
+
 struct LayerW {
-    const float *ln1_w, *ln1_b, *in_w, *in_b, *conv_w, *conv_b, *x_w, *dt_w, *dt_b, *A_log, *D, *out_w, *out_b,
-        *ln2_w, *ln2_b, *ff1_w, *ff1_b, *ff2_w, *ff2_b;
+    const float *ln1_w, *ln1_b, *in_b, *conv_w, *conv_b, *dt_w, *dt_b, *A_log, *D, *out_b, *ln2_w, *ln2_b, *ff1_b,
+        *ff2_b;
+    MatW in_w, x_w, out_w, ff1_w, ff2_w;
     float* Aneg;
 };
+
+static GemmArgs gemm_args(const float* A, int64_t lda, const MatW& W, const float* bias, float* C, int64_t ldc,
+                          int64_t M, int N, int K) {
+    GemmArgs g;
+    memset(&g, 0, sizeof(g));
+    g.A = A; g.lda = lda; g.W = W.f; g.Wh = W.h; g.Wl = W.l; g.bias = bias; g.C = C; g.ldc = ldc;
+    g.M = M; g.N = N; g.K = K;
+    return g;
+}
 
 // Per-kernel-class event timing (boa_profile / boa_profile_read).
 enum ProfClass {
@@ -618,12 +928,16 @@ struct boa_ctx {
     int64_t max_rows = 0;
     float* wblob = nullptr;
     float* aneg = nullptr;
-    const float *emb = nullptr, *h1_w = nullptr, *h1_b = nullptr, *h2_w = nullptr, *h2_b = nullptr;
+    const float *emb = nullptr, *h1_b = nullptr, *h2_b = nullptr;
+    MatW h1_w, h2_w;
+    int prec = BOA_PREC_F32;
+    uint16_t* wsplit = nullptr;
     std::vector<LayerW> layers;
     float* conv_hist = nullptr;  // [L][max_lanes][3][di]
-    float* ssm = nullptr;        // [L][max_lanes][di][NS]
+    float* ssm = nullptr;        // [L][max_lanes][NS/4][di][4]
     float *x = nullptr, *xz = nullptr, *xs = nullptr, *dbc = nullptr, *mm = nullptr, *logits = nullptr;
     float2* stats = nullptr;
+    uint16_t *ah = nullptr, *al = nullptr;  // split activations [max_rows][max(d, di)] (split modes)
     int32_t* tokens = nullptr;
     EncState* enc = nullptr;
     DecState* dec = nullptr;
@@ -740,7 +1054,8 @@ extern "C" int boa_ctx_destroy(boa_ctx* ctx) {
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     else (void)hipDeviceSynchronize();
     void* ptrs[] = {ctx->wblob, ctx->aneg, ctx->conv_hist, ctx->ssm, ctx->x, ctx->xz, ctx->xs, ctx->dbc,
-                    ctx->mm, ctx->logits, ctx->stats, ctx->tokens, ctx->enc, ctx->dec, ctx->flag};
+                    ctx->mm, ctx->logits, ctx->stats, ctx->tokens, ctx->enc, ctx->dec, ctx->flag, ctx->wsplit,
+                    ctx->ah, ctx->al};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     for (auto& p : ctx->prof)
@@ -756,7 +1071,22 @@ static hipError_t dmalloc(boa_ctx* c, T** p, int64_t count) {
     return hipMalloc((void**)p, (size_t)bytes);
 }
 
-extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, int64_t nbytes, int weight_dtype,
+// Host-side round to nearest even of a float to bfloat16 bits (finite inputs).
+static uint16_t host_bf16(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+static float host_bf16_to_f(uint16_t h) {
+    const uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, int64_t nbytes, int precision,
                               int32_t max_lanes, int32_t tile_len, void* stream, boa_ctx** out) {
     if (!out) return boa_fail(BOA_ERR_ARG, "boa_ctx_create: null output");
     *out = nullptr;
@@ -764,8 +1094,8 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
     int R;
     int rc = resolve_cfg(cfg, c, R);
     if (rc != BOA_OK) return rc;
-    if (weight_dtype != BOA_WEIGHTS_F32)
-        return boa_fail(BOA_ERR_ARG, "boa_ctx_create: weight dtype %d not supported", weight_dtype);
+    if (precision != BOA_PREC_F32 && precision != BOA_PREC_BF16X3 && precision != BOA_PREC_BF16W)
+        return boa_fail(BOA_ERR_ARG, "boa_ctx_create: unknown precision mode %d", precision);
     const int64_t nf = weights_floats(c, R);
     if (!h_weights || nbytes != nf * 4)
         return boa_fail(BOA_ERR_ARG, "weight blob must be %lld bytes (got %lld)", (long long)(nf * 4), (long long)nbytes);
@@ -779,6 +1109,7 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
     x->d = c.d_model; x->di = c.expand * c.d_model; x->NS = c.d_state; x->R = R; x->V = c.vocab;
     x->L = c.n_layers; x->DC = c.d_conv;
     x->stream = reinterpret_cast<hipStream_t>(stream);
+    x->prec = precision;
     x->max_lanes = max_lanes; x->tile_len = tile_len; x->max_rows = max_rows;
     const int d = x->d, di = x->di, NS = x->NS, V = x->V, L = x->L;
 
@@ -795,6 +1126,10 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
     TRY_ALLOC(x->mm, max_rows * d);
     TRY_ALLOC(x->logits, max_rows * V);
     TRY_ALLOC(x->stats, max_rows);
+    if (precision != BOA_PREC_F32) {
+        TRY_ALLOC(x->ah, max_rows * std::max(d, di));
+        TRY_ALLOC(x->al, max_rows * std::max(d, di));
+    }
     TRY_ALLOC(x->tokens, (int64_t)max_lanes);
     TRY_ALLOC(x->enc, (int64_t)max_lanes);
     TRY_ALLOC(x->dec, (int64_t)max_lanes);
@@ -810,33 +1145,73 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
     auto take = [&](int64_t n) { const float* p = x->wblob + o; o += n; return p; };
     x->emb = take((int64_t)V * d);
     std::vector<float> aneg_host((size_t)L * di * NS);
+    auto mat = [&](int64_t n) {
+        MatW m;
+        m.f = take(n);
+        m.n = n;
+        return m;
+    };
     for (int l = 0; l < L; ++l) {
         LayerW w;
         w.ln1_w = take(d); w.ln1_b = take(d);
-        w.in_w = take((int64_t)2 * di * d); w.in_b = take(2 * di);
+        w.in_w = mat((int64_t)2 * di * d); w.in_b = take(2 * di);
         w.conv_w = take((int64_t)di * x->DC); w.conv_b = take(di);
-        w.x_w = take((int64_t)(R + 2 * NS) * di);
+        w.x_w = mat((int64_t)(R + 2 * NS) * di);
         w.dt_w = take((int64_t)di * R); w.dt_b = take(di);
         const int64_t a_off = o;
         w.A_log = take((int64_t)di * NS);
         w.D = take(di);
-        w.out_w = take((int64_t)d * di); w.out_b = take(d);
+        w.out_w = mat((int64_t)d * di); w.out_b = take(d);
         w.ln2_w = take(d); w.ln2_b = take(d);
-        w.ff1_w = take((int64_t)4 * d * d); w.ff1_b = take(4 * d);
-        w.ff2_w = take((int64_t)d * 4 * d); w.ff2_b = take(d);
+        w.ff1_w = mat((int64_t)4 * d * d); w.ff1_b = take(4 * d);
+        w.ff2_w = mat((int64_t)d * 4 * d); w.ff2_b = take(d);
         w.Aneg = x->aneg + (int64_t)l * di * NS;
-        for (int64_t i = 0; i < (int64_t)di * NS; ++i)
-            // A = -exp(A_log), stored pre-scaled by log2(e) so that exp(dt * A) = exp2(dt * A2)
-            aneg_host[(size_t)l * di * NS + i] = (float)(-exp((double)hw[a_off + i]) * 1.4426950408889634);
+        // A = -exp(A_log), stored pre-scaled by log2(e) so that exp(dt * A) = exp2(dt * A2); layout [NS/4][di][4]
+        for (int64_t c = 0; c < di; ++c)
+            for (int n = 0; n < NS; ++n)
+                aneg_host[(size_t)l * di * NS + ((size_t)(n / 4) * di + c) * 4 + (n % 4)] =
+                    (float)(-exp((double)hw[a_off + c * NS + n]) * 1.4426950408889634);
         x->layers.push_back(w);
     }
-    x->h1_w = take((int64_t)d * d); x->h1_b = take(d);
-    x->h2_w = take((int64_t)V * d); x->h2_b = take(V);
+    x->h1_w = mat((int64_t)d * d); x->h1_b = take(d);
+    x->h2_w = mat((int64_t)V * d); x->h2_b = take(V);
     if (o != nf) {
         boa_ctx_destroy(x);
         return boa_fail(BOA_ERR_ARG, "internal: weight layout mismatch (%lld vs %lld)", (long long)o, (long long)nf);
     }
+    // split-precision modes: bf16 parts of every GEMM matrix, [hi | lo] per matrix
+    std::vector<uint16_t> split_host;
+    if (x->prec != BOA_PREC_F32) {
+        int64_t total = 0;
+        std::vector<MatW*> mats;
+        for (auto& w : x->layers) { mats.push_back(&w.in_w); mats.push_back(&w.x_w); mats.push_back(&w.out_w);
+                                    mats.push_back(&w.ff1_w); mats.push_back(&w.ff2_w); }
+        mats.push_back(&x->h1_w);
+        mats.push_back(&x->h2_w);
+        for (MatW* m : mats) total += 2 * m->n;
+        if (e == hipSuccess) e = dmalloc(x, &x->wsplit, total);
+        if (e != hipSuccess) {
+            boa_ctx_destroy(x);
+            return boa_fail_hip(e, "boa_ctx_create allocation", __FILE__, __LINE__);
+        }
+        split_host.resize((size_t)total);
+        int64_t so = 0;
+        for (MatW* m : mats) {
+            const float* src = hw + (m->f - x->wblob);
+            uint16_t* hi = split_host.data() + so;
+            uint16_t* lo = hi + m->n;
+            for (int64_t i = 0; i < m->n; ++i) {
+                hi[i] = host_bf16(src[i]);
+                lo[i] = (x->prec == BOA_PREC_BF16X3) ? host_bf16(src[i] - host_bf16_to_f(hi[i])) : (uint16_t)0;
+            }
+            m->h = x->wsplit + so;
+            m->l = (x->prec == BOA_PREC_BF16X3) ? x->wsplit + so + m->n : nullptr;
+            so += 2 * m->n;
+        }
+    }
     e = hipMemcpyAsync(x->wblob, h_weights, (size_t)nbytes, hipMemcpyHostToDevice, x->stream);
+    if (e == hipSuccess && !split_host.empty())
+        e = hipMemcpyAsync(x->wsplit, split_host.data(), split_host.size() * 2, hipMemcpyHostToDevice, x->stream);
     if (e == hipSuccess)
         e = hipMemcpyAsync(x->aneg, aneg_host.data(), aneg_host.size() * 4, hipMemcpyHostToDevice, x->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(x->stream);
@@ -880,20 +1255,60 @@ static void launch_ln_stats(boa_ctx* x, const float* A, int64_t lda, int64_t M) 
              hipLaunchKernelGGL((k_ln_stats<2>), dim3(blocks), dim3(256), 0, x->stream, A, lda, M, x->stats));
 }
 
+// LayerNorm + split into ctx->ah / ctx->al (row stride d).
+static void launch_ln_split(boa_ctx* x, const float* A, int64_t M, const float* w, const float* b) {
+    const unsigned blocks = (unsigned)((M + 3) / 4);
+    const int64_t d = x->d;
+    if (x->d == 256)
+        PROF(PC_LN, 0.0, 8.0 * M * d,
+             hipLaunchKernelGGL((k_ln_split<1>), dim3(blocks), dim3(256), 0, x->stream, A, d, M, w, b, x->ah, x->al));
+    else
+        PROF(PC_LN, 0.0, 8.0 * M * d,
+             hipLaunchKernelGGL((k_ln_split<2>), dim3(blocks), dim3(256), 0, x->stream, A, d, M, w, b, x->ah, x->al));
+}
+
+template <int NS, int R, bool OUTS>
+static void launch_scan(boa_ctx* x, const LayerW& w, float* ssm, int B, int Tc) {
+    const int di = x->di;
+    const size_t lds = sizeof(float) * (size_t)Tc * (R + 2 * NS);
+    const dim3 grid((di + 255) / 256, B);
+    if (Tc == 1)
+        hipLaunchKernelGGL((k_scan_step<NS, R, OUTS>), grid, dim3(256), 0, x->stream, x->xs, x->dbc, R + 2 * NS, x->xz,
+                           (int64_t)2 * di, w.dt_w, w.dt_b, w.Aneg, w.D, ssm, di, x->ah, x->al);
+    else
+        hipLaunchKernelGGL((k_scan<NS, R, OUTS>), grid, dim3(256), lds, x->stream, x->xs, x->dbc, R + 2 * NS, x->xz,
+                           (int64_t)2 * di, w.dt_w, w.dt_b, w.Aneg, w.D, ssm, di, Tc, x->ah, x->al);
+}
+
 // One block of the model over B lanes x Tc positions, in place on ctx->x.
+//   fp32 mode:  LN stats -> in_proj(LN on load) -> conv -> x_proj -> scan (y in place of xs) -> out_proj ->
+//               LN stats -> FF1(LN on load, GELU) into xz -> FF2(+residual) into x
+//   split modes: LN+split -> in_proj -> conv -> x_proj -> scan (y split) -> out_proj -> LN+split ->
+//               FF1(GELU, split output into xz's memory) -> FF2(+residual) into x
 static int run_layer(boa_ctx* x, int l, int B, int Tc) {
     const LayerW& w = x->layers[l];
     const int d = x->d, di = x->di, NS = x->NS, R = x->R;
     const int64_t M = (int64_t)B * Tc;
     hipStream_t s = x->stream;
+    const bool split = x->prec != BOA_PREC_F32;
+    // FF hidden activations (split): two bf16 arrays in the memory of xz (dead after the scan)
+    uint16_t* gh = reinterpret_cast<uint16_t*>(x->xz);
+    uint16_t* gl = gh + M * 4 * d;
     int rc = 0;
     // LN1 + in_proj -> xz [M][2di]
     {
-        launch_ln_stats(x, x->x, d, M);
         GemmArgs g = gemm_args(x->x, d, w.in_w, w.in_b, x->xz, 2 * di, M, 2 * di, d);
-        g.ln_w = w.ln1_w; g.ln_b = w.ln1_b; g.ln_stats = x->stats;
-        PROF(PC_IN, gemm_flops(M, 2 * di, d), gemm_bytes(M, 2 * di, d),
-             rc = (d == 256) ? launch_gemm<1, EPI_BIAS>(g, s) : launch_gemm<2, EPI_BIAS>(g, s));
+        if (split) {
+            launch_ln_split(x, x->x, M, w.ln1_w, w.ln1_b);
+            g.Ah = x->ah; g.Al = x->al;
+            PROF(PC_IN, gemm_flops(M, 2 * di, d), gemm_bytes(M, 2 * di, d),
+                 rc = (launch_gemm_bf<EPI_BIAS, true, false>(g, s)));
+        } else {
+            launch_ln_stats(x, x->x, d, M);
+            g.ln_w = w.ln1_w; g.ln_b = w.ln1_b; g.ln_stats = x->stats;
+            PROF(PC_IN, gemm_flops(M, 2 * di, d), gemm_bytes(M, 2 * di, d),
+                 rc = (d == 256) ? launch_gemm_f32<1, EPI_BIAS>(g, s) : launch_gemm_f32<2, EPI_BIAS>(g, s));
+        }
         if (rc) return rc;
     }
     // conv + SiLU -> xs
@@ -904,54 +1319,62 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc) {
     {
         GemmArgs g = gemm_args(x->xs, di, w.x_w, nullptr, x->dbc, R + 2 * NS, M, R + 2 * NS, di);
         PROF(PC_XPROJ, gemm_flops(M, R + 2 * NS, di), gemm_bytes(M, R + 2 * NS, di),
-             rc = (launch_gemm_cfg<64, 64, 0, EPI_NONE>(g, s)));
+             rc = split ? (launch_gemm_bf_cfg<64, 64, EPI_NONE, false, false>(g, s))
+                        : (launch_gemm_f32_cfg<64, 64, 0, EPI_NONE>(g, s)));
         if (rc) return rc;
     }
-    // dt_proj + softplus + scan + D + gate, y in place of xs
+    // dt_proj + softplus + scan + D + gate: y in place of xs (fp32) or split into ah/al
     {
-        const size_t lds = sizeof(float) * (size_t)Tc * (R + 2 * NS);
         float* ssm = x->ssm + (int64_t)l * x->max_lanes * di * NS;
         const double flops = (double)M * di * (2.0 * R + 6.0 * NS + 8.0);
         const double bytes = 4.0 * ((double)M * (3.0 * di + R + 2 * NS) + 2.0 * B * di * NS);
-        const dim3 grid((di + 255) / 256, B);
-        if (Tc == 1 && R == 16)
-            PROF(PC_SCAN, flops, bytes,
-                 hipLaunchKernelGGL((k_scan_step<16, 16>), grid, dim3(256), 0, s, x->xs, x->dbc, R + 2 * NS, x->xz,
-                                    (int64_t)2 * di, w.dt_w, w.dt_b, w.Aneg, w.D, ssm, di));
-        else if (Tc == 1)
-            PROF(PC_SCAN, flops, bytes,
-                 hipLaunchKernelGGL((k_scan_step<16, 32>), grid, dim3(256), 0, s, x->xs, x->dbc, R + 2 * NS, x->xz,
-                                    (int64_t)2 * di, w.dt_w, w.dt_b, w.Aneg, w.D, ssm, di));
-        else if (R == 16)
-            PROF(PC_SCAN, flops, bytes,
-                 hipLaunchKernelGGL((k_scan<16, 16>), grid, dim3(256), lds, s, x->xs, x->dbc, R + 2 * NS, x->xz,
-                                    (int64_t)2 * di, w.dt_w, w.dt_b, w.Aneg, w.D, ssm, di, Tc));
-        else
-            PROF(PC_SCAN, flops, bytes,
-                 hipLaunchKernelGGL((k_scan<16, 32>), grid, dim3(256), lds, s, x->xs, x->dbc, R + 2 * NS, x->xz,
-                                    (int64_t)2 * di, w.dt_w, w.dt_b, w.Aneg, w.D, ssm, di, Tc));
+        if (R == 16) {
+            if (split) PROF(PC_SCAN, flops, bytes, (launch_scan<16, 16, true>(x, w, ssm, B, Tc)));
+            else PROF(PC_SCAN, flops, bytes, (launch_scan<16, 16, false>(x, w, ssm, B, Tc)));
+        } else {
+            if (split) PROF(PC_SCAN, flops, bytes, (launch_scan<16, 32, true>(x, w, ssm, B, Tc)));
+            else PROF(PC_SCAN, flops, bytes, (launch_scan<16, 32, false>(x, w, ssm, B, Tc)));
+        }
     }
     // out_proj -> mm [M][d]
     {
         GemmArgs g = gemm_args(x->xs, di, w.out_w, w.out_b, x->mm, d, M, d, di);
-        PROF(PC_OUT, gemm_flops(M, d, di), gemm_bytes(M, d, di), rc = (launch_gemm<0, EPI_BIAS>(g, s)));
+        if (split) {
+            g.Ah = x->ah; g.Al = x->al;
+            PROF(PC_OUT, gemm_flops(M, d, di), gemm_bytes(M, d, di), rc = (launch_gemm_bf<EPI_BIAS, true, false>(g, s)));
+        } else {
+            PROF(PC_OUT, gemm_flops(M, d, di), gemm_bytes(M, d, di), rc = (launch_gemm_f32<0, EPI_BIAS>(g, s)));
+        }
         if (rc) return rc;
     }
-    // LN2 + FF1 + GELU -> g [M][4d] (reuses xz)
+    // LN2 + FF1 + GELU -> g [M][4d]
     {
-        launch_ln_stats(x, x->mm, d, M);
         GemmArgs g = gemm_args(x->mm, d, w.ff1_w, w.ff1_b, x->xz, 4 * d, M, 4 * d, d);
-        g.ln_w = w.ln2_w; g.ln_b = w.ln2_b; g.ln_stats = x->stats;
-        PROF(PC_FF1, gemm_flops(M, 4 * d, d), gemm_bytes(M, 4 * d, d),
-             rc = (d == 256) ? launch_gemm<1, EPI_GELU>(g, s) : launch_gemm<2, EPI_GELU>(g, s));
+        if (split) {
+            launch_ln_split(x, x->mm, M, w.ln2_w, w.ln2_b);
+            g.Ah = x->ah; g.Al = x->al; g.Ch = gh; g.Cl = gl;
+            PROF(PC_FF1, gemm_flops(M, 4 * d, d), gemm_bytes(M, 4 * d, d),
+                 rc = (launch_gemm_bf<EPI_GELU, true, true>(g, s)));
+        } else {
+            launch_ln_stats(x, x->mm, d, M);
+            g.ln_w = w.ln2_w; g.ln_b = w.ln2_b; g.ln_stats = x->stats;
+            PROF(PC_FF1, gemm_flops(M, 4 * d, d), gemm_bytes(M, 4 * d, d),
+                 rc = (d == 256) ? launch_gemm_f32<1, EPI_GELU>(g, s) : launch_gemm_f32<2, EPI_GELU>(g, s));
+        }
         if (rc) return rc;
     }
     // FF2 + bias + block residual -> x
     {
         GemmArgs g = gemm_args(x->xz, 4 * d, w.ff2_w, w.ff2_b, x->x, d, M, d, 4 * d);
         g.R = x->x; g.ldr = d;
-        PROF(PC_FF2, gemm_flops(M, d, 4 * d), gemm_bytes(M, d, 4 * d) + 4.0 * M * d,
-             rc = (launch_gemm<0, EPI_RESID>(g, s)));
+        if (split) {
+            g.Ah = gh; g.Al = gl;
+            PROF(PC_FF2, gemm_flops(M, d, 4 * d), gemm_bytes(M, d, 4 * d) + 4.0 * M * d,
+                 rc = (launch_gemm_bf<EPI_RESID, true, false>(g, s)));
+        } else {
+            PROF(PC_FF2, gemm_flops(M, d, 4 * d), gemm_bytes(M, d, 4 * d) + 4.0 * M * d,
+                 rc = (launch_gemm_f32<0, EPI_RESID>(g, s)));
+        }
         if (rc) return rc;
     }
     return BOA_OK;
@@ -961,16 +1384,27 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc) {
 static int run_model(boa_ctx* x, int B, int Tc, float* out) {
     const int d = x->d, V = x->V;
     const int64_t M = (int64_t)B * Tc;
+    const bool split = x->prec != BOA_PREC_F32;
     int rc = 0;
     for (int l = 0; l < x->L; ++l) {
         rc = run_layer(x, l, B, Tc);
         if (rc) return rc;
     }
     GemmArgs g1 = gemm_args(x->x, d, x->h1_w, x->h1_b, x->mm, d, M, d, d);
-    PROF(PC_HEAD1, gemm_flops(M, d, d), gemm_bytes(M, d, d), rc = (launch_gemm<0, EPI_RELU>(g1, x->stream)));
-    if (rc) return rc;
     GemmArgs g2 = gemm_args(x->mm, d, x->h2_w, x->h2_b, out, V, M, V, d);
-    PROF(PC_HEAD2, gemm_flops(M, V, d), gemm_bytes(M, V, d), rc = (launch_gemm<0, EPI_BIAS>(g2, x->stream)));
+    if (split) {
+        g1.Ch = x->ah; g1.Cl = x->al;
+        g2.Ah = x->ah; g2.Al = x->al;
+        PROF(PC_HEAD1, gemm_flops(M, d, d), gemm_bytes(M, d, d),
+             rc = (launch_gemm_bf<EPI_RELU, false, true>(g1, x->stream)));
+        if (rc) return rc;
+        PROF(PC_HEAD2, gemm_flops(M, V, d), gemm_bytes(M, V, d),
+             rc = (launch_gemm_bf<EPI_BIAS, true, false>(g2, x->stream)));
+    } else {
+        PROF(PC_HEAD1, gemm_flops(M, d, d), gemm_bytes(M, d, d), rc = (launch_gemm_f32<0, EPI_RELU>(g1, x->stream)));
+        if (rc) return rc;
+        PROF(PC_HEAD2, gemm_flops(M, V, d), gemm_bytes(M, V, d), rc = (launch_gemm_f32<0, EPI_BIAS>(g2, x->stream)));
+    }
     if (rc) return rc;
     BOA_HIP_TRY(hipGetLastError());
     return BOA_OK;

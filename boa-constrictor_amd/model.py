@@ -26,6 +26,11 @@ __all__ = ["BoaConstrictor", "BoaBytePredictor", "MambaBlock", "Mixer"]
 
 DEFAULT_TILE_LEN = int(os.environ.get("BOA_TILE_LEN", "64"))
 
+# GEMM arithmetic (include/boa_hip.h BOA_PREC_*): "f32" fp32 MFMA, "bf16x3" split-bfloat16 products (default),
+# "bf16w" bfloat16 weight matrices.  Compressor and decompressor must use the same mode.
+PRECISIONS = {"f32": _nat.BOA_PREC_F32, "bf16x3": _nat.BOA_PREC_BF16X3, "bf16w": _nat.BOA_PREC_BF16W}
+DEFAULT_PRECISION = os.environ.get("BOA_PRECISION", "bf16x3")
+
 
 class Mixer(nn.Module):
     """Parameters of one Mamba mixer, named as mamba_ssm.Mamba / mambapy.MambaBlock name them.
@@ -68,15 +73,19 @@ class MambaBlock(nn.Module):
 class _Engine:
     """One libboa_hip model context: device copy of the weights + recurrent state + workspace."""
 
-    def __init__(self, blob: np.ndarray, cfg: _W.Cfg, max_lanes: int, tile_len: int):
+    def __init__(self, blob: np.ndarray, cfg: _W.Cfg, max_lanes: int, tile_len: int,
+                 precision: str = DEFAULT_PRECISION):
         self._lib = _nat.lib()
         self.cfg = cfg
         self.max_lanes = int(max_lanes)
         self.tile_len = int(tile_len)
+        if precision not in PRECISIONS:
+            raise ValueError(f"precision must be one of {sorted(PRECISIONS)}")
+        self.precision = precision
         c = _nat.ModelCfg(cfg.d_model, cfg.n_layers, cfg.vocab, cfg.d_state, cfg.d_conv, cfg.expand, 0)
         h = ctypes.c_void_p()
         blob = np.ascontiguousarray(blob, dtype=np.float32)
-        _nat.check(self._lib.boa_ctx_create(ctypes.byref(c), _nat.ptr(blob), blob.nbytes, _nat.BOA_WEIGHTS_F32,
+        _nat.check(self._lib.boa_ctx_create(ctypes.byref(c), _nat.ptr(blob), blob.nbytes, PRECISIONS[precision],
                                             self.max_lanes, self.tile_len, _nat.stream_ptr(), ctypes.byref(h)))
         self.h = h
 
@@ -121,6 +130,7 @@ class BoaBytePredictor(nn.Module):
         self.blocks = nn.ModuleList([MambaBlock(d_model) for _ in range(num_layers)])
         self.head = nn.Sequential(nn.Linear(d_model, d_model), nn.ReLU(), nn.Linear(d_model, vocab_size))
         self._engines = {}
+        self.precision = DEFAULT_PRECISION
 
     # ---- weights ---------------------------------------------------------------------------------
     @property
@@ -150,12 +160,12 @@ class BoaBytePredictor(nn.Module):
     def engine(self, max_lanes: int, tile_len: int = DEFAULT_TILE_LEN) -> _Engine:
         """Cached context with capacity for max_lanes x tile_len rows (rebuilt when weights change)."""
         self._require_gpu()
-        key = self._weights_key()
+        key = (self._weights_key(), self.precision)
         e = self._engines.get("codec")
         if e is not None and e[0] == key and e[1].max_lanes >= max_lanes and e[1].tile_len >= tile_len:
             return e[1]
         self._engines.pop("codec", None)
-        eng = _Engine(self.weight_blob(), self.cfg, max_lanes, tile_len)
+        eng = _Engine(self.weight_blob(), self.cfg, max_lanes, tile_len, self.precision)
         self._engines["codec"] = (key, eng)
         return eng
 
@@ -191,7 +201,7 @@ class BoaBytePredictor(nn.Module):
     def init_stream(self, max_len: int, batch_size: int = 1, device=None, dtype=None):
         """model.py:103-106 / 120-123: fresh (zero) recurrent state for batch_size lanes."""
         self._require_gpu()
-        eng = _Engine(self.weight_blob(), self.cfg, batch_size, 1)
+        eng = _Engine(self.weight_blob(), self.cfg, batch_size, 1, self.precision)
         eng.reset(batch_size)
         return _Stream(eng, batch_size, max_len)
 

@@ -47,20 +47,29 @@ typedef struct boa_model_cfg {
     int32_t dt_rank;    /* 0 = ceil(d_model / 16) */
 } boa_model_cfg;
 
-#define BOA_WEIGHTS_F32 0   /* flat little-endian float32 blob in convert_boa_weights.py:22-133 order */
-#define BOA_WEIGHTS_BF16 1  /* same order; GEMM weight matrices stored as bfloat16, everything else f32 */
+/* GEMM arithmetic of a context.  The weight blob passed in is always float32
+ * (convert_boa_weights.py:22-133 order).
+ *   BOA_PREC_F32     fp32 MFMA (v_mfma_f32_16x16x4_f32).
+ *   BOA_PREC_BF16X3  activations and weights each split into two bfloat16 parts; three bf16 MFMA products
+ *                    (lo*hi + hi*lo + hi*hi) accumulated in fp32.
+ *   BOA_PREC_BF16W   GEMM weight matrices rounded to bfloat16 (bf16-weight models); activations split as
+ *                    above; two products.
+ * Encoder and decoder must use the same mode: the logits (and so the streams) depend on it.              */
+#define BOA_PREC_F32 0
+#define BOA_PREC_BF16X3 1
+#define BOA_PREC_BF16W 2
 
 typedef struct boa_ctx boa_ctx;
 
 /* Size in bytes of the flat float32 weight blob for cfg (convert_boa_weights.py:22-133 order). */
 int64_t boa_weights_nbytes(const boa_model_cfg* cfg);
 
-/* Creates a model context: uploads the weights (host blob, BOA_WEIGHTS_F32 layout) and allocates the
- * recurrent state and workspace for up to max_lanes chunks processed tile_len positions at a time.
- * Replaces BoaPredictorGPU's constructor + load_weights (boa_gpu.hpp:489-555) and the nvcc-at-import
- * RangeCoderBatch holder's allocations (gpu_range_coder.py:212-236).  weight_dtype selects the device
- * storage of the GEMM weights (BOA_WEIGHTS_F32 or BOA_WEIGHTS_BF16); stream may be NULL.              */
-int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights_f32, int64_t nbytes, int weight_dtype,
+/* Creates a model context: uploads the weights (host float32 blob) and allocates the recurrent state and
+ * workspace for up to max_lanes chunks processed tile_len (1..256) positions at a time.  precision is a
+ * BOA_PREC_* mode; stream may be NULL.  Replaces BoaPredictorGPU's constructor + load_weights
+ * (boa_gpu.hpp:489-555) and the nvcc-at-import RangeCoderBatch holder's allocations
+ * (gpu_range_coder.py:212-236).                                                                        */
+int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights_f32, int64_t nbytes, int precision,
                    int32_t max_lanes, int32_t tile_len, void* stream, boa_ctx** out);
 int boa_ctx_destroy(boa_ctx* ctx);
 /* Bytes of device memory the context holds. */

@@ -33,10 +33,12 @@ def _markov(n, seed=0, alpha=0.1):
     return out
 
 
-def test_round_trip_ragged(gpu):
+@pytest.mark.parametrize("precision", ["f32", "bf16x3", "bf16w"])
+def test_round_trip_ragged(gpu, precision):
     import codec
 
     m, _ = _model(2)
+    m.precision = precision
     rng = np.random.default_rng(1)
     lens = [1, 2, 3, 64, 65, 129, 200, 1, 77]
     chunks = [rng.integers(0, 256, L).astype(np.uint8) for L in lens]

@@ -16,7 +16,18 @@ pytestmark = pytest.mark.gpu
 REL_TOL = 1e-4
 
 
-def _model(n_layers=2, seed=0, d=256):
+GEMM_MATRICES = ("in_proj.weight", "x_proj.weight", "out_proj.weight", "ff.0.weight", "ff.2.weight",
+                 "head.0.weight", "head.2.weight")
+
+
+def bf16_round(a):
+    """Round float32 values to bfloat16 (nearest even), returned as float32."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32)
+
+
+def _model(n_layers=2, seed=0, d=256, precision="bf16x3"):
     from boa_amd import weights as W
 
     import model as M
@@ -24,7 +35,15 @@ def _model(n_layers=2, seed=0, d=256):
     cfg = W.Cfg(d_model=d, n_layers=n_layers)
     blob = W.seeded_blob(cfg, seed)
     m = M.BoaConstrictor(d_model=d, num_layers=n_layers, vocab_size=256).load_blob(blob)
-    ref = model_ref.RefModel(blob, weights_ref.Cfg(d_model=d, n_layers=n_layers))
+    m.precision = precision
+    ref_blob = blob
+    if precision == "bf16w":  # the model's GEMM matrices are bfloat16: the oracle runs with the same values
+        sd = W.unpack(blob.copy(), cfg)
+        for k in sd:
+            if k.endswith(GEMM_MATRICES):
+                sd[k][...] = bf16_round(sd[k])
+        ref_blob = W.pack(sd, cfg)
+    ref = model_ref.RefModel(ref_blob, weights_ref.Cfg(d_model=d, n_layers=n_layers))
     return m, ref
 
 
@@ -32,9 +51,10 @@ def _rel(a, b):
     return float((a - b).abs().max() / b.abs().max())
 
 
+@pytest.mark.parametrize("precision", ["f32", "bf16x3", "bf16w"])
 @pytest.mark.parametrize("n_layers", [1, 8])
-def test_step_logits_vs_oracle(gpu, n_layers):
-    m, ref = _model(n_layers)
+def test_step_logits_vs_oracle(gpu, n_layers, precision):
+    m, ref = _model(n_layers, precision=precision)
     rng = np.random.default_rng(n_layers)
     B, T = 24, 12
     tok = torch.from_numpy(rng.integers(0, 256, (B, T)))
@@ -48,8 +68,9 @@ def test_step_logits_vs_oracle(gpu, n_layers):
         assert err <= REL_TOL, (t, err)
 
 
-def test_forward_vs_oracle_and_step_identity(gpu):
-    m, ref = _model(2)
+@pytest.mark.parametrize("precision", ["f32", "bf16x3", "bf16w"])
+def test_forward_vs_oracle_and_step_identity(gpu, precision):
+    m, ref = _model(2, precision=precision)
     rng = np.random.default_rng(5)
     B, T = 16, 150  # > tile length: several tiles, state carried between them
     tok = torch.from_numpy(rng.integers(0, 256, (B, T)))
@@ -62,10 +83,11 @@ def test_forward_vs_oracle_and_step_identity(gpu):
     assert torch.equal(ls, lf), float((ls - lf).abs().max())
 
 
-def test_tile_length_independence(gpu):
+@pytest.mark.parametrize("precision", ["f32", "bf16x3"])
+def test_tile_length_independence(gpu, precision):
     import model as M
 
-    m, _ = _model(2)
+    m, _ = _model(2, precision=precision)
     rng = np.random.default_rng(6)
     tok = torch.from_numpy(rng.integers(0, 256, (8, 100))).cuda()
     outs = []
