@@ -1,0 +1,117 @@
+"""BOA2 container (boa.py:89-157) on the CPU: closed forms and every host-forceable error path."""
+import hashlib
+import struct
+import zlib
+
+import numpy as np
+import pytest
+
+
+def test_uvarint_known_answers():
+    import boa
+
+    cases = {0: b"\x00", 1: b"\x01", 127: b"\x7f", 128: b"\x80\x01", 300: b"\xac\x02", 2**32: b"\x80\x80\x80\x80\x10"}
+    for v, enc in cases.items():
+        assert boa.uvarint_encode(v) == enc
+        assert boa.uvarint_decode(enc, 0) == (v, len(enc))
+
+
+def test_fingerprint_closed_form():
+    import boa
+
+    class BoaBytePredictor:
+        pass
+
+    f = boa.BoaFile("/dev/null", BoaBytePredictor())
+    assert f._model_fingerprint().hex() == "c257ec9cf5938905c67212f4001ac357"
+    assert f._model_fingerprint() == hashlib.blake2s(b"BoaBytePredictor", digest_size=16).digest()
+
+
+def _write_boa2(path, streams, first, chunk_len, last_len, ulen, fp=b"\x11" * 16, version=1):
+    with open(path, "wb") as f:
+        f.write(b"BOA2" + struct.pack("<IIQIII", version, 0, ulen, chunk_len, len(streams), last_len))
+        f.write(struct.pack("<B", len(fp)) + fp)
+        offs, off = [], 0
+        for s in streams:
+            f.write(s)
+            offs.append(off)
+            off += len(s)
+        import boa
+
+        idx = bytearray(b"IDX1") + bytes(first)
+        prev = 0
+        for o in offs:
+            idx += boa.uvarint_encode(o - prev)
+            prev = o
+        for s in streams:
+            idx += boa.uvarint_encode(len(s))
+        f.write(idx + struct.pack("<I", zlib.crc32(idx) & 0xFFFFFFFF))
+
+
+def test_reader_parses_handmade_file(tmp_path):
+    import boa
+
+    streams = [np.arange(3, dtype="<u4").tobytes(), b"", np.arange(5, dtype="<u4").tobytes()]
+    p = tmp_path / "a.boa"
+    _write_boa2(p, streams, [7, 8, 9], 100, 42, 242)
+    f = boa.BoaFile(str(p), object())
+    f._read_file()
+    assert f.compressed_data == streams
+    assert f.first_bytes == [7, 8, 9]
+    assert f.lengths == [100, 100, 42]
+    assert f.get_metadata() == {"chunk_len": 100, "n_chunks": 3, "last_chunk_len": 42, "uncompressed_len": 242}
+
+
+@pytest.mark.parametrize("mutate,msg", [
+    (lambda b: b"XOA2" + b[4:], "Bad file magic"),
+    (lambda b: b[:4] + struct.pack("<I", 2) + b[8:], "Unsupported version"),
+    (lambda b: b[:-1] + bytes([b[-1] ^ 1]), "Bad index CRC"),
+    (lambda b: b.replace(b"IDX1", b"IDX2"), "Index not found"),
+])
+def test_reader_errors(tmp_path, mutate, msg):
+    import boa
+
+    p = tmp_path / "a.boa"
+    _write_boa2(p, [b"\x01\x00\x00\x00"], [0], 10, 10, 10)
+    p.write_bytes(mutate(p.read_bytes()))
+    with pytest.raises(ValueError, match=msg):
+        boa.BoaFile(str(p), object())._read_file()
+
+
+def test_reader_rejects_out_of_range_payload(tmp_path):
+    import boa
+
+    p = tmp_path / "a.boa"
+    _write_boa2(p, [b"\x01\x00\x00\x00"], [0], 10, 10, 10)
+    raw = bytearray(p.read_bytes())
+    i = raw.rfind(b"IDX1")
+    # lengths uvarint is the byte after first_bytes (1) and offsets (1): set it to 200
+    raw[i + 4 + 1 + 1] = 100
+    idx = bytes(raw[i:-4])
+    raw[-4:] = struct.pack("<I", zlib.crc32(idx) & 0xFFFFFFFF)
+    p.write_bytes(bytes(raw))
+    with pytest.raises(ValueError, match="out of range"):
+        boa.BoaFile(str(p), object())._read_file()
+
+
+def test_chunking_formula():
+    import boa
+
+    ch = boa.BoaFile._chunking
+    assert ch(5000, 0, 7) == (715, 7, 710)        # boa.py:171-172: ceil(n / count)
+    assert ch(5000, 1024, 0) == (1024, 5, 904)
+    assert ch(16, 0, 4) == (4, 4, 4)
+    assert ch(9, 0, 4) == (3, 3, 3)               # would leave an empty 4th chunk: dropped
+    with pytest.raises(ValueError):
+        ch(10, 0, 0)
+
+
+def test_cpu_device_refused():
+    import torch
+
+    import boa
+
+    if torch.cuda.is_available():
+        return
+    with pytest.raises(RuntimeError):
+        boa.BOA("cpu", "/tmp/x.boa", object())
