@@ -1,0 +1,441 @@
+// Fused decompress steps: the whole model for 16 chunk lanes per workgroup, many positions per launch:
+// embedding -> L x (LN1, in_proj, conv, x_proj, dt_proj + selective scan, out_proj, LN2, FF1 + GELU,
+// FF2 + residual) -> head (Linear-ReLU-Linear) -> quantiser + range decoder -> next byte, which is the
+// next step's input without leaving the workgroup.
+//
+// Reference: the per-step loop of codec.py:211-323 (decompress_GPU: model.step on the batch of streams,
+// softmax, Q2 table, coder.decode_step) and of portability_solved_cpp/boa.cpp:556-569 (step_batch +
+// gpu_rc_decode_fused_step_batch), done here without leaving the chip between layers.
+//
+// Design (gfx950): 512 threads (8 waves) own 16 lanes = the M of one v_mfma_f32_16x16x32_bf16 fragment.
+// Activations stay in LDS for the whole step (~116 KB: residual stream, split-bf16 GEMM operand, xz / FF
+// hidden, dt|B|C rows); GEMM weights stream from L2 in fragment-packed blocks (one coalesced 16-byte load
+// per lane per block); the only HBM traffic is the recurrent state (SSM state and the conv history ring)
+// and the step's inputs and outputs.  Lanes are independent, so a workgroup runs its steps without any
+// grid-wide synchronisation; workgroup classes start at fixed offsets (stagger_us) so that at any moment
+// some CUs are in their HBM-bound scan while others stream weights from L2.  GEMM phases: wave w computes output fragments w, w + 8, ...; each
+// output accumulates 32-wide K steps in ascending order, lo*hi, hi*lo, hi*hi per step, exactly as the tiled
+// split-precision GEMM does, and every elementwise phase calls the same device function as the tiled
+// path (model_dev.h).  The logits of a lane are therefore bit-identical to those the compress path
+// computes for the same position, which the decoder depends on.
+#include "model_dev.h"
+#include "model_internal.h"
+
+namespace boa {
+
+namespace {
+
+constexpr int FD = 256;             // d_model
+constexpr int FDI = 512;            // d_inner
+constexpr int FNS = 16;             // d_state
+constexpr int FR = 16;              // dt_rank
+constexpr int FW = FR + 2 * FNS;    // x_proj width (dt | B | C)
+constexpr int ROWS = 16;            // lanes per workgroup
+constexpr int NTHR = 512;
+constexpr int NWAVE = NTHR / 64;
+
+constexpr int LRES = FD + 4;        // fp32 rows of 256 (+4: conflict-free fragment-order writes)
+constexpr int LA = FDI + 8;         // split operand rows, K <= 512 (bf16 elements)
+constexpr int LXZ = 2 * FDI + 4;    // in_proj output rows (fp32)
+constexpr int LH = 4 * FD + 8;      // FF hidden split rows, K = 1024 (bf16 elements)
+constexpr int LH1 = FD + 8;         // head hidden split rows, K = 256
+
+constexpr int SZ_RES = ROWS * LRES * 4;
+constexpr int SZ_A = 2 * ROWS * LA * 2;
+constexpr int SZ_X = (ROWS * LXZ * 4 > 2 * ROWS * LH * 2) ? ROWS * LXZ * 4 : 2 * ROWS * LH * 2;
+constexpr int SZ_DBC = ROWS * FW * 4;
+constexpr int OFF_RES = 0;
+constexpr int OFF_A = OFF_RES + SZ_RES;
+constexpr int OFF_X = OFF_A + SZ_A;
+constexpr int OFF_DBC = OFF_X + SZ_X;
+constexpr int LDS_BYTES = OFF_DBC + SZ_DBC;
+static_assert(LDS_BYTES <= 160 * 1024, "fused step LDS budget");
+static_assert(OFF_A % 16 == 0 && OFF_X % 16 == 0 && OFF_DBC % 16 == 0, "LDS alignment");
+static_assert(ROWS * LRES * 4 <= SZ_A, "logits tile must fit the operand region");
+
+// C[16][16 nfrag] = A[16][K] (split bf16 in LDS, row stride lda) x W^T (fragment-packed), for this wave's
+// fragments f = rot(f0 + wave + 8 j) (j < FPW, f0 + wave + 8 j < nfrag), rot(f) = (f + rot) mod nfrag.  B
+// blocks of D - 1 K steps ahead are in flight (a register ring) while the current step is multiplied: one
+// workgroup per CU streams every weight of the layer from L2, so latency bounds a shallow pipeline.  The
+// rotation (per workgroup) spreads the workgroups of an XCD over different weight blocks at any moment
+// instead of all reading the same L2 lines; it does not change any output (each output fragment still
+// accumulates its K steps in ascending order).  Output column of acc[j]: 16 * frag_of(...) + lane % 16.
+__device__ __forceinline__ int frag_of(int f0, int wave, int j, int nfrag, int rot) {
+    const int f = f0 + wave + 8 * j + rot;
+    return f >= nfrag ? f - nfrag : f;
+}
+
+template <int NT, int FPW, int K, int D>
+__device__ __forceinline__ void mgemm(const uint16_t* sAh, const uint16_t* sAl, int lda,
+                                      const uint16_t* __restrict__ Wp, int f0, int nfrag, int wave, int lane,
+                                      int rot, floatx4 (&acc)[FPW]) {
+    constexpr int BLK = (NT == 3) ? 1024 : 512;
+    constexpr int S = K / 32;
+    const int kq = 8 * (lane >> 4), ar = lane & 15;
+    const int fw = f0 + wave;
+#pragma unroll
+    for (int j = 0; j < FPW; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    uint4 bh[D][FPW], bl[D][FPW];
+    auto load = [&](int s, int slot) {
+#pragma unroll
+        for (int j = 0; j < FPW; ++j) {
+            if (fw + NWAVE * j < nfrag) {
+                const int f = frag_of(f0, wave, j, nfrag, rot);
+                const uint16_t* p = Wp + ((int64_t)f * S + s) * BLK + lane * 8;
+                bh[slot][j] = *reinterpret_cast<const uint4*>(p);
+                if constexpr (NT == 3) bl[slot][j] = *reinterpret_cast<const uint4*>(p + 512);
+            }
+        }
+    };
+#pragma unroll
+    for (int s = 0; s < D - 1; ++s)
+        if (s < S) load(s, s);
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        if (s + D - 1 < S) load(s + D - 1, (s + D - 1) % D);
+        const bf16x8 ah = *reinterpret_cast<const bf16x8*>(sAh + ar * lda + 32 * s + kq);
+        const bf16x8 al = *reinterpret_cast<const bf16x8*>(sAl + ar * lda + 32 * s + kq);
+#pragma unroll
+        for (int j = 0; j < FPW; ++j) {
+            if (fw + NWAVE * j < nfrag) {
+                const bf16x8 h = __builtin_bit_cast(bf16x8, bh[s % D][j]);
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, h, acc[j], 0, 0, 0);
+                if constexpr (NT == 3)
+                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, __builtin_bit_cast(bf16x8, bl[s % D][j]),
+                                                                     acc[j], 0, 0, 0);
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, h, acc[j], 0, 0, 0);
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ void put_split(uint16_t* h, uint16_t* l, int idx, float v) {
+    uint32_t hi, lo;
+    split2(v, hi, lo);
+    h[idx] = (uint16_t)hi;
+    l[idx] = (uint16_t)lo;
+}
+
+// LayerNorm of rows 2*wave, 2*wave + 1 of src (fp32, stride LRES) into the split operand (stride LA).
+__device__ __forceinline__ void ln_rows(const float* src, const float* __restrict__ w, const float* __restrict__ b,
+                                       uint16_t* sAh, uint16_t* sAl, int wave, int lane) {
+    const float4 wv = *reinterpret_cast<const float4*>(w + 4 * lane);
+    const float4 bv = *reinterpret_cast<const float4*>(b + 4 * lane);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int r = 2 * wave + q;
+        const float4 x4 = *reinterpret_cast<const float4*>(src + r * LRES + 4 * lane);
+        const float v[4] = {x4.x, x4.y, x4.z, x4.w};
+        float mu, rs;
+        ln_stats_row<1>(v, mu, rs);
+        const float y[4] = {ln_apply(v[0], mu, rs, wv.x, bv.x), ln_apply(v[1], mu, rs, wv.y, bv.y),
+                            ln_apply(v[2], mu, rs, wv.z, bv.z), ln_apply(v[3], mu, rs, wv.w, bv.w)};
+        uint32_t h[4], l[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) split2(y[j], h[j], l[j]);
+        *reinterpret_cast<uint2*>(sAh + r * LA + 4 * lane) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+        *reinterpret_cast<uint2*>(sAl + r * LA + 4 * lane) = make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
+    }
+}
+
+typedef __attribute__((address_space(4))) const FusedArgs KArgs;
+
+template <int NT>
+__global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
+    __shared__ __attribute__((aligned(16))) unsigned char lds[LDS_BYTES];
+    float* sRes = reinterpret_cast<float*>(lds + OFF_RES);
+    uint16_t* sAh = reinterpret_cast<uint16_t*>(lds + OFF_A);
+    uint16_t* sAl = sAh + ROWS * LA;
+    float* sX = reinterpret_cast<float*>(lds + OFF_X);
+    uint16_t* sHh = reinterpret_cast<uint16_t*>(lds + OFF_X);
+    uint16_t* sHl = sHh + ROWS * LH;
+    float* sDbc = reinterpret_cast<float*>(lds + OFF_DBC);
+    float* sLog = reinterpret_cast<float*>(lds + OFF_A);  // head output (operand region is free by then)
+
+    __shared__ int sTok[ROWS];
+    __shared__ int sMaxLen;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t b0 = (int64_t)blockIdx.x * ROWS;
+    const int nb = (int)((a.B - b0) < ROWS ? (a.B - b0) : ROWS);  // valid lanes of this workgroup
+    const int V = a.V;
+    if (tid < ROWS) sTok[tid] = tid < nb ? a.tokens_in[b0 + tid] : 0;
+    if (tid == 0) {
+        int ml = 0;
+        if (a.decode)
+            for (int r = 0; r < nb; ++r) ml = a.lens[b0 + r] > ml ? a.lens[b0 + r] : ml;
+        sMaxLen = ml;
+        // start offset of this workgroup's class (4 classes, by XCD-local index)
+        if (a.stagger_us > 0) {
+            const uint64_t until = wall_clock64() + (uint64_t)(((blockIdx.x >> 3) & 3) * a.stagger_us) * 100u;
+            while (wall_clock64() < until) __builtin_amdgcn_s_sleep(8);
+        }
+    }
+    __syncthreads();
+    const int m_of = 4 * (lane >> 4);  // first output row of this lane in a fragment
+    const int n_of = lane & 15;        // output column within a fragment
+
+    int p0m3 = a.p0m3;
+#pragma unroll 1
+    for (int step = 0; step < a.nsteps; ++step) {
+    const int t = a.t + step;
+    // Per-workgroup values are re-derived in every step from an opaque copy of the block index, so that
+    // the compiler does not keep dozens of loop-invariant lane addresses live across the whole step.
+    // The kernel arguments are read again through an opaque pointer to the kernarg segment for the
+    // same reason (otherwise every field stays in SGPRs across the loop and spills).
+    int bid = (int)blockIdx.x;
+    __asm__ volatile("" : "+s"(bid));
+    auto kp = (__attribute__((address_space(4))) const char*)__builtin_amdgcn_kernarg_segment_ptr();
+    __asm__ volatile("" : "+s"(kp));
+    KArgs& a = *reinterpret_cast<KArgs*>(kp);
+    const int64_t b0 = (int64_t)bid * ROWS;
+    // fragment rotations: consecutive workgroups of an XCD (blockIdx / 8) start on different weight blocks
+    const int rot64 = ((bid >> 3) & 7) * 8, rot16 = (bid >> 3) & 15;
+    if (a.decode && t >= sMaxLen) break;  // every lane of this workgroup is complete (uniform condition)
+    // embedding (model.py:97): x = E[byte]
+    for (int i = tid; i < ROWS * (FD / 4); i += NTHR) {
+        const int r = i / (FD / 4), c4 = (i % (FD / 4)) * 4;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (r < nb) {
+            int tok = sTok[r];
+            tok = tok < 0 ? 0 : (tok >= V ? V - 1 : tok);
+            v = *reinterpret_cast<const float4*>(a.emb + (int64_t)tok * FD + c4);
+        }
+        *reinterpret_cast<float4*>(sRes + r * LRES + c4) = v;
+    }
+    __syncthreads();
+
+    const int s1 = p0m3 == 2 ? 0 : p0m3 + 1, s2 = p0m3 == 0 ? 2 : p0m3 - 1;
+
+    for (int l = 0; l < a.L; ++l) {
+        const FusedLayer& w = a.layers[l];
+        // ---- LN1 -> split operand
+        ln_rows(sRes, w.ln1_w, w.ln1_b, sAh, sAl, wave, lane);
+        __syncthreads();
+        // ---- in_proj (+bias) -> xz fp32
+#pragma unroll 1
+        for (int f0 = 0; f0 < 2 * FDI / 16; f0 += 4 * NWAVE) {
+            floatx4 acc[4];
+            mgemm<NT, 4, FD, 3>(sAh, sAl, LA, w.in_p, f0, 2 * FDI / 16, wave, lane, rot64, acc);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int n = 16 * frag_of(f0, wave, j, 2 * FDI / 16, rot64) + n_of;
+                const float bias = w.in_b[n];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sX[(m_of + r) * LXZ + n] = epi_value<EPI_BIAS>(acc[j][r], bias);
+            }
+        }
+        __syncthreads();
+        // ---- conv + SiLU (thread = channel): xs fp32 in place of x, split operand for x_proj, history ring
+        {
+            const int c = tid;
+            const float4 cw = *reinterpret_cast<const float4*>(w.conv_w + 4 * c);
+            const float cb = w.conv_b[c];
+            float* hl = a.hist + (int64_t)l * a.max_lanes * 3 * FDI;
+            float h0[ROWS], h1[ROWS], h2[ROWS];
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) {
+                h0[r] = h1[r] = h2[r] = 0.0f;
+                if (r < nb) {
+                    const float* hb = hl + (b0 + r) * 3 * FDI;
+                    h0[r] = hb[p0m3 * FDI + c];
+                    h1[r] = hb[s1 * FDI + c];
+                    h2[r] = hb[s2 * FDI + c];
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) {
+                const float x = sX[r * LXZ + c];
+                const float y = conv_point(cw, cb, h0[r], h1[r], h2[r], x);
+                sX[r * LXZ + c] = y;
+                put_split(sAh, sAl, r * LA + c, y);
+                if (r < nb) hl[(b0 + r) * 3 * FDI + p0m3 * FDI + c] = x;
+            }
+        }
+        __syncthreads();
+        // ---- x_proj -> [dt | B | C] rows
+        if (wave < FW / 16) {
+            floatx4 acc[1];
+            mgemm<NT, 1, FDI, 8>(sAh, sAl, LA, w.x_p, 0, FW / 16, wave, lane, 0, acc);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sDbc[(m_of + r) * FW + 16 * wave + n_of] = acc[0][r];
+        }
+        __syncthreads();
+        // ---- dt_proj + softplus + selective scan + D + gate (thread = channel) -> y split operand
+        {
+            const int c = tid;
+            float av[FNS], wr[FR];
+            const float* Ag = w.Aneg;
+#pragma unroll
+            for (int n = 0; n < FNS; n += 4) {
+                const float4 p = *reinterpret_cast<const float4*>(Ag + ((int64_t)(n / 4) * FDI + c) * 4);
+                av[n] = p.x; av[n + 1] = p.y; av[n + 2] = p.z; av[n + 3] = p.w;
+            }
+#pragma unroll
+            for (int r = 0; r < FR; r += 4) {
+                const float4 q = *reinterpret_cast<const float4*>(w.dt_w + (int64_t)c * FR + r);
+                wr[r] = q.x; wr[r + 1] = q.y; wr[r + 2] = q.z; wr[r + 3] = q.w;
+            }
+            const float bdt = w.dt_b[c], Dc = w.D[c];
+            float* sl = a.ssm + (int64_t)l * a.max_lanes * FDI * FNS + 4 * c;
+            constexpr int PD = 4;  // lanes of state in flight
+            float hr[PD][FNS];
+            auto load_h = [&](int r, float (&h)[FNS]) {
+                if (r < nb) {
+                    const float* hp = sl + (b0 + r) * FDI * FNS;
+#pragma unroll
+                    for (int n = 0; n < FNS; n += 4) {
+                        const float4 q = *reinterpret_cast<const float4*>(hp + (int64_t)(n / 4) * FDI * 4);
+                        h[n] = q.x; h[n + 1] = q.y; h[n + 2] = q.z; h[n + 3] = q.w;
+                    }
+                } else {
+#pragma unroll
+                    for (int n = 0; n < FNS; ++n) h[n] = 0.0f;
+                }
+            };
+#pragma unroll
+            for (int r = 0; r < PD - 1; ++r) load_h(r, hr[r]);
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) {
+                if (r + PD - 1 < ROWS) load_h(r + PD - 1, hr[(r + PD - 1) % PD]);
+                float (&h)[FNS] = hr[r % PD];
+                const float x = sX[r * LXZ + c], z = sX[r * LXZ + FDI + c];
+                const float y = scan_position<FNS, FR>(sDbc + r * FW, wr, bdt, av, Dc, x, z, h);
+                put_split(sAh, sAl, r * LA + c, y);
+                if (r < nb) {
+                    float* hp = sl + (b0 + r) * FDI * FNS;
+#pragma unroll
+                    for (int n = 0; n < FNS; n += 4)
+                        *reinterpret_cast<float4*>(hp + (int64_t)(n / 4) * FDI * 4) =
+                            make_float4(h[n], h[n + 1], h[n + 2], h[n + 3]);
+                }
+            }
+        }
+        __syncthreads();
+        // ---- out_proj (+bias) -> mixer output fp32 (stride LRES, in the xz region)
+        {
+            floatx4 acc[2];
+            mgemm<NT, 2, FDI, 6>(sAh, sAl, LA, w.out_p, 0, FD / 16, wave, lane, rot16, acc);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int n = 16 * frag_of(0, wave, j, FD / 16, rot16) + n_of;
+                const float bias = w.out_b[n];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sX[(m_of + r) * LRES + n] = epi_value<EPI_BIAS>(acc[j][r], bias);
+            }
+        }
+        __syncthreads();
+        // ---- LN2 -> split operand
+        ln_rows(sX, w.ln2_w, w.ln2_b, sAh, sAl, wave, lane);
+        __syncthreads();
+        // ---- FF1 (+bias, GELU) -> hidden split (xz region)
+#pragma unroll 1
+        for (int f0 = 0; f0 < 4 * FD / 16; f0 += 4 * NWAVE) {
+            floatx4 acc[4];
+            mgemm<NT, 4, FD, 3>(sAh, sAl, LA, w.ff1_p, f0, 4 * FD / 16, wave, lane, rot64, acc);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int n = 16 * frag_of(f0, wave, j, 4 * FD / 16, rot64) + n_of;
+                const float bias = w.ff1_b[n];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) put_split(sHh, sHl, (m_of + r) * LH + n, epi_value<EPI_GELU>(acc[j][r], bias));
+            }
+        }
+        __syncthreads();
+        // ---- FF2 (+bias) + block residual -> residual stream
+        {
+            floatx4 acc[2];
+            mgemm<NT, 2, 4 * FD, 6>(sHh, sHl, LH, w.ff2_p, 0, FD / 16, wave, lane, rot16, acc);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int n = 16 * frag_of(0, wave, j, FD / 16, rot16) + n_of;
+                const float bias = w.ff2_b[n];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int idx = (m_of + r) * LRES + n;
+                    sRes[idx] = sRes[idx] + epi_value<EPI_RESID>(acc[j][r], bias);
+                }
+            }
+        }
+        __syncthreads();
+    }
+
+    // ---- head: Linear -> ReLU -> Linear (model.py:95, 101)
+    for (int i = tid; i < ROWS * FD; i += NTHR) {
+        const int r = i / FD, c = i % FD;
+        put_split(sAh, sAl, r * LA + c, sRes[r * LRES + c]);
+    }
+    __syncthreads();
+    uint16_t* sGh = sHh;
+    uint16_t* sGl = sHh + ROWS * LH1;
+    {
+        floatx4 acc[2];
+        mgemm<NT, 2, FD, 6>(sAh, sAl, LA, a.h1_p, 0, FD / 16, wave, lane, rot16, acc);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int n = 16 * frag_of(0, wave, j, FD / 16, rot16) + n_of;
+            const float bias = a.h1_b[n];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) put_split(sGh, sGl, (m_of + r) * LH1 + n, epi_value<EPI_RELU>(acc[j][r], bias));
+        }
+    }
+    __syncthreads();
+    {
+        floatx4 acc[2];
+        mgemm<NT, 2, FD, 6>(sGh, sGl, LH1, a.h2_p, 0, V / 16, wave, lane, 0, acc);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int f = wave + NWAVE * j;
+            if (f < V / 16) {
+                const int n = 16 * f + n_of;
+                const float bias = a.h2_b[n];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sLog[(m_of + r) * LRES + n] = epi_value<EPI_BIAS>(acc[j][r], bias);
+            }
+        }
+    }
+    __syncthreads();
+    if (a.logits) {
+        for (int i = tid; i < ROWS * V; i += NTHR) {
+            const int r = i / V, n = i % V;
+            if (r < nb) a.logits[(b0 + r) * V + n] = sLog[r * LRES + n];
+        }
+    }
+    if (a.decode) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int r = 2 * wave + q;
+            if (r >= nb) continue;
+            const int64_t b = b0 + r;
+            if (t >= a.lens[b]) continue;
+            DecState st = a.dec[b];
+            const int s = decode_row(sLog + r * LRES, V, lane, st, a.payload + a.off[b], a.nwords[b]);
+            if (lane == 0) {
+                a.dec[b] = st;
+                sTok[r] = s;
+                a.out[b * a.out_stride + t] = (uint8_t)s;
+            }
+        }
+    }
+    __syncthreads();  // next step reads sTok, and sLog's region is reused
+    p0m3 = p0m3 == 2 ? 0 : p0m3 + 1;
+    }
+    if (a.decode && tid < nb) a.tokens_out[b0 + tid] = sTok[tid];
+}
+
+}  // namespace
+
+bool fused_step_supported(int d_model, int d_state, int dt_rank, int d_conv, int vocab) {
+    return d_model == FD && d_state == FNS && dt_rank == FR && d_conv == 4 && vocab % 16 == 0 && vocab <= 256;
+}
+
+hipError_t launch_fused_step(const FusedArgs& a, int nt, hipStream_t s) {
+    const dim3 grid((unsigned)((a.B + ROWS - 1) / ROWS));
+    if (nt == 3)
+        hipLaunchKernelGGL(k_fused_step<3>, grid, dim3(NTHR), 0, s, a);
+    else
+        hipLaunchKernelGGL(k_fused_step<2>, grid, dim3(NTHR), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace boa

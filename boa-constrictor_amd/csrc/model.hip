@@ -11,11 +11,13 @@
 //   - the conv and selective-scan kernels run the same per-position code whether the state comes from
 //     registers (previous position in the same tile) or from HBM (previous launch).
 // This is what makes the encoder's and decoder's logits bit-identical.
-#include "boa_common.h"
+#include "model_dev.h"
+#include "model_internal.h"
 
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 #include <algorithm>
 #include <string>
@@ -24,8 +26,6 @@
 #include "../../include/boa_hip.h"
 
 using namespace boa;
-
-typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 // ================================================================================================
 // Errors (thread-local last message)
@@ -66,8 +66,6 @@ extern "C" int boa_is_device_pointer(const void* p) {
 // Within a 16-wide K group, lane group g = lane/16 supplies k = 4g + s to MFMA step s, so each lane reads
 // one float4 per fragment from LDS.  Rows of the LDS tiles are padded to 36 floats (conflict-free b128
 // reads for the 16 rows a quarter-wave touches).
-enum { EPI_NONE = 0, EPI_BIAS = 1, EPI_GELU = 2, EPI_RELU = 3, EPI_RESID = 4 };
-
 struct GemmArgs {
     const float* A;
     int64_t lda;
@@ -93,8 +91,6 @@ struct GemmArgs {
     int ntiles;
     int per_xcd;
 };
-
-__device__ __forceinline__ float gelu_erf(float v) { return (v * 0.5f) * (1.0f + erff(v * 0.70710678118654752f)); }
 
 template <int BM, int BN, int LNV, int EPI>
 __global__ void __launch_bounds__(256, 2) k_gemm(GemmArgs g) {
@@ -134,10 +130,10 @@ __global__ void __launch_bounds__(256, 2) k_gemm(GemmArgs g) {
                     const float mu = st.x, rs = st.y;
                     const float4 w = *reinterpret_cast<const float4*>(g.ln_w + k0 + c);
                     const float4 b = *reinterpret_cast<const float4*>(g.ln_b + k0 + c);
-                    v.x = ((v.x - mu) * rs) * w.x + b.x;
-                    v.y = ((v.y - mu) * rs) * w.y + b.y;
-                    v.z = ((v.z - mu) * rs) * w.z + b.z;
-                    v.w = ((v.w - mu) * rs) * w.w + b.w;
+                    v.x = ln_apply(v.x, mu, rs, w.x, b.x);
+                    v.y = ln_apply(v.y, mu, rs, w.y, b.y);
+                    v.z = ln_apply(v.z, mu, rs, w.z, b.z);
+                    v.w = ln_apply(v.w, mu, rs, w.w, b.w);
                 }
             }
             ra[i] = v;
@@ -216,10 +212,7 @@ __global__ void __launch_bounds__(256, 2) k_gemm(GemmArgs g) {
             for (int r = 0; r < 4; ++r) {
                 const int64_t row = m0 + wm * WM + 16 * i + 4 * (lane >> 4) + r;
                 if (row >= M) continue;
-                float v = acc[i][j][r];
-                if constexpr (EPI != EPI_NONE) v = v + bias;
-                if constexpr (EPI == EPI_GELU) v = gelu_erf(v);
-                if constexpr (EPI == EPI_RELU) v = fmaxf(v, 0.0f);
+                float v = epi_value<EPI>(acc[i][j][r], bias);
                 if constexpr (EPI == EPI_RESID) v = g.R[row * g.ldr + col] + v;
                 g.C[row * g.ldc + col] = v;
             }
@@ -235,22 +228,11 @@ __global__ void __launch_bounds__(256, 2) k_gemm(GemmArgs g) {
 // exact in fp32, so the only losses are the dropped term and fp32 accumulation.  K order per output is
 // fixed (32 per MFMA step, steps ascending), independent of M: the encoder/decoder identity holds as in
 // the fp32 kernel.  LDS rows hold 32 bf16 + 8 pad (80 B: conflict-free b128 fragment reads).
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-
-__device__ __forceinline__ uint32_t bf16_rne(float f) {
-    uint32_t u = __float_as_uint(f);
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return u >> 16;
-}
-
-__device__ __forceinline__ void split2(float f, uint32_t& hi, uint32_t& lo) {
-    hi = bf16_rne(f);
-    lo = bf16_rne(f - __uint_as_float(hi << 16));
-}
-
-template <int BM, int BN, int EPI, int NT, bool ASPLIT, bool OUTS>
-__global__ void __launch_bounds__(256, 2) k_gemm_bf(GemmArgs g) {
-    constexpr int BK = 32, LDK = BK + 8;
+// BK (K per LDS stage, a multiple of 32) changes only data movement: every output still accumulates
+// 32-wide MFMA K steps in ascending order, so results do not depend on BK, BM or BN.
+template <int BM, int BN, int BK, int EPI, int NT, bool ASPLIT, bool OUTS>
+__global__ void __launch_bounds__(256, (BK > 32) ? 1 : 2) k_gemm_bf(GemmArgs g) {
+    constexpr int LDK = BK + 8;
     constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 16, FN = WN / 16;
     constexpr int A_LD = ASPLIT ? BM * BK / 8 / 256 : BM * BK / 4 / 256;  // per thread: 8-bf16 or float4 loads
     constexpr int B_LD = BN * BK / 8 / 256;
@@ -285,7 +267,7 @@ __global__ void __launch_bounds__(256, 2) k_gemm_bf(GemmArgs g) {
 #pragma unroll
             for (int i = 0; i < A_LD; ++i) {
                 const int q = tid + 256 * i;
-                const int r = q >> 2, c = (q & 3) * 8;
+                const int r = q / (BK / 8), c = (q % (BK / 8)) * 8;
                 const int64_t m = m0 + r;
                 const bool ok = m < M;
                 rah4[i] = ok ? *reinterpret_cast<const uint4*>(g.Ah + m * g.lda + k0 + c) : make_uint4(0, 0, 0, 0);
@@ -295,7 +277,7 @@ __global__ void __launch_bounds__(256, 2) k_gemm_bf(GemmArgs g) {
 #pragma unroll
             for (int i = 0; i < A_LD; ++i) {
                 const int q = tid + 256 * i;
-                const int r = q >> 3, c = (q & 7) * 4;
+                const int r = q / (BK / 4), c = (q % (BK / 4)) * 4;
                 const int64_t m = m0 + r;
                 float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
                 if (m < M) v = *reinterpret_cast<const float4*>(g.A + m * g.lda + k0 + c);
@@ -311,7 +293,7 @@ __global__ void __launch_bounds__(256, 2) k_gemm_bf(GemmArgs g) {
 #pragma unroll
         for (int i = 0; i < B_LD; ++i) {
             const int q = tid + 256 * i;
-            const int r = q >> 2, c = (q & 3) * 8;
+            const int r = q / (BK / 8), c = (q % (BK / 8)) * 8;
             const int n = n0 + r;
             const bool ok = n < N;
             rbh[i] = ok ? *reinterpret_cast<const uint4*>(g.Wh + (int64_t)n * K + k0 + c) : make_uint4(0, 0, 0, 0);
@@ -324,11 +306,11 @@ __global__ void __launch_bounds__(256, 2) k_gemm_bf(GemmArgs g) {
         for (int i = 0; i < A_LD; ++i) {
             const int q = tid + 256 * i;
             if constexpr (ASPLIT) {
-                const int off = (q >> 2) * LDK + (q & 3) * 8;
+                const int off = (q / (BK / 8)) * LDK + (q % (BK / 8)) * 8;
                 *reinterpret_cast<uint4*>(&sAh[buf][off]) = rah4[i];
                 *reinterpret_cast<uint4*>(&sAl[buf][off]) = ral4[i];
             } else {
-                const int off = (q >> 3) * LDK + (q & 7) * 4;
+                const int off = (q / (BK / 4)) * LDK + (q % (BK / 4)) * 4;
                 *reinterpret_cast<uint2*>(&sAh[buf][off]) = rah2[i];
                 *reinterpret_cast<uint2*>(&sAl[buf][off]) = ral2[i];
             }
@@ -336,7 +318,7 @@ __global__ void __launch_bounds__(256, 2) k_gemm_bf(GemmArgs g) {
 #pragma unroll
         for (int i = 0; i < B_LD; ++i) {
             const int q = tid + 256 * i;
-            const int off = (q >> 2) * LDK + (q & 3) * 8;
+            const int off = (q / (BK / 8)) * LDK + (q % (BK / 8)) * 8;
             *reinterpret_cast<uint4*>(&sBh[buf][off]) = rbh[i];
             if constexpr (NT == 3) *reinterpret_cast<uint4*>(&sBl[buf][off]) = rbl[i];
         }
@@ -358,26 +340,30 @@ __global__ void __launch_bounds__(256, 2) k_gemm_bf(GemmArgs g) {
     for (int kt = 0; kt < KT; ++kt) {
         const int cur = kt & 1;
         if (kt + 1 < KT) load_tiles((kt + 1) * BK);
-        bf16x8 ah[FM], al[FM], bh[FN], bl[FN];
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
-            ah[i] = *reinterpret_cast<const bf16x8*>(&sAh[cur][(arow + 16 * i) * LDK + kq]);
-            al[i] = *reinterpret_cast<const bf16x8*>(&sAl[cur][(arow + 16 * i) * LDK + kq]);
-        }
+        for (int ks = 0; ks < BK; ks += 32) {
+            bf16x8 ah[FM], al[FM], bh[FN], bl[FN];
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            bh[j] = *reinterpret_cast<const bf16x8*>(&sBh[cur][(brow + 16 * j) * LDK + kq]);
-            if constexpr (NT == 3) bl[j] = *reinterpret_cast<const bf16x8*>(&sBl[cur][(brow + 16 * j) * LDK + kq]);
-        }
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
+            for (int i = 0; i < FM; ++i) {
+                ah[i] = *reinterpret_cast<const bf16x8*>(&sAh[cur][(arow + 16 * i) * LDK + ks + kq]);
+                al[i] = *reinterpret_cast<const bf16x8*>(&sAl[cur][(arow + 16 * i) * LDK + ks + kq]);
+            }
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bh[j], acc[i][j], 0, 0, 0);
+                bh[j] = *reinterpret_cast<const bf16x8*>(&sBh[cur][(brow + 16 * j) * LDK + ks + kq]);
                 if constexpr (NT == 3)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bl[j], acc[i][j], 0, 0, 0);
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bh[j], acc[i][j], 0, 0, 0);
+                    bl[j] = *reinterpret_cast<const bf16x8*>(&sBl[cur][(brow + 16 * j) * LDK + ks + kq]);
             }
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bh[j], acc[i][j], 0, 0, 0);
+                    if constexpr (NT == 3)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bl[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bh[j], acc[i][j], 0, 0, 0);
+                }
+        }
         if (kt + 1 < KT) store_tiles(cur ^ 1);
         __syncthreads();
     }
@@ -394,13 +380,8 @@ __global__ void __launch_bounds__(256, 2) k_gemm_bf(GemmArgs g) {
             float bias = 0.0f;
             if constexpr (EPI != EPI_NONE) bias = (col < N) ? g.bias[col] : 0.0f;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float v = acc[i][j][r];
-                if constexpr (EPI != EPI_NONE) v = v + bias;
-                if constexpr (EPI == EPI_GELU) v = gelu_erf(v);
-                if constexpr (EPI == EPI_RELU) v = fmaxf(v, 0.0f);
-                sC[(wm * WM + 16 * i + 4 * (lane >> 4) + r) * LDC + cl] = v;
-            }
+            for (int r = 0; r < 4; ++r)
+                sC[(wm * WM + 16 * i + 4 * (lane >> 4) + r) * LDC + cl] = epi_value<EPI>(acc[i][j][r], bias);
         }
     __syncthreads();
     constexpr int Q = BN / 4;  // float4 pieces per tile row
@@ -457,21 +438,28 @@ static int launch_gemm_f32(const GemmArgs& g, hipStream_t s) {
     return launch_gemm_f32_cfg<64, 64, LNV, EPI>(g, s);
 }
 
-template <int BM, int BN, int EPI, bool ASPLIT, bool OUTS>
+template <int BM, int BN, int BK, int EPI, bool ASPLIT, bool OUTS>
 static int launch_gemm_bf_cfg(GemmArgs g, hipStream_t s) {
+    if (g.K % BK != 0) return boa_fail(BOA_ERR_ARG, "internal: K=%d not a multiple of BK=%d", g.K, BK);
     int64_t grid;
     tile_grid(g, BM, BN, grid);
     if (g.Wl)
-        hipLaunchKernelGGL((k_gemm_bf<BM, BN, EPI, 3, ASPLIT, OUTS>), dim3((unsigned)grid), dim3(256), 0, s, g);
+        hipLaunchKernelGGL((k_gemm_bf<BM, BN, BK, EPI, 3, ASPLIT, OUTS>), dim3((unsigned)grid), dim3(256), 0, s, g);
     else
-        hipLaunchKernelGGL((k_gemm_bf<BM, BN, EPI, 2, ASPLIT, OUTS>), dim3((unsigned)grid), dim3(256), 0, s, g);
+        hipLaunchKernelGGL((k_gemm_bf<BM, BN, BK, EPI, 2, ASPLIT, OUTS>), dim3((unsigned)grid), dim3(256), 0, s, g);
     return BOA_OK;
 }
 
+// Shape-dependent data movement (results are independent of it, see k_gemm_bf), from a sweep on MI355X:
+//   many tiles (compress, M = lanes x 64):   128x128, BK 32, 2 workgroups per CU
+//   M = 4096, N >= 512 (in_proj, FF1):        64x64,  BK 32
+//   M = 4096, N <= 256 (out_proj, FF2, head): 64x64,  BK 128 (fewer K stages: latency-bound shapes)
 template <int EPI, bool ASPLIT, bool OUTS>
 static int launch_gemm_bf(const GemmArgs& g, hipStream_t s) {
-    if (big_tiles(g)) return launch_gemm_bf_cfg<128, 128, EPI, ASPLIT, OUTS>(g, s);
-    return launch_gemm_bf_cfg<64, 64, EPI, ASPLIT, OUTS>(g, s);
+    const int64_t t128 = ((g.M + 127) / 128) * (int64_t)((g.N + 127) / 128);
+    if (g.N >= 128 && t128 >= 512) return launch_gemm_bf_cfg<128, 128, 32, EPI, ASPLIT, OUTS>(g, s);
+    if (g.N >= 512 || g.K % 128 != 0) return launch_gemm_bf_cfg<64, 64, 32, EPI, ASPLIT, OUTS>(g, s);
+    return launch_gemm_bf_cfg<64, 64, 128, EPI, ASPLIT, OUTS>(g, s);
 }
 
 // ================================================================================================
@@ -492,20 +480,9 @@ __global__ void __launch_bounds__(256) k_ln_stats(const float* __restrict__ A, i
         const float4 q = *reinterpret_cast<const float4*>(row + 256 * i + 4 * lane);
         v[4 * i + 0] = q.x; v[4 * i + 1] = q.y; v[4 * i + 2] = q.z; v[4 * i + 3] = q.w;
     }
-    float s = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4 * LNV; ++i) s = s + v[i];
-    s = wave_sum(s);
-    const float mu = s / (float)(256 * LNV);
-    float sq = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4 * LNV; ++i) {
-        const float d = v[i] - mu;
-        sq = sq + d * d;
-    }
-    sq = wave_sum(sq);
-    const float var = sq / (float)(256 * LNV);
-    if (lane == 0) stats[m] = make_float2(mu, 1.0f / sqrtf(var + 1e-5f));
+    float mu, rs;
+    ln_stats_row<LNV>(v, mu, rs);
+    if (lane == 0) stats[m] = make_float2(mu, rs);
 }
 
 // LayerNorm of a row, written as split bfloat16 parts (hi, lo) for the split-precision GEMMs: the same
@@ -524,27 +501,15 @@ __global__ void __launch_bounds__(256) k_ln_split(const float* __restrict__ A, i
         const float4 q = *reinterpret_cast<const float4*>(row + 256 * i + 4 * lane);
         v[4 * i + 0] = q.x; v[4 * i + 1] = q.y; v[4 * i + 2] = q.z; v[4 * i + 3] = q.w;
     }
-    float s = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4 * LNV; ++i) s = s + v[i];
-    s = wave_sum(s);
-    const float mu = s / (float)(256 * LNV);
-    float sq = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4 * LNV; ++i) {
-        const float d = v[i] - mu;
-        sq = sq + d * d;
-    }
-    sq = wave_sum(sq);
-    const float var = sq / (float)(256 * LNV);
-    const float rs = 1.0f / sqrtf(var + 1e-5f);
+    float mu, rs;
+    ln_stats_row<LNV>(v, mu, rs);
 #pragma unroll
     for (int i = 0; i < LNV; ++i) {
         const int c = 256 * i + 4 * lane;
         const float4 wv = *reinterpret_cast<const float4*>(w + c);
         const float4 bv = *reinterpret_cast<const float4*>(bvec + c);
-        const float y[4] = {((v[4 * i + 0] - mu) * rs) * wv.x + bv.x, ((v[4 * i + 1] - mu) * rs) * wv.y + bv.y,
-                            ((v[4 * i + 2] - mu) * rs) * wv.z + bv.z, ((v[4 * i + 3] - mu) * rs) * wv.w + bv.w};
+        const float y[4] = {ln_apply(v[4 * i + 0], mu, rs, wv.x, bv.x), ln_apply(v[4 * i + 1], mu, rs, wv.y, bv.y),
+                            ln_apply(v[4 * i + 2], mu, rs, wv.z, bv.z), ln_apply(v[4 * i + 3], mu, rs, wv.w, bv.w)};
         uint32_t h[4], l[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) split2(y[j], h[j], l[j]);
@@ -587,31 +552,92 @@ __global__ void __launch_bounds__(256) k_embed_tokens(const int32_t* __restrict_
 
 // ================================================================================================
 // Depthwise causal conv (d_conv = 4) + bias + SiLU, per (lane, channel), sequential over the Tc positions
-// of the launch.  History = the 3 previous x values of the channel, [lane][3][di] in HBM between launches
-// (oldest first, model.py:72 / App. A: xc = b + w0*x[t-3] + w1*x[t-2] + w2*x[t-1] + w3*x[t]).
+// of the launch (conv_point).  History = the 3 previous x values of the channel, [lane][3][di] in HBM
+// between launches, as a ring: the input of absolute position p lives in slot p % 3, so the history of
+// position p0 is slots p0 % 3 (x[p0-3]), (p0+1) % 3 (x[p0-2]), (p0+2) % 3 (x[p0-1]) and a one-position
+// launch rewrites one slot only.  p0m3 = p0 % 3.
 __global__ void __launch_bounds__(256) k_conv_silu(const float* __restrict__ xz, int64_t ldxz,
                                                   float* __restrict__ hist, const float* __restrict__ w,
                                                   const float* __restrict__ bias, float* __restrict__ xs,
-                                                  int di, int Tc) {
+                                                  int di, int Tc, int p0m3) {
     const int c = blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t b = blockIdx.y;
     if (c >= di) return;
     float* hb = hist + b * 3 * di;
-    float h0 = hb[c], h1 = hb[di + c], h2 = hb[2 * di + c];
+    const int s1 = p0m3 == 2 ? 0 : p0m3 + 1, s2 = p0m3 == 0 ? 2 : p0m3 - 1;
+    float h0 = hb[p0m3 * di + c], h1 = hb[s1 * di + c], h2 = hb[s2 * di + c];
     const float4 wv = *reinterpret_cast<const float4*>(w + 4 * c);
     const float bb = bias[c];
     for (int t = 0; t < Tc; ++t) {
         const int64_t m = b * Tc + t;
         const float x = xz[m * ldxz + c];
-        float v = bb;
-        v = v + wv.x * h0;
-        v = v + wv.y * h1;
-        v = v + wv.z * h2;
-        v = v + wv.w * x;
-        xs[m * di + c] = v / (1.0f + expf(-v));
+        xs[m * di + c] = conv_point(wv, bb, h0, h1, h2, x);
         h0 = h1; h1 = h2; h2 = x;
     }
-    hb[c] = h0; hb[di + c] = h1; hb[2 * di + c] = h2;
+    // h0, h1, h2 = inputs of positions p0+Tc-3 .. p0+Tc-1 (or older history, rewritten unchanged)
+    const int e0 = (p0m3 + Tc) % 3, e1 = (e0 + 1) % 3, e2 = (e0 + 2) % 3;
+    hb[e0 * di + c] = h0; hb[e1 * di + c] = h1; hb[e2 * di + c] = h2;
+}
+
+// ================================================================================================
+// Decompress-step fusion of the conv + SiLU and x_proj (split-precision modes): one workgroup owns 16 lanes.
+//   phase 1: conv_point for one position, x into LDS (and to xs for the scan), one history slot rewritten;
+//   phase 2: x_proj on v_mfma_f32_16x16x32_bf16 with A split from LDS exactly as k_gemm_bf splits fp32 A
+//            on load, the same product order (lo*hi, hi*lo, hi*hi) and ascending 32-wide K steps, one wave
+//            per 16-column output fragment, so every output equals the standalone GEMM's bit for bit.
+template <int NT>
+__global__ void __launch_bounds__(256) k_convx_step(const float* __restrict__ xz, int64_t ldxz, float* __restrict__ hist,
+                                                   const float* __restrict__ w, const float* __restrict__ bias,
+                                                   float* __restrict__ xs, const uint16_t* __restrict__ Wh,
+                                                   const uint16_t* __restrict__ Wl, float* __restrict__ dbc, int ldd,
+                                                   int di, int B, int p0m3) {
+    extern __shared__ float sX[];  // [16][di + 4]
+    const int LDX = di + 4;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t b0 = (int64_t)blockIdx.x * 16;
+    const int s1 = p0m3 == 2 ? 0 : p0m3 + 1, s2 = p0m3 == 0 ? 2 : p0m3 - 1;
+    for (int c = tid; c < di; c += 256) {
+        const float4 wv = *reinterpret_cast<const float4*>(w + 4 * c);
+        const float bb = bias[c];
+#pragma unroll 4
+        for (int r = 0; r < 16; ++r) {
+            const int64_t b = b0 + r;
+            if (b >= B) break;
+            float* hb = hist + b * 3 * di;
+            const float x = xz[b * ldxz + c];
+            const float y = conv_point(wv, bb, hb[p0m3 * di + c], hb[s1 * di + c], hb[s2 * di + c], x);
+            xs[b * di + c] = y;
+            sX[r * LDX + c] = y;
+            hb[p0m3 * di + c] = x;
+        }
+    }
+    __syncthreads();
+    if (wave * 16 >= ldd) return;  // ldd = r + 2N output columns: 48 (d 256) or 64 (d 512)
+    const int i = lane & 15, kq = 8 * (lane >> 4);
+    const int n = wave * 16 + i;
+    floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < di; k0 += 32) {
+        const float* xa = &sX[i * LDX + k0 + kq];
+        uint32_t hh[8], ll[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) split2(xa[e], hh[e], ll[e]);
+        const uint4 ah4 = make_uint4(hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16), hh[4] | (hh[5] << 16), hh[6] | (hh[7] << 16));
+        const uint4 al4 = make_uint4(ll[0] | (ll[1] << 16), ll[2] | (ll[3] << 16), ll[4] | (ll[5] << 16), ll[6] | (ll[7] << 16));
+        const bf16x8 ah = __builtin_bit_cast(bf16x8, ah4);
+        const bf16x8 al = __builtin_bit_cast(bf16x8, al4);
+        const bf16x8 bh = *reinterpret_cast<const bf16x8*>(Wh + (int64_t)n * di + k0 + kq);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
+        if constexpr (NT == 3) {
+            const bf16x8 bl = *reinterpret_cast<const bf16x8*>(Wl + (int64_t)n * di + k0 + kq);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
+        }
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int64_t b = b0 + 4 * (lane >> 4) + r;
+        if (b < B) dbc[b * ldd + wave * 16 + (lane & 15)] = acc[r];
+    }
 }
 
 // ================================================================================================
@@ -623,27 +649,7 @@ __global__ void __launch_bounds__(256) k_conv_silu(const float* __restrict__ xz,
 // One thread per (lane, channel), h[16] in registers across the Tc positions; the [dr | B | C] rows of the
 // lane's positions are staged in LDS (uniform across the workgroup).  State [lane][di][NS] in HBM between
 // launches.  y overwrites x in place.
-// One position of one channel: the arithmetic shared by the tile kernel and the step kernel (this shared
-// function is what makes the two produce identical bits).  row = [dr (R) | B (NS) | C (NS)] of the position.
-template <int NS, int R>
-__device__ __forceinline__ float scan_position(const float* row, const float (&wr)[R], float bdt, const float (&a)[NS],
-                                               float Dc, float x, float z, float (&h)[NS]) {
-    float dt = 0.0f;
-#pragma unroll
-    for (int r = 0; r < R; ++r) dt = dt + row[r] * wr[r];
-    dt = dt + bdt;
-    dt = (dt > 20.0f) ? dt : log1pf(expf(dt));
-    float y = 0.0f;
-#pragma unroll
-    for (int n = 0; n < NS; ++n) {
-        const float dA = exp2f(dt * a[n]);
-        const float dBx = (dt * row[R + n]) * x;
-        h[n] = dA * h[n] + dBx;
-        y = y + h[n] * row[R + NS + n];
-    }
-    y = y + Dc * x;
-    return y * (z / (1.0f + expf(-z)));
-}
+// The per-position arithmetic is scan_position (shared with the fused decompress-step kernel).
 
 template <int NS, int R>
 __device__ __forceinline__ void scan_load_channel(int c, int di, const float* hp, const float* Aneg, const float* dt_w,
@@ -742,8 +748,6 @@ __global__ void __launch_bounds__(256) k_scan_step(float* __restrict__ xs_y, con
 
 // ================================================================================================
 // Fused coder kernels (quantiser XQ at PRECISION 24), one wavefront per chunk lane.
-static constexpr int CODER_P = 24;
-
 __global__ void k_enc_init(EncState* st, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) enc_init(st[i]);
@@ -778,16 +782,8 @@ __global__ void __launch_bounds__(64) k_encode_tile(const float* __restrict__ lo
         if (p + 1 >= L) break;
         const int s = src[p + 1];
         if (s >= V) continue;  // as gpu_range_coder.py:97: symbols outside [0, K) are skipped
-        const float* row = logits + (b * Tc + t) * V;
-        float4 l4 = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (4 * lane + 3 < V) l4 = *reinterpret_cast<const float4*>(row + 4 * lane);
-        else {
-            if (4 * lane + 0 < V) l4.x = row[4 * lane + 0];
-            if (4 * lane + 1 < V) l4.y = row[4 * lane + 1];
-            if (4 * lane + 2 < V) l4.z = row[4 * lane + 2];
-        }
         XQ q;
-        xq_build(q, l4, lane, V, CODER_P);
+        xq_build(q, logits_row4(logits + (b * Tc + t) * V, V, lane), lane, V, CODER_P);
         uint32_t c_s, f_s;
         xq_sym(q, s, c_s, f_s);
         const uint32_t lo = xq_cdf_at(q, c_s, s);
@@ -833,30 +829,7 @@ __global__ void __launch_bounds__(64) k_decode_step(const float* __restrict__ lo
     const int lane = threadIdx.x;
     if (t >= lens[b]) return;
     DecState st = states[b];
-    const uint32_t* in = payload + off[b];
-    const int32_t nw = nwords[b];
-    const float* row = logits + b * V;
-    float4 l4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (4 * lane + 3 < V) l4 = *reinterpret_cast<const float4*>(row + 4 * lane);
-    else {
-        if (4 * lane + 0 < V) l4.x = row[4 * lane + 0];
-        if (4 * lane + 1 < V) l4.y = row[4 * lane + 1];
-        if (4 * lane + 2 < V) l4.z = row[4 * lane + 2];
-    }
-    XQ q;
-    xq_build(q, l4, lane, V, CODER_P);
-    uint32_t e[4];
-    uint32_t c = q.base;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int k = 4 * lane + j;
-        e[j] = (k < V) ? xq_cdf_at(q, c, k) : (1u << CODER_P);
-        c += q.f[j];
-    }
-    const uint32_t qv = dec_target(st, CODER_P);
-    uint32_t lo, hi;
-    const int s = wave_find_symbol<CODER_P>(e, V, qv, lane, lo, hi);
-    dec_advance(st, CODER_P, lo, hi - lo, in, nw);
+    const int s = decode_row(logits + b * V, V, lane, st, payload + off[b], nwords[b]);
     if (lane == 0) {
         states[b] = st;
         tokens[b] = s;
@@ -885,7 +858,9 @@ struct MatW {
     const float* f = nullptr;
     const uint16_t* h = nullptr;
     const uint16_t* l = nullptr;
+    const uint16_t* p = nullptr;  // fragment-packed parts (fused step kernel)
     int64_t n = 0;
+    int N = 0, K = 0;
 };
 
 struct LayerW {
@@ -907,12 +882,12 @@ static GemmArgs gemm_args(const float* A, int64_t lda, const MatW& W, const floa
 // Per-kernel-class event timing (boa_profile / boa_profile_read).
 enum ProfClass {
     PC_EMBED, PC_IN, PC_CONV, PC_XPROJ, PC_SCAN, PC_OUT, PC_FF1, PC_FF2, PC_HEAD1, PC_HEAD2, PC_ENCODE, PC_DECODE,
-    PC_LN, PC_COUNT
+    PC_LN, PC_FUSED, PC_COUNT
 };
 static const char* kProfNames[PC_COUNT] = {"embed",    "gemm_in_proj", "conv",     "gemm_x_proj",
                                            "scan",     "gemm_out_proj", "gemm_ff1", "gemm_ff2",
                                            "gemm_head1", "gemm_head2", "encode",   "decode",
-                                           "ln_stats"};
+                                           "ln_stats", "fused_step"};
 struct ProfClassState {
     int64_t launches = 0;
     int64_t used = 0;
@@ -942,6 +917,12 @@ struct boa_ctx {
     EncState* enc = nullptr;
     DecState* dec = nullptr;
     int32_t* flag = nullptr;
+    int64_t pos = 0;                   // positions processed since the last state reset (conv history ring)
+    bool fused = false;                // decompress / step through k_fused_step
+    int fused_steps = 64;              // decode steps per k_fused_step launch
+    int stagger_us = 25;               // start offset between the fused kernel's workgroup classes
+    uint16_t* wfrag = nullptr;         // fragment-packed GEMM weights (fused)
+    FusedLayer* d_layers = nullptr;    // per-layer pointer table (fused)
     int64_t device_bytes = 0;
     bool prof_on = false;
     ProfClassState prof[PC_COUNT];
@@ -1055,7 +1036,7 @@ extern "C" int boa_ctx_destroy(boa_ctx* ctx) {
     else (void)hipDeviceSynchronize();
     void* ptrs[] = {ctx->wblob, ctx->aneg, ctx->conv_hist, ctx->ssm, ctx->x, ctx->xz, ctx->xs, ctx->dbc,
                     ctx->mm, ctx->logits, ctx->stats, ctx->tokens, ctx->enc, ctx->dec, ctx->flag, ctx->wsplit,
-                    ctx->ah, ctx->al};
+                    ctx->ah, ctx->al, ctx->wfrag, ctx->d_layers};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     for (auto& p : ctx->prof)
@@ -1084,6 +1065,21 @@ static float host_bf16_to_f(uint16_t h) {
     float f;
     memcpy(&f, &u, 4);
     return f;
+}
+
+// Fragment order for the fused kernel's B operands (layout in model_internal.h).
+static void pack_fragments(const uint16_t* hi, const uint16_t* lo, int N, int K, bool two, uint16_t* out) {
+    const int S = K / 32, blk = two ? 1024 : 512;
+    for (int f = 0; f < N / 16; ++f)
+        for (int s = 0; s < S; ++s) {
+            uint16_t* o = out + ((int64_t)f * S + s) * blk;
+            for (int l = 0; l < 64; ++l)
+                for (int j = 0; j < 8; ++j) {
+                    const int64_t src = (int64_t)(16 * f + (l & 15)) * K + 32 * s + 8 * (l >> 4) + j;
+                    o[l * 8 + j] = hi[src];
+                    if (two) o[512 + l * 8 + j] = lo[src];
+                }
+        }
 }
 
 extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, int64_t nbytes, int precision,
@@ -1145,26 +1141,28 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
     auto take = [&](int64_t n) { const float* p = x->wblob + o; o += n; return p; };
     x->emb = take((int64_t)V * d);
     std::vector<float> aneg_host((size_t)L * di * NS);
-    auto mat = [&](int64_t n) {
+    auto mat = [&](int N, int K) {
         MatW m;
-        m.f = take(n);
-        m.n = n;
+        m.n = (int64_t)N * K;
+        m.f = take(m.n);
+        m.N = N;
+        m.K = K;
         return m;
     };
     for (int l = 0; l < L; ++l) {
         LayerW w;
         w.ln1_w = take(d); w.ln1_b = take(d);
-        w.in_w = mat((int64_t)2 * di * d); w.in_b = take(2 * di);
+        w.in_w = mat(2 * di, d); w.in_b = take(2 * di);
         w.conv_w = take((int64_t)di * x->DC); w.conv_b = take(di);
-        w.x_w = mat((int64_t)(R + 2 * NS) * di);
+        w.x_w = mat(R + 2 * NS, di);
         w.dt_w = take((int64_t)di * R); w.dt_b = take(di);
         const int64_t a_off = o;
         w.A_log = take((int64_t)di * NS);
         w.D = take(di);
-        w.out_w = mat((int64_t)d * di); w.out_b = take(d);
+        w.out_w = mat(d, di); w.out_b = take(d);
         w.ln2_w = take(d); w.ln2_b = take(d);
-        w.ff1_w = mat((int64_t)4 * d * d); w.ff1_b = take(4 * d);
-        w.ff2_w = mat((int64_t)d * 4 * d); w.ff2_b = take(d);
+        w.ff1_w = mat(4 * d, d); w.ff1_b = take(4 * d);
+        w.ff2_w = mat(d, 4 * d); w.ff2_b = take(d);
         w.Aneg = x->aneg + (int64_t)l * di * NS;
         // A = -exp(A_log), stored pre-scaled by log2(e) so that exp(dt * A) = exp2(dt * A2); layout [NS/4][di][4]
         for (int64_t c = 0; c < di; ++c)
@@ -1173,14 +1171,15 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
                     (float)(-exp((double)hw[a_off + c * NS + n]) * 1.4426950408889634);
         x->layers.push_back(w);
     }
-    x->h1_w = mat((int64_t)d * d); x->h1_b = take(d);
-    x->h2_w = mat((int64_t)V * d); x->h2_b = take(V);
+    x->h1_w = mat(d, d); x->h1_b = take(d);
+    x->h2_w = mat(V, d); x->h2_b = take(V);
     if (o != nf) {
         boa_ctx_destroy(x);
         return boa_fail(BOA_ERR_ARG, "internal: weight layout mismatch (%lld vs %lld)", (long long)o, (long long)nf);
     }
     // split-precision modes: bf16 parts of every GEMM matrix, [hi | lo] per matrix
-    std::vector<uint16_t> split_host;
+    std::vector<uint16_t> split_host, frag_host;
+    std::vector<FusedLayer> layers_host;
     if (x->prec != BOA_PREC_F32) {
         int64_t total = 0;
         std::vector<MatW*> mats;
@@ -1208,10 +1207,48 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
             m->l = (x->prec == BOA_PREC_BF16X3) ? x->wsplit + so + m->n : nullptr;
             so += 2 * m->n;
         }
+        const char* fenv = getenv("BOA_FUSED_STEP");
+        x->fused = fused_step_supported(d, NS, R, x->DC, V) && !(fenv && fenv[0] == '0');
+        if (const char* v = getenv("BOA_FUSED_STEPS_PER_LAUNCH")) x->fused_steps = std::max(1, atoi(v));
+        if (const char* v = getenv("BOA_FUSED_STAGGER_US")) x->stagger_us = std::max(0, atoi(v));
+        if (x->fused) {
+            const bool two = x->prec == BOA_PREC_BF16X3;
+            int64_t ftotal = 0;
+            for (MatW* m : mats) ftotal += (two ? 2 : 1) * m->n;
+            frag_host.resize((size_t)ftotal);
+            if (e == hipSuccess) e = dmalloc(x, &x->wfrag, ftotal);
+            if (e == hipSuccess) e = dmalloc(x, &x->d_layers, (int64_t)L);
+            if (e != hipSuccess) {
+                boa_ctx_destroy(x);
+                return boa_fail_hip(e, "boa_ctx_create allocation", __FILE__, __LINE__);
+            }
+            int64_t fo = 0, hs = 0;
+            for (MatW* m : mats) {
+                const uint16_t* hi = split_host.data() + hs;
+                pack_fragments(hi, hi + m->n, m->N, m->K, two, frag_host.data() + fo);
+                m->p = x->wfrag + fo;
+                fo += (two ? 2 : 1) * m->n;
+                hs += 2 * m->n;
+            }
+            layers_host.resize((size_t)L);
+            for (int l = 0; l < L; ++l) {
+                const LayerW& w = x->layers[l];
+                FusedLayer& f = layers_host[(size_t)l];
+                f.ln1_w = w.ln1_w; f.ln1_b = w.ln1_b; f.in_b = w.in_b; f.conv_w = w.conv_w; f.conv_b = w.conv_b;
+                f.dt_w = w.dt_w; f.dt_b = w.dt_b; f.Aneg = w.Aneg; f.D = w.D; f.out_b = w.out_b;
+                f.ln2_w = w.ln2_w; f.ln2_b = w.ln2_b; f.ff1_b = w.ff1_b; f.ff2_b = w.ff2_b;
+                f.in_p = w.in_w.p; f.x_p = w.x_w.p; f.out_p = w.out_w.p; f.ff1_p = w.ff1_w.p; f.ff2_p = w.ff2_w.p;
+            }
+        }
     }
     e = hipMemcpyAsync(x->wblob, h_weights, (size_t)nbytes, hipMemcpyHostToDevice, x->stream);
     if (e == hipSuccess && !split_host.empty())
         e = hipMemcpyAsync(x->wsplit, split_host.data(), split_host.size() * 2, hipMemcpyHostToDevice, x->stream);
+    if (e == hipSuccess && !frag_host.empty())
+        e = hipMemcpyAsync(x->wfrag, frag_host.data(), frag_host.size() * 2, hipMemcpyHostToDevice, x->stream);
+    if (e == hipSuccess && !layers_host.empty())
+        e = hipMemcpyAsync(x->d_layers, layers_host.data(), layers_host.size() * sizeof(FusedLayer),
+                           hipMemcpyHostToDevice, x->stream);
     if (e == hipSuccess)
         e = hipMemcpyAsync(x->aneg, aneg_host.data(), aneg_host.size() * 4, hipMemcpyHostToDevice, x->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(x->stream);
@@ -1225,6 +1262,7 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
 
 extern "C" int boa_state_reset(boa_ctx* x, int32_t lanes) {
     if (!x || lanes < 0 || lanes > x->max_lanes) return boa_fail(BOA_ERR_ARG, "boa_state_reset: bad lanes");
+    x->pos = 0;
     for (int l = 0; l < x->L; ++l) {
         BOA_HIP_TRY(hipMemsetAsync(x->conv_hist + (int64_t)l * x->max_lanes * 3 * x->di, 0,
                                    sizeof(float) * (size_t)lanes * 3 * x->di, x->stream));
@@ -1311,17 +1349,35 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc) {
         }
         if (rc) return rc;
     }
+    float* hist = x->conv_hist + (int64_t)l * x->max_lanes * 3 * di;
+    if (split && Tc == 1) {
+        // decompress step: conv + SiLU + x_proj in one kernel (same arithmetic as the two kernels below)
+        const size_t lds = sizeof(float) * 16 * (size_t)(di + 4);
+        const double flops = 8.0 * M * di + gemm_flops(M, R + 2 * NS, di);
+        const double bytes = 4.0 * (3.0 * M * di + 6.0 * B * di + M * (R + 2 * NS));
+        if (w.x_w.l)
+            PROF(PC_CONV, flops, bytes,
+                 hipLaunchKernelGGL((k_convx_step<3>), dim3((B + 15) / 16), dim3(256), lds, s, x->xz, (int64_t)2 * di,
+                                    hist, w.conv_w, w.conv_b, x->xs, w.x_w.h, w.x_w.l, x->dbc, R + 2 * NS, di, B,
+                                    (int)(x->pos % 3)));
+        else
+            PROF(PC_CONV, flops, bytes,
+                 hipLaunchKernelGGL((k_convx_step<2>), dim3((B + 15) / 16), dim3(256), lds, s, x->xz, (int64_t)2 * di,
+                                    hist, w.conv_w, w.conv_b, x->xs, w.x_w.h, w.x_w.l, x->dbc, R + 2 * NS, di, B,
+                                    (int)(x->pos % 3)));
+    } else {
     // conv + SiLU -> xs
     PROF(PC_CONV, 8.0 * M * di, 4.0 * (2.0 * M * di + 6.0 * B * di),
          hipLaunchKernelGGL(k_conv_silu, dim3((di + 255) / 256, B), dim3(256), 0, s, x->xz, (int64_t)2 * di,
-                            x->conv_hist + (int64_t)l * x->max_lanes * 3 * di, w.conv_w, w.conv_b, x->xs, di, Tc));
+                            hist, w.conv_w, w.conv_b, x->xs, di, Tc, (int)(x->pos % 3)));
     // x_proj -> dbc [M][R+2NS]
     {
         GemmArgs g = gemm_args(x->xs, di, w.x_w, nullptr, x->dbc, R + 2 * NS, M, R + 2 * NS, di);
         PROF(PC_XPROJ, gemm_flops(M, R + 2 * NS, di), gemm_bytes(M, R + 2 * NS, di),
-             rc = split ? (launch_gemm_bf_cfg<64, 64, EPI_NONE, false, false>(g, s))
+             rc = split ? (launch_gemm_bf<EPI_NONE, false, false>(g, s))
                         : (launch_gemm_f32_cfg<64, 64, 0, EPI_NONE>(g, s)));
         if (rc) return rc;
+    }
     }
     // dt_proj + softplus + scan + D + gate: y in place of xs (fp32) or split into ah/al
     {
@@ -1418,11 +1474,57 @@ static void launch_embed_tokens(boa_ctx* x, const int32_t* tokens, int64_t tok_s
                             Tc, rows, x->emb, x->d, x->V, x->x));
 }
 
+// Arguments of one k_fused_step launch at the context's current position (logits and decode fields are
+// filled in by the caller).
+static FusedArgs fused_args(boa_ctx* x, int32_t lanes, const int32_t* tokens_in) {
+    FusedArgs a;
+    memset(&a, 0, sizeof(a));
+    a.layers = x->d_layers; a.L = x->L; a.V = x->V; a.B = lanes; a.p0m3 = (int)(x->pos % 3);
+    a.max_lanes = x->max_lanes;
+    a.emb = x->emb; a.h1_b = x->h1_b; a.h2_b = x->h2_b; a.h1_p = x->h1_w.p; a.h2_p = x->h2_w.p;
+    a.ssm = x->ssm; a.hist = x->conv_hist; a.tokens_in = tokens_in;
+    a.nsteps = 1;
+    return a;
+}
+
+// Compulsory HBM bytes of one fused step: SSM state read + write, conv history (3 reads, 1 write), input
+// embedding rows, per-lane coder state and bytes, plus the packed weights once.
+static double fused_bytes(const boa_ctx* x, int32_t lanes) {
+    const double per_lane_layer = 2.0 * x->di * x->NS * 4 + 4.0 * x->di * 4;
+    double wbytes = 0.0;
+    for (const auto& w : x->layers)
+        wbytes += 2.0 * (double)(w.in_w.n + w.x_w.n + w.out_w.n + w.ff1_w.n + w.ff2_w.n);
+    wbytes += 2.0 * (double)(x->h1_w.n + x->h2_w.n);
+    if (x->prec == BOA_PREC_BF16X3) wbytes *= 2.0;
+    return (double)lanes * (x->L * per_lane_layer + 4.0 * x->d + 64.0) + wbytes;
+}
+
+static double fused_flops(const boa_ctx* x, int32_t lanes) {
+    double params = 0.0;
+    for (const auto& w : x->layers)
+        params += (double)(w.in_w.n + w.x_w.n + w.out_w.n + w.ff1_w.n + w.ff2_w.n);
+    params += (double)(x->h1_w.n + x->h2_w.n);
+    const double scan = (double)x->L * x->di * (2.0 * x->R + 6.0 * x->NS + 8.0);
+    return (double)lanes * (2.0 * params + scan);
+}
+
 extern "C" int boa_model_step(boa_ctx* x, const int32_t* d_tokens, int32_t lanes, float* d_logits) {
     if (!x || !d_tokens || !d_logits || lanes < 1 || lanes > x->max_lanes)
         return boa_fail(BOA_ERR_ARG, "boa_model_step: bad arguments");
+    if (x->fused) {
+        FusedArgs a = fused_args(x, lanes, d_tokens);
+        a.logits = d_logits;
+        hipError_t e = hipSuccess;
+        PROF(PC_FUSED, fused_flops(x, lanes), fused_bytes(x, lanes),
+             e = launch_fused_step(a, x->prec == BOA_PREC_BF16X3 ? 3 : 2, x->stream));
+        if (e != hipSuccess) return boa_fail_hip(e, "k_fused_step", __FILE__, __LINE__);
+        x->pos += 1;
+        return BOA_OK;
+    }
     launch_embed_tokens(x, d_tokens, 1, 0, 1, lanes);
-    return run_model(x, lanes, 1, d_logits);
+    const int rc = run_model(x, lanes, 1, d_logits);
+    x->pos += 1;
+    return rc;
 }
 
 extern "C" int boa_model_forward(boa_ctx* x, const int32_t* d_tokens, int64_t tok_stride, int32_t lanes, int32_t len,
@@ -1434,6 +1536,7 @@ extern "C" int boa_model_forward(boa_ctx* x, const int32_t* d_tokens, int64_t to
         const int64_t rows = (int64_t)lanes * Tc;
         launch_embed_tokens(x, d_tokens, tok_stride, t0, Tc, rows);
         int rc = run_model(x, lanes, Tc, x->logits);
+        x->pos += Tc;
         if (rc) return rc;
         hipLaunchKernelGGL(k_scatter_logits, dim3(row_blocks(rows)), dim3(256), 0, x->stream, x->logits, x->V, Tc, t0,
                            len, rows, d_logits);
@@ -1460,6 +1563,7 @@ extern "C" int boa_compress(boa_ctx* x, const uint8_t* d_bytes, int64_t byte_str
              hipLaunchKernelGGL(k_embed_bytes, dim3(row_blocks(rows)), dim3(256), 0, s, d_bytes, byte_stride, d_lens,
                                 t0, Tc, rows, x->emb, x->d, x->V, x->x));
         rc = run_model(x, lanes, Tc, x->logits);
+        x->pos += Tc;
         if (rc) return rc;
         PROF(PC_ENCODE, 0.0, 4.0 * rows * x->V + (double)rows,
              hipLaunchKernelGGL(k_encode_tile, dim3(lanes), dim3(64), 0, s, x->logits, x->V, Tc, t0, d_bytes,
@@ -1486,9 +1590,26 @@ extern "C" int boa_decompress(boa_ctx* x, const uint32_t* d_payload, const int64
     if (rc) return rc;
     hipLaunchKernelGGL(k_dec_init, dim3((lanes + 255) / 256), dim3(256), 0, s, x->dec, d_payload, d_word_off, d_nwords,
                        d_first, d_lens, x->tokens, d_out, out_stride, lanes);
+    if (x->fused) {
+        // the fused kernel runs fused_steps positions per launch, feeding each decoded byte back itself
+        for (int t = 1; t < max_len; t += x->fused_steps) {
+            FusedArgs a = fused_args(x, lanes, x->tokens);
+            a.decode = 1; a.t = t; a.nsteps = std::min(x->fused_steps, max_len - t); a.stagger_us = x->stagger_us;
+            a.lens = d_lens; a.dec = x->dec; a.payload = d_payload; a.off = d_word_off;
+            a.nwords = d_nwords; a.tokens_out = x->tokens; a.out = d_out; a.out_stride = out_stride;
+            hipError_t e = hipSuccess;
+            PROF(PC_FUSED, a.nsteps * fused_flops(x, lanes), a.nsteps * fused_bytes(x, lanes),
+                 e = launch_fused_step(a, x->prec == BOA_PREC_BF16X3 ? 3 : 2, s));
+            if (e != hipSuccess) return boa_fail_hip(e, "k_fused_step", __FILE__, __LINE__);
+            x->pos += a.nsteps;
+        }
+        BOA_HIP_TRY(hipStreamSynchronize(s));
+        return BOA_OK;
+    }
     for (int t = 1; t < max_len; ++t) {
         launch_embed_tokens(x, x->tokens, 1, 0, 1, lanes);
         rc = run_model(x, lanes, 1, x->logits);
+        x->pos += 1;
         if (rc) return rc;
         PROF(PC_DECODE, 0.0, 4.0 * lanes * x->V + (double)lanes,
              hipLaunchKernelGGL(k_decode_step, dim3(lanes), dim3(64), 0, s, x->logits, x->V, t, d_lens, x->dec,

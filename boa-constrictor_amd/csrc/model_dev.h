@@ -1,0 +1,137 @@
+// Per-element model arithmetic shared by every model kernel of libboa_hip.so (the tiled GEMMs, the
+// LayerNorm / conv / scan kernels and the fused decompress-step kernel).  Each function below is the one
+// place its expression is written: the compress path and the decompress path call the same code, which is
+// what keeps their logits bit-identical (with -ffp-contract=off every operation rounds once as written).
+#pragma once
+
+#include "boa_common.h"
+
+namespace boa {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// GEMM epilogues: none | +bias | +bias,GELU(erf) | +bias,ReLU | residual + (acc + bias)
+enum { EPI_NONE = 0, EPI_BIAS = 1, EPI_GELU = 2, EPI_RELU = 3, EPI_RESID = 4 };
+
+// Quantiser precision of the fused coder (bits of the CDF total).
+static constexpr int CODER_P = 24;
+
+__device__ __forceinline__ float gelu_erf(float v) { return (v * 0.5f) * (1.0f + erff(v * 0.70710678118654752f)); }
+
+// Epilogue value of one accumulator before the residual add (EPI_RESID adds bias here, residual later).
+template <int EPI>
+__device__ __forceinline__ float epi_value(float acc, float bias) {
+    float v = acc;
+    if constexpr (EPI != EPI_NONE) v = v + bias;
+    if constexpr (EPI == EPI_GELU) v = gelu_erf(v);
+    if constexpr (EPI == EPI_RELU) v = fmaxf(v, 0.0f);
+    return v;
+}
+
+// fp32 -> bfloat16 bits, round to nearest even
+__device__ __forceinline__ uint32_t bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+// f = hi + lo (+ a remainder below 2^-16 of f): both parts bfloat16, hi = RNE(f), lo = RNE(f - hi)
+__device__ __forceinline__ void split2(float f, uint32_t& hi, uint32_t& lo) {
+    hi = bf16_rne(f);
+    lo = bf16_rne(f - __uint_as_float(hi << 16));
+}
+
+// LayerNorm statistics of a row of 256 * LNV values held by one wavefront, lane j holding elements
+// 256 * i + 4j .. 256 * i + 4j + 3 in v[4i .. 4i + 3].  Biased variance, eps 1e-5 (nn.LayerNorm).
+template <int LNV>
+__device__ __forceinline__ void ln_stats_row(const float (&v)[4 * LNV], float& mu, float& rs) {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4 * LNV; ++i) s = s + v[i];
+    s = wave_sum(s);
+    mu = s / (float)(256 * LNV);
+    float sq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4 * LNV; ++i) {
+        const float d = v[i] - mu;
+        sq = sq + d * d;
+    }
+    sq = wave_sum(sq);
+    const float var = sq / (float)(256 * LNV);
+    rs = 1.0f / sqrtf(var + 1e-5f);
+}
+
+__device__ __forceinline__ float ln_apply(float v, float mu, float rs, float w, float b) { return ((v - mu) * rs) * w + b; }
+
+// Depthwise causal conv (d_conv = 4) + bias + SiLU of one channel at one position:
+// xc = b + w0*x[t-3] + w1*x[t-2] + w2*x[t-1] + w3*x[t] (model.py:72, PyTorch Conv1d cross-correlation).
+__device__ __forceinline__ float conv_point(const float4 w, float bias, float h0, float h1, float h2, float x) {
+    float v = bias;
+    v = __builtin_fmaf(w.x, h0, v);
+    v = __builtin_fmaf(w.y, h1, v);
+    v = __builtin_fmaf(w.z, h2, v);
+    v = __builtin_fmaf(w.w, x, v);
+    return v / (1.0f + expf(-v));
+}
+
+// Selective scan, one position of one channel (Mamba's selective_scan_fn on one step):
+//   dt = softplus(dr . dt_w[c] + dt_b[c])     (threshold 20 as F.softplus)
+//   h_n <- exp(dt * A_n) * h_n + dt * B_n * x ;  with a[n] = A_n * log2(e) so exp(dt*A_n) = exp2(dt*a[n])
+//   y = sum_n h_n * C_n + D * x ;  y <- y * SiLU(z)
+// row = [dr (R) | B (NS) | C (NS)] of the position.
+template <int NS, int R>
+__device__ __forceinline__ float scan_position(const float* row, const float (&wr)[R], float bdt, const float (&a)[NS],
+                                               float Dc, float x, float z, float (&h)[NS]) {
+    float dt = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) dt = __builtin_fmaf(row[r], wr[r], dt);
+    dt = dt + bdt;
+    dt = (dt > 20.0f) ? dt : log1pf(expf(dt));
+    float y = 0.0f;
+#pragma unroll
+    for (int n = 0; n < NS; ++n) {
+        const float dA = __builtin_amdgcn_exp2f(dt * a[n]);  // v_exp_f32
+        const float dBx = (dt * row[R + n]) * x;
+        h[n] = __builtin_fmaf(dA, h[n], dBx);
+        y = __builtin_fmaf(h[n], row[R + NS + n], y);
+    }
+    y = __builtin_fmaf(Dc, x, y);
+    return y * (z / (1.0f + expf(-z)));
+}
+
+// Logits of one lane (a V-wide row) as held by one wavefront: lane j gets elements 4j .. 4j + 3 (0 beyond V).
+__device__ __forceinline__ float4 logits_row4(const float* row, int V, int lane) {
+    float4 l4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (4 * lane + 3 < V) {
+        l4 = *reinterpret_cast<const float4*>(row + 4 * lane);
+    } else {
+        if (4 * lane + 0 < V) l4.x = row[4 * lane + 0];
+        if (4 * lane + 1 < V) l4.y = row[4 * lane + 1];
+        if (4 * lane + 2 < V) l4.z = row[4 * lane + 2];
+    }
+    return l4;
+}
+
+// One decode step of one lane (whole wavefront): quantise the logits (XQ), find the symbol the coder state
+// points into, advance the state.  Returns the symbol (uniform across the wave).
+__device__ __forceinline__ int decode_row(const float* row, int V, int lane, DecState& st, const uint32_t* in,
+                                          int32_t nw) {
+    XQ q;
+    xq_build(q, logits_row4(row, V, lane), lane, V, CODER_P);
+    uint32_t e[4];
+    uint32_t c = q.base;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int k = 4 * lane + j;
+        e[j] = (k < V) ? xq_cdf_at(q, c, k) : (1u << CODER_P);
+        c += q.f[j];
+    }
+    const uint32_t qv = dec_target(st, CODER_P);
+    uint32_t lo, hi;
+    const int s = wave_find_symbol<CODER_P>(e, V, qv, lane, lo, hi);
+    dec_advance(st, CODER_P, lo, hi - lo, in, nw);
+    return s;
+}
+
+}  // namespace boa

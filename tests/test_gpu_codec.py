@@ -104,3 +104,26 @@ def test_boa_file_round_trip(gpu, tmp_path):
         assert boa.BOA("cuda", str(tmp_path / "x.boa"), m).decompress(progress=False) == data
     finally:
         del os.environ["BOA_GPU_STREAMS"]
+
+
+def test_decompress_fused_and_layer_kernels_agree(gpu):
+    """Decompression through the fused step kernel and through the per-layer kernels gives the same bytes
+    (both must reproduce the compressor's logits bit for bit to decode at all)."""
+    import codec
+
+    m, _ = _model(2)
+    lens = [300, 17, 1, 256, 45]
+    chunks = [_markov(L, seed=20 + i) for i, L in enumerate(lens)]
+    payload, nw, fb, Ls = codec.compress_payload(m, chunks)
+    outs = []
+    for flag in ("1", "0"):
+        os.environ["BOA_FUSED_STEP"] = flag
+        try:
+            m.release_engines()
+            outs.append(codec.decompress_payload(m, payload, nw, Ls, fb))
+        finally:
+            del os.environ["BOA_FUSED_STEP"]
+    m.release_engines()
+    for out in outs:
+        for i, c in enumerate(chunks):
+            assert (out[i, :lens[i]] == c).all(), i

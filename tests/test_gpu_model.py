@@ -137,3 +137,52 @@ def test_zero_weights_give_bias_only_logits(gpu):
     out = m(torch.randint(0, 256, (4, 9)).cuda()).cpu()
     hb = torch.from_numpy(sd["head.2.bias"])
     assert torch.equal(out, hb.expand_as(out))
+
+
+@pytest.mark.parametrize("precision", ["f32", "bf16x3"])
+def test_gemm_tiling_independence_at_scale(gpu, precision):
+    """4096 lanes: the step path runs the 128x128/BK64 and 64x64/BK128 GEMM configurations, the 8-position
+    tile path the 128x128/BK32 one; logits must agree bit for bit (the decoder depends on it)."""
+    m, _ = _model(1, precision=precision)
+    B, T = 4096, 8
+    tok = torch.randint(0, 256, (B, T), generator=torch.Generator().manual_seed(3)).cuda()
+    m.release_engines()
+    eng = m.engine(B, T)
+    eng.reset(B)
+    tiled = torch.empty((B, T, 256), dtype=torch.float32, device="cuda")
+    eng.forward(tok.to(torch.int32).contiguous(), tiled)
+    inf = m.init_stream(max_len=T, batch_size=B)
+    for t in range(T):
+        st = m.step(tok[:, t], inf)
+        assert torch.equal(st, tiled[:, t]), (t, float((st - tiled[:, t]).abs().max()))
+    m.release_engines()
+
+
+def _stream_logits(m, tok, fused):
+    """Step logits [B, T, V] from a fresh stream; fused=False builds the context with BOA_FUSED_STEP=0."""
+    import os
+
+    old = os.environ.get("BOA_FUSED_STEP")
+    os.environ["BOA_FUSED_STEP"] = "1" if fused else "0"
+    try:
+        inf = m.init_stream(max_len=tok.shape[1], batch_size=tok.shape[0])
+    finally:
+        if old is None:
+            del os.environ["BOA_FUSED_STEP"]
+        else:
+            os.environ["BOA_FUSED_STEP"] = old
+    return torch.stack([m.step(tok[:, t], inf) for t in range(tok.shape[1])], dim=1)
+
+
+@pytest.mark.parametrize("precision", ["bf16x3", "bf16w"])
+def test_fused_step_matches_layer_kernels(gpu, precision):
+    """The one-launch decompress step (16 lanes per workgroup, activations in LDS) against the per-layer
+    step kernels: identical bits, including a partial last workgroup (37 lanes) and > 3 positions (the conv
+    history ring wraps)."""
+    m, ref = _model(8, precision=precision)
+    tok = torch.from_numpy(np.random.default_rng(11).integers(0, 256, (37, 9))).cuda()
+    a = _stream_logits(m, tok, fused=True)
+    b = _stream_logits(m, tok, fused=False)
+    assert torch.equal(a, b), float((a - b).abs().max())
+    lr = ref.forward(tok.cpu())
+    assert _rel(a.cpu(), lr) <= REL_TOL
