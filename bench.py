@@ -28,23 +28,44 @@ for _p in (REPO, os.path.join(REPO, "boa-constrictor_amd")):
         sys.path.insert(0, _p)
 
 METRIC = "input MB/s compress + decompress, d256×8L Mamba, 4096 chunks, 1 GPU"
-PEAK_FP32_MFMA_TFLOPS = 157.3
+PEAK_BF16_MFMA_TFLOPS = 2500.0  # dense; a bf16x3 GEMM issues 3 bf16 products per model multiply-add
 PEAK_HBM_GBPS = 8000.0
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_fused_step_d256x8L_4096lanes.json")
 
-# rocprof names of the kernel instances each profiled class launches at the benchmark's shapes
-# (k_gemm<BM, BN, LN, EPI>: EPI 1 bias, 2 GELU, 3 ReLU, 4 residual)
+# rocprof names of the kernel instances each profiled class launches at the benchmark's shapes, default
+# precision bf16x3 (k_gemm_bf<BM, BN, BK, EPI, NT, A split, C split>: EPI 0 none, 1 bias, 2 GELU, 4 residual)
 KERNEL_NAMES = {
-    ("compress", "gemm_in_proj"): "k_gemm<128, 128, 1, 1>",
-    ("compress", "gemm_ff1"): "k_gemm<128, 128, 1, 2>",
-    ("compress", "gemm_ff2"): "k_gemm<128, 128, 0, 4>",
-    ("compress", "gemm_out_proj"): "k_gemm<128, 128, 0, 1>",
-    ("decompress", "gemm_in_proj"): "k_gemm<64, 64, 1, 1>",
-    ("decompress", "gemm_ff1"): "k_gemm<64, 64, 1, 2>",
-    ("decompress", "gemm_ff2"): "k_gemm<64, 64, 0, 4>",
-    ("decompress", "gemm_out_proj"): "k_gemm<64, 64, 0, 1>",
+    ("compress", "gemm_in_proj"): "k_gemm_bf<128, 128, 32, 1, 3, true, false>",
+    ("compress", "gemm_ff1"): "k_gemm_bf<128, 128, 32, 2, 3, true, true>",
+    ("compress", "gemm_ff2"): "k_gemm_bf<128, 128, 32, 4, 3, true, false>",
+    ("compress", "gemm_out_proj"): "k_gemm_bf<128, 128, 32, 1, 3, true, false>",
+    ("compress", "gemm_x_proj"): "k_gemm_bf<64, 64, 128, 0, 3, false, false>",
     ("compress", "scan"): "k_scan<16, 16, true>",
-    ("decompress", "scan"): "k_scan_step<16, 16, true>",
+    ("compress", "conv"): "k_conv_silu",
+    ("decompress", "fused_step"): "k_fused_step<3>",
 }
+
+
+def fused_step_bytes(lanes: int, d: int = 256, L: int = 8, di: int = 512, ns: int = 16, V: int = 256) -> float:
+    """Compulsory HBM bytes of one fused decode step (the library's own estimate, restated): SSM state read +
+    write and conv history (3 reads + 1 write) per lane and layer, the input embedding row and coder state per
+    lane, plus the bf16x3 weights (hi + lo) once."""
+    params = L * (2 * di * d + (d // 16 + 2 * ns) * di + d * di + 4 * d * d * 2) + d * d + V * d
+    return lanes * (L * (2.0 * di * ns * 4 + 4.0 * di * 4) + 4.0 * d + 64.0) + 4.0 * params
+
+
+def measured_traffic(lanes: int, steps_per_launch: float):
+    """HBM bytes per fused-step launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled by the
+    same counters on a copy kernel of known size), from the committed profile summary when it describes this
+    launch shape; otherwise None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if t.get("lanes") != lanes:
+        return None
+    return t["bytes_per_step"] * steps_per_launch
 
 
 def log(msg):
@@ -135,6 +156,8 @@ def main():
     ap.add_argument("--tile-len", type=int, default=int(os.environ.get("BOA_TILE_LEN", "64")))
     ap.add_argument("--cpu-steps", type=int, default=300, help="coded positions per chunk in the CPU sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 1 GiB device-to-device copy 3 times (PMC byte-counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (chunks are independent and would "
@@ -149,6 +172,15 @@ def main():
     import model as M
 
     assert torch.cuda.is_available(), "bench.py needs the GPU"
+    if args.calibrate_copy:
+        src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "copy", "bytes_read": src.numel() * 4, "bytes_written": dst.numel() * 4,
+                          "launches": 3}))
+        return
     lib = N.lib()
     dev = torch.device("cuda")
     nbytes = args.payload_mib << 20
@@ -246,10 +278,10 @@ def main():
         _, phase, name, e = best
         avg_ms = e["ms"] / e["sampled"]
         if name.startswith("gemm"):
-            achieved = e["flops"] / (e["ms"] * 1e-3) / 1e12
-            roofline = {"bound": "mfma", "achieved": achieved, "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
-                        "frac": achieved / PEAK_FP32_MFMA_TFLOPS, "traffic": None}
-            per_launch = e["flops"] / e["sampled"]
+            achieved = 3.0 * e["flops"] / (e["ms"] * 1e-3) / 1e12  # bf16 MFMA flops (3 products)
+            roofline = {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_MFMA_TFLOPS, "unit": "TFLOP/s",
+                        "frac": achieved / PEAK_BF16_MFMA_TFLOPS, "traffic": None}
+            per_launch = 3.0 * e["flops"] / e["sampled"]
         else:
             achieved = e["bytes"] / (e["ms"] * 1e-3) / 1e9
             roofline = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
@@ -258,6 +290,9 @@ def main():
         roofline.update({"kernel": f"{phase}/{name}", "rocprof_name": KERNEL_NAMES.get((phase, name), name),
                          "avg_launch_ms": avg_ms, "algorithmic_per_launch": per_launch,
                          "launches": e["launches"], "time_share": best[0] / total_ms if total_ms else None})
+        if name == "fused_step":
+            roofline["steps_per_launch"] = round(per_launch / fused_step_bytes(B), 3)
+            roofline["traffic"] = measured_traffic(B, roofline["steps_per_launch"])
 
     cpu = None
     if not args.no_cpu:
