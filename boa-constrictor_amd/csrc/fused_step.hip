@@ -165,9 +165,11 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
         if (a.decode)
             for (int r = 0; r < nb; ++r) ml = a.lens[b0 + r] > ml ? a.lens[b0 + r] : ml;
         sMaxLen = ml;
-        // start offset of this workgroup's class (4 classes, by XCD-local index)
-        if (a.stagger_us > 0) {
-            const uint64_t until = wall_clock64() + (uint64_t)(((blockIdx.x >> 3) & 3) * a.stagger_us) * 100u;
+        // start offset of this workgroup's class: classes are sets of XCDs (workgroup i runs on XCD i mod 8),
+        // which do not share an L2, so a following class does not catch up on the leaders' L2 hits
+        if (a.stagger_us > 0 && a.stagger_classes > 1) {
+            const int cls = (int)(blockIdx.x & 7) * a.stagger_classes / 8;
+            const uint64_t until = wall_clock64() + (uint64_t)(cls * a.stagger_us) * 100u;
             while (wall_clock64() < until) __builtin_amdgcn_s_sleep(8);
         }
     }

@@ -919,8 +919,12 @@ struct boa_ctx {
     int32_t* flag = nullptr;
     int64_t pos = 0;                   // positions processed since the last state reset (conv history ring)
     bool fused = false;                // decompress / step through k_fused_step
-    int fused_steps = 64;              // decode steps per k_fused_step launch
-    int stagger_us = 25;               // start offset between the fused kernel's workgroup classes
+    int fused_steps = 128;             // decode steps per k_fused_step launch
+    // k_fused_step workgroup classes (sets of XCDs) start this far apart, so that one class runs its
+    // HBM-bound scans while the other streams weights from L2.  Offsets below ~2 layers' time (~250 us at
+    // d256x8L, 4096 lanes) do not hold: the follower catches up on the leader's cached weights.
+    int stagger_us = 320;
+    int stagger_classes = 2;
     uint16_t* wfrag = nullptr;         // fragment-packed GEMM weights (fused)
     FusedLayer* d_layers = nullptr;    // per-layer pointer table (fused)
     int64_t device_bytes = 0;
@@ -1211,6 +1215,7 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
         x->fused = fused_step_supported(d, NS, R, x->DC, V) && !(fenv && fenv[0] == '0');
         if (const char* v = getenv("BOA_FUSED_STEPS_PER_LAUNCH")) x->fused_steps = std::max(1, atoi(v));
         if (const char* v = getenv("BOA_FUSED_STAGGER_US")) x->stagger_us = std::max(0, atoi(v));
+        if (const char* v = getenv("BOA_FUSED_STAGGER_CLASSES")) x->stagger_classes = std::min(8, std::max(1, atoi(v)));
         if (x->fused) {
             const bool two = x->prec == BOA_PREC_BF16X3;
             int64_t ftotal = 0;
@@ -1595,6 +1600,7 @@ extern "C" int boa_decompress(boa_ctx* x, const uint32_t* d_payload, const int64
         for (int t = 1; t < max_len; t += x->fused_steps) {
             FusedArgs a = fused_args(x, lanes, x->tokens);
             a.decode = 1; a.t = t; a.nsteps = std::min(x->fused_steps, max_len - t); a.stagger_us = x->stagger_us;
+            a.stagger_classes = x->stagger_classes;
             a.lens = d_lens; a.dec = x->dec; a.payload = d_payload; a.off = d_word_off;
             a.nwords = d_nwords; a.tokens_out = x->tokens; a.out = d_out; a.out_stride = out_stride;
             hipError_t e = hipSuccess;

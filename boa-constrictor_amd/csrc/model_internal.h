@@ -38,6 +38,7 @@ struct FusedArgs {
     int t;
     int nsteps;
     int stagger_us;            // start offset between workgroup classes (multi-step launches), microseconds
+    int stagger_classes;       // number of classes (1, 2, 4 or 8 sets of XCDs)
     const int32_t* lens;
     DecState* dec;
     const uint32_t* payload;
