@@ -101,6 +101,110 @@ def markov_bytes(n: int, seed: int = 0, alpha: float = 0.1):
     return out
 
 
+CODER_METRIC = "range coder alone: symbols/s encode + decode, 16384 streams x 4096 symbols, P=16, 1 GPU"
+
+
+def coder_bench(args):
+    """per-step 256-symbol tables from N(0, 3^2) logits quantised to total 2^16 (min freq 1),
+    symbols drawn from them, 16384 streams x 4096 symbols, generated on the device (not timed); then one
+    timed encode and one timed decode over tables resident in HBM.  Byte-exact decode is checked on the
+    device; the CPU leg runs this repo's C coder on a sample of streams and must produce the same words."""
+    import numpy as np
+    import torch
+
+    from boa_amd import _native as N
+
+    lib = N.lib()
+    S, T, K, P = args.coder_streams, args.coder_len, 256, 16
+    d_cdf = torch.empty((S, T, K), dtype=torch.int16, device="cuda")
+    d_syms = torch.empty((S, T), dtype=torch.uint8, device="cuda")
+    log(f"[coder] synthesising {S} x {T} tables ({d_cdf.numel() * 2 / 2**30:.1f} GiB)")
+    N.check(lib.rc_synth_tables(0, 3.0, P, 2, K, S, T, N.ptr(d_cdf), N.ptr(d_syms), N.stream_ptr()))
+    pitch = T + 8
+    d_words = torch.zeros((S, pitch), dtype=torch.int32, device="cuda")
+    d_n = torch.zeros(S, dtype=torch.int32, device="cuda")
+    d_out = torch.zeros((S, T), dtype=torch.uint8, device="cuda")
+
+    def enc():
+        N.check(lib.rc_encode_tables(P, 2, N.ptr(d_cdf), K, N.ptr(d_syms), S, T, N.ptr(d_words), pitch, N.ptr(d_n),
+                                     N.stream_ptr()))
+
+    def dec():
+        N.check(lib.rc_decode_tables(P, 2, N.ptr(d_cdf), K, N.ptr(d_words), pitch, N.ptr(d_n), S, T, N.ptr(d_out),
+                                     N.stream_ptr()))
+
+    for _ in range(args.warmup):
+        enc()
+        dec()
+    te, td = [], []
+    for _ in range(args.steps):
+        e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+        torch.cuda.synchronize()
+        e0.record()
+        enc()
+        e1.record()
+        dec()
+        e2.record()
+        torch.cuda.synchronize()
+        te.append(e0.elapsed_time(e1) * 1e-3)
+        td.append(e1.elapsed_time(e2) * 1e-3)
+    ok = bool(torch.equal(d_out, d_syms))
+    t_e, t_d = float(np.mean(te)), float(np.mean(td))
+    nsym = S * T
+    code_bytes = 4 * int(d_n.sum().item())
+    # decode reads each step's full table row (K entries, 2 B) + writes 1 B; encode reads 2 entries + 1 B
+    dec_bytes = nsym * (2.0 * K + 1) + code_bytes
+    enc_bytes = nsym * (2.0 * 2 + 1) + code_bytes
+    roofline = {"bound": "hbm", "kernel": "k_rc_decode_tables", "achieved": dec_bytes / t_d / 1e9,
+                "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": dec_bytes / t_d / 1e9 / PEAK_HBM_GBPS, "traffic": None,
+                "avg_launch_ms": t_d * 1e3, "algorithmic_per_launch": dec_bytes}
+    cpu = None
+    if not args.no_cpu:
+        from oracle import ora
+
+        ns = args.coder_cpu_streams
+        tab = d_cdf[:ns].cpu().numpy().view(np.uint16).astype(np.uint32)
+        full = np.concatenate([tab, np.full((ns, T, 1), 1 << P, np.uint32)], axis=-1)
+        syms = d_syms[:ns].cpu().numpy().astype(np.int32)
+        words = d_words[:ns].cpu().numpy().view(np.uint32)
+        nw = d_n[:ns].cpu().numpy()
+        t0 = time.perf_counter()
+        ref = [ora.encode_tables(P, full[i], syms[i]) for i in range(ns)]
+        t1 = time.perf_counter()
+        back = [ora.decode_tables(P, full[i], ref[i]) for i in range(ns)]
+        t2 = time.perf_counter()
+        same = all(np.array_equal(words[i, :nw[i]], ref[i]) for i in range(ns))
+        rt = all(np.array_equal(back[i], syms[i]) for i in range(ns))
+        cpu = {"value": ns * T / (t2 - t0), "unit": "symbols/s", "cores": 1, "kind": "port",
+               "sample": f"first {ns} streams of the same tables (this repo's C coder, oracle/rc_oracle.c), "
+                         "encode then decode, one thread",
+               "encode_symbols_per_s": ns * T / (t1 - t0), "decode_symbols_per_s": ns * T / (t2 - t1),
+               "words_identical_to_gpu": bool(same), "round_trip_ok": bool(rt)}
+    res = {
+        "metric": CODER_METRIC,
+        "value": nsym / (t_e + t_d),
+        "unit": "symbols/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": (t_e + t_d) * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u32",
+        "data": "synthetic",
+        "config": {"workload": f"configs[1]: {S} streams x {T} symbols, K=256, P=16, tables in HBM (int16 entries)",
+                   "streams": S, "symbols_per_stream": T},
+        "encode_symbols_per_s": nsym / t_e,
+        "decode_symbols_per_s": nsym / t_d,
+        "code_bytes": code_bytes,
+        "round_trip_ok": ok,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res))
+
+
 def cpu_baseline(steps: int):
     import numpy as np
     import torch
@@ -156,6 +260,11 @@ def main():
     ap.add_argument("--tile-len", type=int, default=int(os.environ.get("BOA_TILE_LEN", "64")))
     ap.add_argument("--cpu-steps", type=int, default=300, help="coded positions per chunk in the CPU sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--workload", choices=["codec", "coder"], default="codec",
+                    help="codec: configs[2]+[3] (the metric); coder: configs[1], the range coder alone")
+    ap.add_argument("--coder-streams", type=int, default=16384)
+    ap.add_argument("--coder-len", type=int, default=4096)
+    ap.add_argument("--coder-cpu-streams", type=int, default=64)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy 3 times (PMC byte-counter calibration)")
     args = ap.parse_args()
@@ -180,6 +289,9 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"calibration": "copy", "bytes_read": src.numel() * 4, "bytes_written": dst.numel() * 4,
                           "launches": 3}))
+        return
+    if args.workload == "coder":
+        coder_bench(args)
         return
     lib = N.lib()
     dev = torch.device("cuda")
@@ -260,6 +372,22 @@ def main():
     ok = bool(torch.equal(out, X))
     comp_bytes = 4 * int(nw.sum().item())
     tc, td = float(np.mean(tcs)), float(np.mean(tds))
+    # PCIe legs of the host-memory API (codec.compress_GPU / decompress_GPU): input H2D + payload D2H for
+    # compress, payload H2D + output D2H for decompress, pinned host buffers, timed on their own
+    host_payload = torch.empty(comp_bytes // 4, dtype=torch.int32, pin_memory=True)
+    host_out = torch.empty_like(host, pin_memory=True)
+
+    def timed(fn):
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        fn()
+        torch.cuda.synchronize()
+        return time.perf_counter() - t
+
+    t_h2d_in = timed(lambda: X.copy_(host, non_blocking=True))
+    t_d2h_pl = timed(lambda: host_payload.copy_(payload[:comp_bytes // 4], non_blocking=True))
+    t_h2d_pl = timed(lambda: payload[:comp_bytes // 4].copy_(host_payload, non_blocking=True))
+    t_d2h_out = timed(lambda: host_out.copy_(out, non_blocking=True))
 
     # dominant kernel: largest estimated total time (sampled time scaled to all launches)
     share = {}
@@ -328,6 +456,10 @@ def main():
         "decompress_MiBps": nbytes / td / 2**20,
         "decompress_step_ms": td / (chunk - 1) * 1e3,
         "compressed_bytes": comp_bytes,
+        "host_compress_MBps": nbytes / (tc + t_h2d_in + t_d2h_pl) / 1e6,
+        "host_decompress_MBps": nbytes / (td + t_h2d_pl + t_d2h_out) / 1e6,
+        "pcie_ms": {"input_h2d": t_h2d_in * 1e3, "payload_d2h": t_d2h_pl * 1e3, "payload_h2d": t_h2d_pl * 1e3,
+                    "output_d2h": t_d2h_out * 1e3},
         "round_trip_ok": ok,
         "roofline": roofline,
         "kernel_ms": {k: round(v, 3) for k, v in sorted(share.items(), key=lambda kv: -kv[1])},
