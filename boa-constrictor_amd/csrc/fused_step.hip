@@ -31,8 +31,6 @@ constexpr int FNS = 16;             // d_state
 constexpr int FR = 16;              // dt_rank
 constexpr int FW = FR + 2 * FNS;    // x_proj width (dt | B | C)
 constexpr int ROWS = 16;            // lanes per workgroup
-constexpr int NTHR = 512;
-constexpr int NWAVE = NTHR / 64;
 
 constexpr int LRES = FD + 4;        // fp32 rows of 256 (+4: conflict-free fragment-order writes)
 constexpr int LA = FDI + 8;         // split operand rows, K <= 512 (bf16 elements)
@@ -54,18 +52,19 @@ static_assert(OFF_A % 16 == 0 && OFF_X % 16 == 0 && OFF_DBC % 16 == 0, "LDS alig
 static_assert(ROWS * LRES * 4 <= SZ_A, "logits tile must fit the operand region");
 
 // C[16][16 nfrag] = A[16][K] (split bf16 in LDS, row stride lda) x W^T (fragment-packed), for this wave's
-// fragments f = rot(f0 + wave + 8 j) (j < FPW, f0 + wave + 8 j < nfrag), rot(f) = (f + rot) mod nfrag.  B
+// fragments f = rot(f0 + wave + NWAVE j) (j < FPW, f0 + wave + NWAVE j < nfrag), rot(f) = (f + rot) mod nfrag.  B
 // blocks of D - 1 K steps ahead are in flight (a register ring) while the current step is multiplied: one
 // workgroup per CU streams every weight of the layer from L2, so latency bounds a shallow pipeline.  The
 // rotation (per workgroup) spreads the workgroups of an XCD over different weight blocks at any moment
 // instead of all reading the same L2 lines; it does not change any output (each output fragment still
 // accumulates its K steps in ascending order).  Output column of acc[j]: 16 * frag_of(...) + lane % 16.
+template <int NWAVE>
 __device__ __forceinline__ int frag_of(int f0, int wave, int j, int nfrag, int rot) {
-    const int f = f0 + wave + 8 * j + rot;
+    const int f = f0 + wave + NWAVE * j + rot;
     return f >= nfrag ? f - nfrag : f;
 }
 
-template <int NT, int FPW, int K, int D>
+template <int NT, int NWAVE, int FPW, int K, int D>
 __device__ __forceinline__ void mgemm(const uint16_t* sAh, const uint16_t* sAl, int lda,
                                       const uint16_t* __restrict__ Wp, int f0, int nfrag, int wave, int lane,
                                       int rot, floatx4 (&acc)[FPW]) {
@@ -80,7 +79,7 @@ __device__ __forceinline__ void mgemm(const uint16_t* sAh, const uint16_t* sAl, 
 #pragma unroll
         for (int j = 0; j < FPW; ++j) {
             if (fw + NWAVE * j < nfrag) {
-                const int f = frag_of(f0, wave, j, nfrag, rot);
+                const int f = frag_of<NWAVE>(f0, wave, j, nfrag, rot);
                 const uint16_t* p = Wp + ((int64_t)f * S + s) * BLK + lane * 8;
                 bh[slot][j] = *reinterpret_cast<const uint4*>(p);
                 if constexpr (NT == 3) bl[slot][j] = *reinterpret_cast<const uint4*>(p + 512);
@@ -116,14 +115,15 @@ __device__ __forceinline__ void put_split(uint16_t* h, uint16_t* l, int idx, flo
     l[idx] = (uint16_t)lo;
 }
 
-// LayerNorm of rows 2*wave, 2*wave + 1 of src (fp32, stride LRES) into the split operand (stride LA).
+// LayerNorm of rows RPW*wave .. RPW*wave + RPW-1 of src (fp32, stride LRES) into the split operand (stride LA).
+template <int RPW>
 __device__ __forceinline__ void ln_rows(const float* src, const float* __restrict__ w, const float* __restrict__ b,
                                        uint16_t* sAh, uint16_t* sAl, int wave, int lane) {
     const float4 wv = *reinterpret_cast<const float4*>(w + 4 * lane);
     const float4 bv = *reinterpret_cast<const float4*>(b + 4 * lane);
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-        const int r = 2 * wave + q;
+    for (int q = 0; q < RPW; ++q) {
+        const int r = RPW * wave + q;
         const float4 x4 = *reinterpret_cast<const float4*>(src + r * LRES + 4 * lane);
         const float v[4] = {x4.x, x4.y, x4.z, x4.w};
         float mu, rs;
@@ -140,8 +140,19 @@ __device__ __forceinline__ void ln_rows(const float* src, const float* __restric
 
 typedef __attribute__((address_space(4))) const FusedArgs KArgs;
 
-template <int NT>
+// NTHR = 512 (8 waves, 2 per SIMD) or 1024 (16 waves: twice the weight loads in flight per CU, with
+// 128 registers per lane).  The mapping of outputs to waves changes, the arithmetic of each output does not.
+template <int NT, int NTHR>
 __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
+    constexpr int NWAVE = NTHR / 64;
+    constexpr int RPW = ROWS / NWAVE;               // rows per wave (LN, decode)
+    constexpr int TPC = NTHR / FDI;                 // threads per channel (conv, scan)
+    constexpr int RPT = ROWS / TPC;                 // rows per thread (conv, scan)
+    constexpr int FPW_B = NWAVE == 8 ? 4 : 2;       // fragments per wave, N = 1024 GEMMs (per pass)
+    constexpr int D_B = 3;         // K steps in flight, N = 1024 GEMMs
+    constexpr int FPW_S = 16 / NWAVE;               // fragments per wave, N = 256 GEMMs
+    constexpr int D_S = 6;         // K steps in flight, N = 256 GEMMs
+    static_assert(NTHR == 512 || NTHR == 1024, "fused step block size");
     __shared__ __attribute__((aligned(16))) unsigned char lds[LDS_BYTES];
     float* sRes = reinterpret_cast<float*>(lds + OFF_RES);
     uint16_t* sAh = reinterpret_cast<uint16_t*>(lds + OFF_A);
@@ -212,43 +223,46 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
     for (int l = 0; l < a.L; ++l) {
         const FusedLayer& w = a.layers[l];
         // ---- LN1 -> split operand
-        ln_rows(sRes, w.ln1_w, w.ln1_b, sAh, sAl, wave, lane);
+        ln_rows<RPW>(sRes, w.ln1_w, w.ln1_b, sAh, sAl, wave, lane);
         __syncthreads();
         // ---- in_proj (+bias) -> xz fp32
 #pragma unroll 1
-        for (int f0 = 0; f0 < 2 * FDI / 16; f0 += 4 * NWAVE) {
-            floatx4 acc[4];
-            mgemm<NT, 4, FD, 3>(sAh, sAl, LA, w.in_p, f0, 2 * FDI / 16, wave, lane, rot64, acc);
+        for (int f0 = 0; f0 < 2 * FDI / 16; f0 += FPW_B * NWAVE) {
+            floatx4 acc[FPW_B];
+            mgemm<NT, NWAVE, FPW_B, FD, D_B>(sAh, sAl, LA, w.in_p, f0, 2 * FDI / 16, wave, lane, rot64, acc);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int n = 16 * frag_of(f0, wave, j, 2 * FDI / 16, rot64) + n_of;
+            for (int j = 0; j < FPW_B; ++j) {
+                const int n = 16 * frag_of<NWAVE>(f0, wave, j, 2 * FDI / 16, rot64) + n_of;
                 const float bias = w.in_b[n];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) sX[(m_of + r) * LXZ + n] = epi_value<EPI_BIAS>(acc[j][r], bias);
             }
         }
         __syncthreads();
-        // ---- conv + SiLU (thread = channel): xs fp32 in place of x, split operand for x_proj, history ring
+        // ---- conv + SiLU (thread = channel x row range): xs fp32 in place of x, split operand for x_proj,
+        //      history ring
         {
-            const int c = tid;
+            const int c = tid % FDI, rb = TPC == 1 ? 0 : __builtin_amdgcn_readfirstlane(tid / FDI) * RPT;
             const float4 cw = *reinterpret_cast<const float4*>(w.conv_w + 4 * c);
             const float cb = w.conv_b[c];
             float* hl = a.hist + (int64_t)l * a.max_lanes * 3 * FDI;
-            float h0[ROWS], h1[ROWS], h2[ROWS];
+            float h0[RPT], h1[RPT], h2[RPT];
 #pragma unroll
-            for (int r = 0; r < ROWS; ++r) {
-                h0[r] = h1[r] = h2[r] = 0.0f;
+            for (int q = 0; q < RPT; ++q) {
+                const int r = rb + q;
+                h0[q] = h1[q] = h2[q] = 0.0f;
                 if (r < nb) {
                     const float* hb = hl + (b0 + r) * 3 * FDI;
-                    h0[r] = hb[p0m3 * FDI + c];
-                    h1[r] = hb[s1 * FDI + c];
-                    h2[r] = hb[s2 * FDI + c];
+                    h0[q] = hb[p0m3 * FDI + c];
+                    h1[q] = hb[s1 * FDI + c];
+                    h2[q] = hb[s2 * FDI + c];
                 }
             }
 #pragma unroll
-            for (int r = 0; r < ROWS; ++r) {
+            for (int q = 0; q < RPT; ++q) {
+                const int r = rb + q;
                 const float x = sX[r * LXZ + c];
-                const float y = conv_point(cw, cb, h0[r], h1[r], h2[r], x);
+                const float y = conv_point(cw, cb, h0[q], h1[q], h2[q], x);
                 sX[r * LXZ + c] = y;
                 put_split(sAh, sAl, r * LA + c, y);
                 if (r < nb) hl[(b0 + r) * 3 * FDI + p0m3 * FDI + c] = x;
@@ -258,14 +272,14 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
         // ---- x_proj -> [dt | B | C] rows
         if (wave < FW / 16) {
             floatx4 acc[1];
-            mgemm<NT, 1, FDI, 8>(sAh, sAl, LA, w.x_p, 0, FW / 16, wave, lane, 0, acc);
+            mgemm<NT, NWAVE, 1, FDI, 8>(sAh, sAl, LA, w.x_p, 0, FW / 16, wave, lane, 0, acc);
 #pragma unroll
             for (int r = 0; r < 4; ++r) sDbc[(m_of + r) * FW + 16 * wave + n_of] = acc[0][r];
         }
         __syncthreads();
-        // ---- dt_proj + softplus + selective scan + D + gate (thread = channel) -> y split operand
+        // ---- dt_proj + softplus + selective scan + D + gate (thread = channel x row range) -> y split operand
         {
-            const int c = tid;
+            const int c = tid % FDI, rb = TPC == 1 ? 0 : __builtin_amdgcn_readfirstlane(tid / FDI) * RPT;
             float av[FNS], wr[FR];
             const float* Ag = w.Aneg;
 #pragma unroll
@@ -280,9 +294,10 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
             }
             const float bdt = w.dt_b[c], Dc = w.D[c];
             float* sl = a.ssm + (int64_t)l * a.max_lanes * FDI * FNS + 4 * c;
-            constexpr int PD = 4;  // lanes of state in flight
+            constexpr int PD = NTHR == 512 ? 4 : 3;  // lanes of state in flight
             float hr[PD][FNS];
-            auto load_h = [&](int r, float (&h)[FNS]) {
+            auto load_h = [&](int q, float (&h)[FNS]) {
+                const int r = rb + q;
                 if (r < nb) {
                     const float* hp = sl + (b0 + r) * FDI * FNS;
 #pragma unroll
@@ -296,11 +311,12 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
                 }
             };
 #pragma unroll
-            for (int r = 0; r < PD - 1; ++r) load_h(r, hr[r]);
+            for (int q = 0; q < PD - 1; ++q) load_h(q, hr[q]);
 #pragma unroll
-            for (int r = 0; r < ROWS; ++r) {
-                if (r + PD - 1 < ROWS) load_h(r + PD - 1, hr[(r + PD - 1) % PD]);
-                float (&h)[FNS] = hr[r % PD];
+            for (int q = 0; q < RPT; ++q) {
+                if (q + PD - 1 < RPT) load_h(q + PD - 1, hr[(q + PD - 1) % PD]);
+                float (&h)[FNS] = hr[q % PD];
+                const int r = rb + q;
                 const float x = sX[r * LXZ + c], z = sX[r * LXZ + FDI + c];
                 const float y = scan_position<FNS, FR>(sDbc + r * FW, wr, bdt, av, Dc, x, z, h);
                 put_split(sAh, sAl, r * LA + c, y);
@@ -316,11 +332,11 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
         __syncthreads();
         // ---- out_proj (+bias) -> mixer output fp32 (stride LRES, in the xz region)
         {
-            floatx4 acc[2];
-            mgemm<NT, 2, FDI, 6>(sAh, sAl, LA, w.out_p, 0, FD / 16, wave, lane, rot16, acc);
+            floatx4 acc[FPW_S];
+            mgemm<NT, NWAVE, FPW_S, FDI, D_S>(sAh, sAl, LA, w.out_p, 0, FD / 16, wave, lane, rot16, acc);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int n = 16 * frag_of(0, wave, j, FD / 16, rot16) + n_of;
+            for (int j = 0; j < FPW_S; ++j) {
+                const int n = 16 * frag_of<NWAVE>(0, wave, j, FD / 16, rot16) + n_of;
                 const float bias = w.out_b[n];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) sX[(m_of + r) * LRES + n] = epi_value<EPI_BIAS>(acc[j][r], bias);
@@ -328,16 +344,16 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
         }
         __syncthreads();
         // ---- LN2 -> split operand
-        ln_rows(sX, w.ln2_w, w.ln2_b, sAh, sAl, wave, lane);
+        ln_rows<RPW>(sX, w.ln2_w, w.ln2_b, sAh, sAl, wave, lane);
         __syncthreads();
         // ---- FF1 (+bias, GELU) -> hidden split (xz region)
 #pragma unroll 1
-        for (int f0 = 0; f0 < 4 * FD / 16; f0 += 4 * NWAVE) {
-            floatx4 acc[4];
-            mgemm<NT, 4, FD, 3>(sAh, sAl, LA, w.ff1_p, f0, 4 * FD / 16, wave, lane, rot64, acc);
+        for (int f0 = 0; f0 < 4 * FD / 16; f0 += FPW_B * NWAVE) {
+            floatx4 acc[FPW_B];
+            mgemm<NT, NWAVE, FPW_B, FD, D_B>(sAh, sAl, LA, w.ff1_p, f0, 4 * FD / 16, wave, lane, rot64, acc);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int n = 16 * frag_of(f0, wave, j, 4 * FD / 16, rot64) + n_of;
+            for (int j = 0; j < FPW_B; ++j) {
+                const int n = 16 * frag_of<NWAVE>(f0, wave, j, 4 * FD / 16, rot64) + n_of;
                 const float bias = w.ff1_b[n];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) put_split(sHh, sHl, (m_of + r) * LH + n, epi_value<EPI_GELU>(acc[j][r], bias));
@@ -346,11 +362,11 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
         __syncthreads();
         // ---- FF2 (+bias) + block residual -> residual stream
         {
-            floatx4 acc[2];
-            mgemm<NT, 2, 4 * FD, 6>(sHh, sHl, LH, w.ff2_p, 0, FD / 16, wave, lane, rot16, acc);
+            floatx4 acc[FPW_S];
+            mgemm<NT, NWAVE, FPW_S, 4 * FD, D_S>(sHh, sHl, LH, w.ff2_p, 0, FD / 16, wave, lane, rot16, acc);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int n = 16 * frag_of(0, wave, j, FD / 16, rot16) + n_of;
+            for (int j = 0; j < FPW_S; ++j) {
+                const int n = 16 * frag_of<NWAVE>(0, wave, j, FD / 16, rot16) + n_of;
                 const float bias = w.ff2_b[n];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
@@ -371,11 +387,11 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
     uint16_t* sGh = sHh;
     uint16_t* sGl = sHh + ROWS * LH1;
     {
-        floatx4 acc[2];
-        mgemm<NT, 2, FD, 6>(sAh, sAl, LA, a.h1_p, 0, FD / 16, wave, lane, rot16, acc);
+        floatx4 acc[FPW_S];
+        mgemm<NT, NWAVE, FPW_S, FD, D_S>(sAh, sAl, LA, a.h1_p, 0, FD / 16, wave, lane, rot16, acc);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int n = 16 * frag_of(0, wave, j, FD / 16, rot16) + n_of;
+        for (int j = 0; j < FPW_S; ++j) {
+            const int n = 16 * frag_of<NWAVE>(0, wave, j, FD / 16, rot16) + n_of;
             const float bias = a.h1_b[n];
 #pragma unroll
             for (int r = 0; r < 4; ++r) put_split(sGh, sGl, (m_of + r) * LH1 + n, epi_value<EPI_RELU>(acc[j][r], bias));
@@ -383,10 +399,10 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
     }
     __syncthreads();
     {
-        floatx4 acc[2];
-        mgemm<NT, 2, FD, 6>(sGh, sGl, LH1, a.h2_p, 0, V / 16, wave, lane, 0, acc);
+        floatx4 acc[FPW_S];
+        mgemm<NT, NWAVE, FPW_S, FD, D_S>(sGh, sGl, LH1, a.h2_p, 0, V / 16, wave, lane, 0, acc);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < FPW_S; ++j) {
             const int f = wave + NWAVE * j;
             if (f < V / 16) {
                 const int n = 16 * f + n_of;
@@ -405,8 +421,8 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
     }
     if (a.decode) {
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const int r = 2 * wave + q;
+        for (int q = 0; q < RPW; ++q) {
+            const int r = RPW * wave + q;
             if (r >= nb) continue;
             const int64_t b = b0 + r;
             if (t >= a.lens[b]) continue;
@@ -431,12 +447,15 @@ bool fused_step_supported(int d_model, int d_state, int dt_rank, int d_conv, int
     return d_model == FD && d_state == FNS && dt_rank == FR && d_conv == 4 && vocab % 16 == 0 && vocab <= 256;
 }
 
-hipError_t launch_fused_step(const FusedArgs& a, int nt, hipStream_t s) {
+hipError_t launch_fused_step(const FusedArgs& a, int nt, int threads, hipStream_t s) {
     const dim3 grid((unsigned)((a.B + ROWS - 1) / ROWS));
-    if (nt == 3)
-        hipLaunchKernelGGL(k_fused_step<3>, grid, dim3(NTHR), 0, s, a);
-    else
-        hipLaunchKernelGGL(k_fused_step<2>, grid, dim3(NTHR), 0, s, a);
+    if (threads == 1024) {
+        if (nt == 3) hipLaunchKernelGGL((k_fused_step<3, 1024>), grid, dim3(1024), 0, s, a);
+        else hipLaunchKernelGGL((k_fused_step<2, 1024>), grid, dim3(1024), 0, s, a);
+    } else {
+        if (nt == 3) hipLaunchKernelGGL((k_fused_step<3, 512>), grid, dim3(512), 0, s, a);
+        else hipLaunchKernelGGL((k_fused_step<2, 512>), grid, dim3(512), 0, s, a);
+    }
     return hipGetLastError();
 }
 

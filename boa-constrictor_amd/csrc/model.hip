@@ -920,6 +920,7 @@ struct boa_ctx {
     int64_t pos = 0;                   // positions processed since the last state reset (conv history ring)
     bool fused = false;                // decompress / step through k_fused_step
     int fused_steps = 128;             // decode steps per k_fused_step launch
+    int fused_threads = 512;           // k_fused_step workgroup size (512 or 1024)
     // k_fused_step workgroup classes (sets of XCDs) start this far apart, so that one class runs its
     // HBM-bound scans while the other streams weights from L2.  Offsets below ~2 layers' time (~250 us at
     // d256x8L, 4096 lanes) do not hold: the follower catches up on the leader's cached weights.
@@ -1215,6 +1216,7 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
         x->fused = fused_step_supported(d, NS, R, x->DC, V) && !(fenv && fenv[0] == '0');
         if (const char* v = getenv("BOA_FUSED_STEPS_PER_LAUNCH")) x->fused_steps = std::max(1, atoi(v));
         if (const char* v = getenv("BOA_FUSED_STAGGER_US")) x->stagger_us = std::max(0, atoi(v));
+        if (const char* v = getenv("BOA_FUSED_THREADS")) x->fused_threads = atoi(v) == 1024 ? 1024 : 512;
         if (const char* v = getenv("BOA_FUSED_STAGGER_CLASSES")) x->stagger_classes = std::min(8, std::max(1, atoi(v)));
         if (x->fused) {
             const bool two = x->prec == BOA_PREC_BF16X3;
@@ -1521,7 +1523,7 @@ extern "C" int boa_model_step(boa_ctx* x, const int32_t* d_tokens, int32_t lanes
         a.logits = d_logits;
         hipError_t e = hipSuccess;
         PROF(PC_FUSED, fused_flops(x, lanes), fused_bytes(x, lanes),
-             e = launch_fused_step(a, x->prec == BOA_PREC_BF16X3 ? 3 : 2, x->stream));
+             e = launch_fused_step(a, x->prec == BOA_PREC_BF16X3 ? 3 : 2, x->fused_threads, x->stream));
         if (e != hipSuccess) return boa_fail_hip(e, "k_fused_step", __FILE__, __LINE__);
         x->pos += 1;
         return BOA_OK;
@@ -1605,7 +1607,7 @@ extern "C" int boa_decompress(boa_ctx* x, const uint32_t* d_payload, const int64
             a.nwords = d_nwords; a.tokens_out = x->tokens; a.out = d_out; a.out_stride = out_stride;
             hipError_t e = hipSuccess;
             PROF(PC_FUSED, a.nsteps * fused_flops(x, lanes), a.nsteps * fused_bytes(x, lanes),
-                 e = launch_fused_step(a, x->prec == BOA_PREC_BF16X3 ? 3 : 2, s));
+                 e = launch_fused_step(a, x->prec == BOA_PREC_BF16X3 ? 3 : 2, x->fused_threads, s));
             if (e != hipSuccess) return boa_fail_hip(e, "k_fused_step", __FILE__, __LINE__);
             x->pos += a.nsteps;
         }

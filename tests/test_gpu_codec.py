@@ -127,3 +127,29 @@ def test_decompress_fused_and_layer_kernels_agree(gpu):
     for out in outs:
         for i, c in enumerate(chunks):
             assert (out[i, :lens[i]] == c).all(), i
+
+
+def test_round_trip_d512_bf16w(gpu):
+    """configs[4] model shape (d_model 512, bf16 weights), 16 layers, mixed int16 / float32 records."""
+    import codec
+    from boa_amd import weights as W
+
+    import model as M
+
+    cfg = W.Cfg(d_model=512, n_layers=16)
+    m = M.BoaConstrictor(512, 16, 256).load_blob(W.seeded_blob(cfg, 1))
+    m.precision = "bf16w"
+    rng = np.random.default_rng(1)
+    n = 3000
+    ints = np.clip(rng.normal(0, 300, n), -32767, 32767).astype(np.int16)
+    flts = rng.lognormal(1.0, 1.5, n).astype(np.float32)
+    rec = np.empty(n, dtype=[("i", "<i2"), ("f", "<f4")])
+    rec["i"], rec["f"] = ints, flts
+    data = rec.tobytes()
+    data = np.frombuffer(data, dtype=np.uint8)
+    L = len(data) // 12
+    chunks = [data[i * L:(i + 1) * L] for i in range(12)]
+    payload, nw, fb, Ls = codec.compress_payload(m, chunks)
+    out = codec.decompress_payload(m, payload, nw, Ls, fb)
+    for i, c in enumerate(chunks):
+        assert (out[i, :L] == c).all(), i
