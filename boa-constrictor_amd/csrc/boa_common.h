@@ -170,11 +170,21 @@ __device__ __forceinline__ void dec_init(DecState& st, const uint32_t* in, int32
     }
 }
 
-// gpu_range_coder.py:191-194
+// gpu_range_coder.py:191-194: q = min(floor((point - lower) / scale), 2^P - 1), scale = range >> P.
+// The exact u64 quotient is obtained without a 64-bit integer division: an fp64 quotient estimate (relative
+// error ~2^-52, so below 1 in absolute terms for q <= 2^P) clamped to [0, 2^P], then one integer
+// correction step.  q_est * scale cannot overflow: q_est <= 2^P and scale < 2^(64 - P).
 __device__ __forceinline__ uint32_t dec_target(const DecState& st, int P) {
     const uint64_t scale = st.range >> P;
-    uint64_t q = scale ? (st.point - st.lower) / scale : 0ull;
-    if (q >= (1ull << P)) q = (1ull << P) - 1ull;
+    if (scale == 0ull) return 0u;
+    const uint64_t d = st.point - st.lower;
+    const uint64_t cap = 1ull << P;
+    const double qd = (double)d / (double)scale;
+    uint64_t q = qd >= (double)cap ? cap : (uint64_t)qd;
+    const uint64_t prod = q * scale;
+    if (prod > d) q -= 1ull;                      // estimate one too high
+    else if (d - prod >= scale && q < cap) q += 1ull;  // estimate one too low
+    if (q >= cap) q = cap - 1ull;
     return (uint32_t)q;
 }
 
