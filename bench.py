@@ -39,10 +39,10 @@ KERNEL_NAMES = {
     ("compress", "gemm_ff1"): "k_gemm_bf<128, 128, 32, 2, 3, true, true>",
     ("compress", "gemm_ff2"): "k_gemm_bf<128, 128, 32, 4, 3, true, false>",
     ("compress", "gemm_out_proj"): "k_gemm_bf<128, 128, 32, 1, 3, true, false>",
-    ("compress", "gemm_x_proj"): "k_gemm_bf<64, 64, 128, 0, 3, false, false>",
+    ("compress", "gemm_x_proj"): "k_xproj<3, 3>",
     ("compress", "scan"): "k_scan<16, 16, true>",
     ("compress", "conv"): "k_conv_silu",
-    ("decompress", "fused_step"): "k_fused_step<3>",
+    ("decompress", "fused_step"): "k_fused_step<3, 512>",
 }
 
 

@@ -41,7 +41,7 @@ constexpr int LH1 = FD + 8;         // head hidden split rows, K = 256
 constexpr int SZ_RES = ROWS * LRES * 4;
 constexpr int SZ_A = 2 * ROWS * LA * 2;
 constexpr int SZ_X = (ROWS * LXZ * 4 > 2 * ROWS * LH * 2) ? ROWS * LXZ * 4 : 2 * ROWS * LH * 2;
-constexpr int SZ_DBC = ROWS * FW * 4;
+constexpr int SZ_DBC = (FDI / XPROJ_KB) * ROWS * FW * 4;  // x_proj partials; dbc in place of the first
 constexpr int OFF_RES = 0;
 constexpr int OFF_A = OFF_RES + SZ_RES;
 constexpr int OFF_X = OFF_A + SZ_A;
@@ -140,19 +140,17 @@ __device__ __forceinline__ void ln_rows(const float* src, const float* __restric
 
 typedef __attribute__((address_space(4))) const FusedArgs KArgs;
 
-// NTHR = 512 (8 waves, 2 per SIMD) or 1024 (16 waves: twice the weight loads in flight per CU, with
-// 128 registers per lane).  The mapping of outputs to waves changes, the arithmetic of each output does not.
+// 512 threads: 8 waves (2 per SIMD); wave w owns channels 64w .. 64w + 63 in the conv and scan phases, which
+// is x_proj's K block w (XPROJ_KB).
 template <int NT, int NTHR>
 __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
     constexpr int NWAVE = NTHR / 64;
     constexpr int RPW = ROWS / NWAVE;               // rows per wave (LN, decode)
-    constexpr int TPC = NTHR / FDI;                 // threads per channel (conv, scan)
-    constexpr int RPT = ROWS / TPC;                 // rows per thread (conv, scan)
-    constexpr int FPW_B = NWAVE == 8 ? 4 : 2;       // fragments per wave, N = 1024 GEMMs (per pass)
+    constexpr int FPW_B = 4;                        // fragments per wave, N = 1024 GEMMs (per pass)
     constexpr int D_B = 3;         // K steps in flight, N = 1024 GEMMs
     constexpr int FPW_S = 16 / NWAVE;               // fragments per wave, N = 256 GEMMs
     constexpr int D_S = 6;         // K steps in flight, N = 256 GEMMs
-    static_assert(NTHR == 512 || NTHR == 1024, "fused step block size");
+    static_assert(NTHR == 512 && NTHR == FDI && NWAVE * XPROJ_KB == FDI, "fused step block size: one thread per channel");
     __shared__ __attribute__((aligned(16))) unsigned char lds[LDS_BYTES];
     float* sRes = reinterpret_cast<float*>(lds + OFF_RES);
     uint16_t* sAh = reinterpret_cast<uint16_t*>(lds + OFF_A);
@@ -160,7 +158,8 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
     float* sX = reinterpret_cast<float*>(lds + OFF_X);
     uint16_t* sHh = reinterpret_cast<uint16_t*>(lds + OFF_X);
     uint16_t* sHl = sHh + ROWS * LH;
-    float* sDbc = reinterpret_cast<float*>(lds + OFF_DBC);
+    float* sPart = reinterpret_cast<float*>(lds + OFF_DBC);  // x_proj partials [8][ROWS][FW]
+    float* sDbc = sPart;                                      // their sum, in place of the first
     float* sLog = reinterpret_cast<float*>(lds + OFF_A);  // head output (operand region is free by then)
 
     __shared__ int sTok[ROWS];
@@ -239,47 +238,82 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
             }
         }
         __syncthreads();
-        // ---- conv + SiLU (thread = channel x row range): xs fp32 in place of x, split operand for x_proj,
-        //      history ring
+        // ---- conv + SiLU (thread = channel): xs fp32 in place of x, split operand, history ring; then this
+        //      wavefront's x_proj partial P_wave over the 64 channels it has just produced (XPROJ_KB)
         {
-            const int c = tid % FDI, rb = TPC == 1 ? 0 : __builtin_amdgcn_readfirstlane(tid / FDI) * RPT;
+            // x_proj weight blocks of this wave's K block, issued first (they do not depend on the step)
+            constexpr int XS = FDI / 32, XF = FW / 16, XBLK = (NT == 3) ? 1024 : 512;
+            uint4 xwh[XF][2], xwl[XF][2];
+#pragma unroll
+            for (int f = 0; f < XF; ++f)
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    const uint16_t* p = w.x_p + ((int64_t)f * XS + 2 * wave + s) * XBLK + lane * 8;
+                    xwh[f][s] = *reinterpret_cast<const uint4*>(p);
+                    xwl[f][s] = xwh[f][s];
+                    if constexpr (NT == 3) xwl[f][s] = *reinterpret_cast<const uint4*>(p + 512);
+                }
+            const int c = tid;
             const float4 cw = *reinterpret_cast<const float4*>(w.conv_w + 4 * c);
             const float cb = w.conv_b[c];
             float* hl = a.hist + (int64_t)l * a.max_lanes * 3 * FDI;
-            float h0[RPT], h1[RPT], h2[RPT];
+            float h0[ROWS], h1[ROWS], h2[ROWS];
 #pragma unroll
-            for (int q = 0; q < RPT; ++q) {
-                const int r = rb + q;
-                h0[q] = h1[q] = h2[q] = 0.0f;
+            for (int r = 0; r < ROWS; ++r) {
+                h0[r] = h1[r] = h2[r] = 0.0f;
                 if (r < nb) {
                     const float* hb = hl + (b0 + r) * 3 * FDI;
-                    h0[q] = hb[p0m3 * FDI + c];
-                    h1[q] = hb[s1 * FDI + c];
-                    h2[q] = hb[s2 * FDI + c];
+                    h0[r] = hb[p0m3 * FDI + c];
+                    h1[r] = hb[s1 * FDI + c];
+                    h2[r] = hb[s2 * FDI + c];
                 }
             }
 #pragma unroll
-            for (int q = 0; q < RPT; ++q) {
-                const int r = rb + q;
+            for (int r = 0; r < ROWS; ++r) {
                 const float x = sX[r * LXZ + c];
-                const float y = conv_point(cw, cb, h0[q], h1[q], h2[q], x);
+                const float y = conv_point(cw, cb, h0[r], h1[r], h2[r], x);
                 sX[r * LXZ + c] = y;
                 put_split(sAh, sAl, r * LA + c, y);
                 if (r < nb) hl[(b0 + r) * 3 * FDI + p0m3 * FDI + c] = x;
             }
-        }
-        __syncthreads();
-        // ---- x_proj -> [dt | B | C] rows
-        if (wave < FW / 16) {
-            floatx4 acc[1];
-            mgemm<NT, NWAVE, 1, FDI, 8>(sAh, sAl, LA, w.x_p, 0, FW / 16, wave, lane, 0, acc);
+            // the partial reads only split values this wavefront wrote (channels 64 wave .. 64 wave + 63 of
+            // every row); LDS operations of one wavefront complete in order
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const int ar = lane & 15, kq = 8 * (lane >> 4);
+            floatx4 part[XF];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) sDbc[(m_of + r) * FW + 16 * wave + n_of] = acc[0][r];
+            for (int f = 0; f < XF; ++f) part[f] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                const int k0 = XPROJ_KB * wave + 32 * s;
+                const bf16x8 ah = *reinterpret_cast<const bf16x8*>(sAh + ar * LA + k0 + kq);
+                const bf16x8 al = *reinterpret_cast<const bf16x8*>(sAl + ar * LA + k0 + kq);
+#pragma unroll
+                for (int f = 0; f < XF; ++f)
+                    part[f] = mfma_split_step<NT>(part[f], ah, al, __builtin_bit_cast(bf16x8, xwh[f][s]),
+                                                  __builtin_bit_cast(bf16x8, xwl[f][s]));
+            }
+            float* pw = sPart + wave * (ROWS * FW);
+#pragma unroll
+            for (int f = 0; f < XF; ++f)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) pw[(m_of + r) * FW + 16 * f + n_of] = part[f][r];
         }
         __syncthreads();
-        // ---- dt_proj + softplus + selective scan + D + gate (thread = channel x row range) -> y split operand
+        // ---- x_proj fold: dbc = P_0 + P_1 + ... + P_7, in place of P_0 (element i is read and written by
+        //      one thread only)
+        for (int i = tid; i < ROWS * FW; i += NTHR) {
+            float v = sPart[i];
+#pragma unroll
+            for (int q = 1; q < FDI / XPROJ_KB; ++q) v = v + sPart[q * (ROWS * FW) + i];
+            sDbc[i] = v;
+        }
+        __syncthreads();
+        // ---- dt_proj + softplus + selective scan + D + gate (thread = channel) -> y split operand
         {
-            const int c = tid % FDI, rb = TPC == 1 ? 0 : __builtin_amdgcn_readfirstlane(tid / FDI) * RPT;
+            const int c = tid;
             float av[FNS], wr[FR];
             const float* Ag = w.Aneg;
 #pragma unroll
@@ -294,10 +328,9 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
             }
             const float bdt = w.dt_b[c], Dc = w.D[c];
             float* sl = a.ssm + (int64_t)l * a.max_lanes * FDI * FNS + 4 * c;
-            constexpr int PD = NTHR == 512 ? 4 : 3;  // lanes of state in flight
+            constexpr int PD = 4;  // lanes of state in flight
             float hr[PD][FNS];
-            auto load_h = [&](int q, float (&h)[FNS]) {
-                const int r = rb + q;
+            auto load_h = [&](int r, float (&h)[FNS]) {
                 if (r < nb) {
                     const float* hp = sl + (b0 + r) * FDI * FNS;
 #pragma unroll
@@ -313,10 +346,9 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
 #pragma unroll
             for (int q = 0; q < PD - 1; ++q) load_h(q, hr[q]);
 #pragma unroll
-            for (int q = 0; q < RPT; ++q) {
-                if (q + PD - 1 < RPT) load_h(q + PD - 1, hr[(q + PD - 1) % PD]);
-                float (&h)[FNS] = hr[q % PD];
-                const int r = rb + q;
+            for (int r = 0; r < ROWS; ++r) {
+                if (r + PD - 1 < ROWS) load_h(r + PD - 1, hr[(r + PD - 1) % PD]);
+                float (&h)[FNS] = hr[r % PD];
                 const float x = sX[r * LXZ + c], z = sX[r * LXZ + FDI + c];
                 const float y = scan_position<FNS, FR>(sDbc + r * FW, wr, bdt, av, Dc, x, z, h);
                 put_split(sAh, sAl, r * LA + c, y);
@@ -447,15 +479,10 @@ bool fused_step_supported(int d_model, int d_state, int dt_rank, int d_conv, int
     return d_model == FD && d_state == FNS && dt_rank == FR && d_conv == 4 && vocab % 16 == 0 && vocab <= 256;
 }
 
-hipError_t launch_fused_step(const FusedArgs& a, int nt, int threads, hipStream_t s) {
+hipError_t launch_fused_step(const FusedArgs& a, int nt, hipStream_t s) {
     const dim3 grid((unsigned)((a.B + ROWS - 1) / ROWS));
-    if (threads == 1024) {
-        if (nt == 3) hipLaunchKernelGGL((k_fused_step<3, 1024>), grid, dim3(1024), 0, s, a);
-        else hipLaunchKernelGGL((k_fused_step<2, 1024>), grid, dim3(1024), 0, s, a);
-    } else {
-        if (nt == 3) hipLaunchKernelGGL((k_fused_step<3, 512>), grid, dim3(512), 0, s, a);
-        else hipLaunchKernelGGL((k_fused_step<2, 512>), grid, dim3(512), 0, s, a);
-    }
+    if (nt == 3) hipLaunchKernelGGL((k_fused_step<3, 512>), grid, dim3(512), 0, s, a);
+    else hipLaunchKernelGGL((k_fused_step<2, 512>), grid, dim3(512), 0, s, a);
     return hipGetLastError();
 }
 

@@ -616,28 +616,93 @@ __global__ void __launch_bounds__(256) k_convx_step(const float* __restrict__ xz
     const int i = lane & 15, kq = 8 * (lane >> 4);
     const int n = wave * 16 + i;
     floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 0; k0 < di; k0 += 32) {
-        const float* xa = &sX[i * LDX + k0 + kq];
-        uint32_t hh[8], ll[8];
+    for (int q = 0; q < di / XPROJ_KB; ++q) {
+        floatx4 part = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int e = 0; e < 8; ++e) split2(xa[e], hh[e], ll[e]);
-        const uint4 ah4 = make_uint4(hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16), hh[4] | (hh[5] << 16), hh[6] | (hh[7] << 16));
-        const uint4 al4 = make_uint4(ll[0] | (ll[1] << 16), ll[2] | (ll[3] << 16), ll[4] | (ll[5] << 16), ll[6] | (ll[7] << 16));
-        const bf16x8 ah = __builtin_bit_cast(bf16x8, ah4);
-        const bf16x8 al = __builtin_bit_cast(bf16x8, al4);
-        const bf16x8 bh = *reinterpret_cast<const bf16x8*>(Wh + (int64_t)n * di + k0 + kq);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
-        if constexpr (NT == 3) {
-            const bf16x8 bl = *reinterpret_cast<const bf16x8*>(Wl + (int64_t)n * di + k0 + kq);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
+        for (int k0 = XPROJ_KB * q; k0 < XPROJ_KB * (q + 1); k0 += 32) {
+            const float* xa = &sX[i * LDX + k0 + kq];
+            bf16x8 ah, al;
+            split8(xa, ah, al);
+            const bf16x8 bh = *reinterpret_cast<const bf16x8*>(Wh + (int64_t)n * di + k0 + kq);
+            bf16x8 bl = bh;
+            if constexpr (NT == 3) bl = *reinterpret_cast<const bf16x8*>(Wl + (int64_t)n * di + k0 + kq);
+            part = mfma_split_step<NT>(part, ah, al, bh, bl);
         }
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
+        acc = q == 0 ? part : acc + part;
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int64_t b = b0 + 4 * (lane >> 4) + r;
         if (b < B) dbc[b * ldd + wave * 16 + (lane & 15)] = acc[r];
     }
+}
+
+// x_proj over M rows in the split modes (compress tiles): one wavefront per 16 rows computes all NF output
+// fragments, A = xs fp32 [M][di] split on load, W [N][K] bf16 parts.  Outputs follow the K-block fold of
+// XPROJ_KB (P_q from zero over the two K steps of block q, then dbc = P_0 + P_1 + ...), like k_convx_step and
+// the fused decode kernel, so a position's dbc row is the same in all three.  Row m of the output depends on
+// row m of A only.
+template <int NT, int NF>
+__global__ void __launch_bounds__(256) k_xproj(const float* __restrict__ xs, int64_t M, int di,
+                                              const uint16_t* __restrict__ Wh, const uint16_t* __restrict__ Wl,
+                                              float* __restrict__ dbc, int ldd) {
+    const int lane = threadIdx.x & 63;
+    const int64_t m0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 16;
+    if (m0 >= M) return;
+    const int ar = lane & 15, kq = 8 * (lane >> 4);
+    const bool ok = m0 + ar < M;
+    const float* xr = xs + (m0 + ar) * di + kq;
+    floatx4 acc[NF];
+    for (int q = 0; q < di / XPROJ_KB; ++q) {
+        floatx4 part[NF];
+#pragma unroll
+        for (int f = 0; f < NF; ++f) part[f] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < XPROJ_KB / 32; ++s) {
+            const int k0 = XPROJ_KB * q + 32 * s;
+            float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            if (ok) {
+                const float4 a0 = *reinterpret_cast<const float4*>(xr + k0);
+                const float4 a1 = *reinterpret_cast<const float4*>(xr + k0 + 4);
+                v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w; v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
+            }
+            bf16x8 ah, al;
+            split8(v, ah, al);
+#pragma unroll
+            for (int f = 0; f < NF; ++f) {
+                const int64_t wo = (int64_t)(16 * f + ar) * di + k0 + kq;
+                const bf16x8 bh = *reinterpret_cast<const bf16x8*>(Wh + wo);
+                bf16x8 bl = bh;
+                if constexpr (NT == 3) bl = *reinterpret_cast<const bf16x8*>(Wl + wo);
+                part[f] = mfma_split_step<NT>(part[f], ah, al, bh, bl);
+            }
+        }
+#pragma unroll
+        for (int f = 0; f < NF; ++f) acc[f] = q == 0 ? part[f] : acc[f] + part[f];
+    }
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t row = m0 + 4 * (lane >> 4) + r;
+            if (row < M) dbc[row * ldd + 16 * f + ar] = acc[f][r];
+        }
+}
+
+static int launch_xproj(const float* xs, int64_t M, int di, const uint16_t* Wh, const uint16_t* Wl, float* dbc, int ldd,
+                        hipStream_t s) {
+    const unsigned grid = (unsigned)((M + 63) / 64);
+    if (di % XPROJ_KB != 0) return boa_fail(BOA_ERR_ARG, "internal: d_inner %d not a multiple of %d", di, XPROJ_KB);
+    if (ldd == 48) {
+        if (Wl) hipLaunchKernelGGL((k_xproj<3, 3>), dim3(grid), dim3(256), 0, s, xs, M, di, Wh, Wl, dbc, ldd);
+        else hipLaunchKernelGGL((k_xproj<2, 3>), dim3(grid), dim3(256), 0, s, xs, M, di, Wh, Wl, dbc, ldd);
+    } else if (ldd == 64) {
+        if (Wl) hipLaunchKernelGGL((k_xproj<3, 4>), dim3(grid), dim3(256), 0, s, xs, M, di, Wh, Wl, dbc, ldd);
+        else hipLaunchKernelGGL((k_xproj<2, 4>), dim3(grid), dim3(256), 0, s, xs, M, di, Wh, Wl, dbc, ldd);
+    } else {
+        return boa_fail(BOA_ERR_ARG, "internal: x_proj width %d not supported (48 or 64)", ldd);
+    }
+    return BOA_OK;
 }
 
 // ================================================================================================
@@ -920,7 +985,6 @@ struct boa_ctx {
     int64_t pos = 0;                   // positions processed since the last state reset (conv history ring)
     bool fused = false;                // decompress / step through k_fused_step
     int fused_steps = 128;             // decode steps per k_fused_step launch
-    int fused_threads = 512;           // k_fused_step workgroup size (512 or 1024)
     // k_fused_step workgroup classes (sets of XCDs) start this far apart, so that one class runs its
     // HBM-bound scans while the other streams weights from L2.  Offsets below ~2 layers' time (~250 us at
     // d256x8L, 4096 lanes) do not hold: the follower catches up on the leader's cached weights.
@@ -1216,7 +1280,6 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
         x->fused = fused_step_supported(d, NS, R, x->DC, V) && !(fenv && fenv[0] == '0');
         if (const char* v = getenv("BOA_FUSED_STEPS_PER_LAUNCH")) x->fused_steps = std::max(1, atoi(v));
         if (const char* v = getenv("BOA_FUSED_STAGGER_US")) x->stagger_us = std::max(0, atoi(v));
-        if (const char* v = getenv("BOA_FUSED_THREADS")) x->fused_threads = atoi(v) == 1024 ? 1024 : 512;
         if (const char* v = getenv("BOA_FUSED_STAGGER_CLASSES")) x->stagger_classes = std::min(8, std::max(1, atoi(v)));
         if (x->fused) {
             const bool two = x->prec == BOA_PREC_BF16X3;
@@ -1381,7 +1444,7 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc) {
     {
         GemmArgs g = gemm_args(x->xs, di, w.x_w, nullptr, x->dbc, R + 2 * NS, M, R + 2 * NS, di);
         PROF(PC_XPROJ, gemm_flops(M, R + 2 * NS, di), gemm_bytes(M, R + 2 * NS, di),
-             rc = split ? (launch_gemm_bf<EPI_NONE, false, false>(g, s))
+             rc = split ? launch_xproj(x->xs, M, di, w.x_w.h, w.x_w.l, x->dbc, R + 2 * NS, s)
                         : (launch_gemm_f32_cfg<64, 64, 0, EPI_NONE>(g, s)));
         if (rc) return rc;
     }
@@ -1523,7 +1586,7 @@ extern "C" int boa_model_step(boa_ctx* x, const int32_t* d_tokens, int32_t lanes
         a.logits = d_logits;
         hipError_t e = hipSuccess;
         PROF(PC_FUSED, fused_flops(x, lanes), fused_bytes(x, lanes),
-             e = launch_fused_step(a, x->prec == BOA_PREC_BF16X3 ? 3 : 2, x->fused_threads, x->stream));
+             e = launch_fused_step(a, x->prec == BOA_PREC_BF16X3 ? 3 : 2, x->stream));
         if (e != hipSuccess) return boa_fail_hip(e, "k_fused_step", __FILE__, __LINE__);
         x->pos += 1;
         return BOA_OK;
@@ -1607,7 +1670,7 @@ extern "C" int boa_decompress(boa_ctx* x, const uint32_t* d_payload, const int64
             a.nwords = d_nwords; a.tokens_out = x->tokens; a.out = d_out; a.out_stride = out_stride;
             hipError_t e = hipSuccess;
             PROF(PC_FUSED, a.nsteps * fused_flops(x, lanes), a.nsteps * fused_bytes(x, lanes),
-                 e = launch_fused_step(a, x->prec == BOA_PREC_BF16X3 ? 3 : 2, x->fused_threads, s));
+                 e = launch_fused_step(a, x->prec == BOA_PREC_BF16X3 ? 3 : 2, s));
             if (e != hipSuccess) return boa_fail_hip(e, "k_fused_step", __FILE__, __LINE__);
             x->pos += a.nsteps;
         }

@@ -42,6 +42,17 @@ __device__ __forceinline__ void split2(float f, uint32_t& hi, uint32_t& lo) {
     lo = bf16_rne(f - __uint_as_float(hi << 16));
 }
 
+// Eight consecutive fp32 values as split bf16 operands (hi, lo) of one MFMA K slice.
+__device__ __forceinline__ void split8(const float* v, bf16x8& ah, bf16x8& al) {
+    uint32_t hh[8], ll[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) split2(v[e], hh[e], ll[e]);
+    ah = __builtin_bit_cast(bf16x8, make_uint4(hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16), hh[4] | (hh[5] << 16),
+                                               hh[6] | (hh[7] << 16)));
+    al = __builtin_bit_cast(bf16x8, make_uint4(ll[0] | (ll[1] << 16), ll[2] | (ll[3] << 16), ll[4] | (ll[5] << 16),
+                                               ll[6] | (ll[7] << 16)));
+}
+
 // LayerNorm statistics of a row of 256 * LNV values held by one wavefront, lane j holding elements
 // 256 * i + 4j .. 256 * i + 4j + 3 in v[4i .. 4i + 3].  Biased variance, eps 1e-5 (nn.LayerNorm).
 template <int LNV>
@@ -63,6 +74,23 @@ __device__ __forceinline__ void ln_stats_row(const float (&v)[4 * LNV], float& m
 }
 
 __device__ __forceinline__ float ln_apply(float v, float mu, float rs, float w, float b) { return ((v - mu) * rs) * w + b; }
+
+// One 32-wide K step of a split-precision product into acc: a = ah + al (activations), w = bh (+ bl): the
+// products lo*hi, hi*lo (NT = 3 only), hi*hi, in this order.  Every split-mode GEMM accumulates its K steps
+// through this sequence.
+template <int NT>
+__device__ __forceinline__ floatx4 mfma_split_step(floatx4 acc, bf16x8 ah, bf16x8 al, bf16x8 bh, bf16x8 bl) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
+    if constexpr (NT == 3) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
+}
+
+// x_proj (d_inner -> dt_rank + 2 d_state) in the split modes is a sum of K-block partials:
+//   dbc = P_0 + P_1 + ... + P_{d_inner/64 - 1}   (left to right, fp32 adds)
+// where P_q accumulates the two 32-wide K steps of channels 64q .. 64q + 63 from zero.  The fused decode
+// kernel computes P_q in the wavefront that produced those channels' conv outputs, so x_proj starts without
+// a workgroup barrier; the compress and per-layer decode paths compute the same partials and the same fold.
+constexpr int XPROJ_KB = 64;
 
 // Depthwise causal conv (d_conv = 4) + bias + SiLU of one channel at one position:
 // xc = b + w0*x[t-3] + w1*x[t-2] + w2*x[t-1] + w3*x[t] (model.py:72, PyTorch Conv1d cross-correlation).

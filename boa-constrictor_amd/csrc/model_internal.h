@@ -52,7 +52,7 @@ struct FusedArgs {
 // Supported shape of the fused kernel: d_model 256, d_state 16, dt_rank 16, d_conv 4, vocab % 16 == 0.
 bool fused_step_supported(int d_model, int d_state, int dt_rank, int d_conv, int vocab);
 
-// nt = 3 (bf16x3 weights, hi + lo) or 2 (bf16 weights); threads = 512 or 1024 per workgroup
-hipError_t launch_fused_step(const FusedArgs& a, int nt, int threads, hipStream_t s);
+// nt = 3 (bf16x3 weights, hi + lo) or 2 (bf16 weights); 512 threads per workgroup of 16 lanes
+hipError_t launch_fused_step(const FusedArgs& a, int nt, hipStream_t s);
 
 }  // namespace boa
