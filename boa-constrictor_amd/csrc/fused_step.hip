@@ -80,9 +80,9 @@ __device__ __forceinline__ void mgemm(const uint16_t* sAh, const uint16_t* sAl, 
         for (int j = 0; j < FPW; ++j) {
             if (fw + NWAVE * j < nfrag) {
                 const int f = frag_of<NWAVE>(f0, wave, j, nfrag, rot);
-                const uint16_t* p = Wp + ((int64_t)f * S + s) * BLK + lane * 8;
-                bh[slot][j] = *reinterpret_cast<const uint4*>(p);
-                if constexpr (NT == 3) bl[slot][j] = *reinterpret_cast<const uint4*>(p + 512);
+                const gptr<uint16_t> p = G(Wp) + ((int64_t)f * S + s) * BLK + lane * 8;
+                bh[slot][j] = __builtin_bit_cast(uint4, ldg16(p));
+                if constexpr (NT == 3) bl[slot][j] = __builtin_bit_cast(uint4, ldg16(p + 512));
             }
         }
     };
@@ -119,8 +119,8 @@ __device__ __forceinline__ void put_split(uint16_t* h, uint16_t* l, int idx, flo
 template <int RPW>
 __device__ __forceinline__ void ln_rows(const float* src, const float* __restrict__ w, const float* __restrict__ b,
                                        uint16_t* sAh, uint16_t* sAl, int wave, int lane) {
-    const float4 wv = *reinterpret_cast<const float4*>(w + 4 * lane);
-    const float4 bv = *reinterpret_cast<const float4*>(b + 4 * lane);
+    const float4 wv = ldg_f4(G(w) + 4 * lane);
+    const float4 bv = ldg_f4(G(b) + 4 * lane);
 #pragma unroll
     for (int q = 0; q < RPW; ++q) {
         const int r = RPW * wave + q;
@@ -211,7 +211,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
         if (r < nb) {
             int tok = sTok[r];
             tok = tok < 0 ? 0 : (tok >= V ? V - 1 : tok);
-            v = *reinterpret_cast<const float4*>(a.emb + (int64_t)tok * FD + c4);
+            v = ldg_f4(G(a.emb) + (int64_t)tok * FD + c4);
         }
         *reinterpret_cast<float4*>(sRes + r * LRES + c4) = v;
     }
@@ -232,7 +232,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
 #pragma unroll
             for (int j = 0; j < FPW_B; ++j) {
                 const int n = 16 * frag_of<NWAVE>(f0, wave, j, 2 * FDI / 16, rot64) + n_of;
-                const float bias = w.in_b[n];
+                const float bias = G(w.in_b)[n];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) sX[(m_of + r) * LXZ + n] = epi_value<EPI_BIAS>(acc[j][r], bias);
             }
@@ -248,21 +248,21 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
             for (int f = 0; f < XF; ++f)
 #pragma unroll
                 for (int s = 0; s < 2; ++s) {
-                    const uint16_t* p = w.x_p + ((int64_t)f * XS + 2 * wave + s) * XBLK + lane * 8;
-                    xwh[f][s] = *reinterpret_cast<const uint4*>(p);
+                    const gptr<uint16_t> p = G(w.x_p) + ((int64_t)f * XS + 2 * wave + s) * XBLK + lane * 8;
+                    xwh[f][s] = __builtin_bit_cast(uint4, ldg16(p));
                     xwl[f][s] = xwh[f][s];
-                    if constexpr (NT == 3) xwl[f][s] = *reinterpret_cast<const uint4*>(p + 512);
+                    if constexpr (NT == 3) xwl[f][s] = __builtin_bit_cast(uint4, ldg16(p + 512));
                 }
             const int c = tid;
-            const float4 cw = *reinterpret_cast<const float4*>(w.conv_w + 4 * c);
-            const float cb = w.conv_b[c];
-            float* hl = a.hist + (int64_t)l * a.max_lanes * 3 * FDI;
+            const float4 cw = ldg_f4(G(w.conv_w) + 4 * c);
+            const float cb = G(w.conv_b)[c];
+            const gmut<float> hl = GM(a.hist) + (int64_t)l * a.max_lanes * 3 * FDI;
             float h0[ROWS], h1[ROWS], h2[ROWS];
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) {
                 h0[r] = h1[r] = h2[r] = 0.0f;
                 if (r < nb) {
-                    const float* hb = hl + (b0 + r) * 3 * FDI;
+                    const gptr<float> hb = hl + (b0 + r) * 3 * FDI;
                     h0[r] = hb[p0m3 * FDI + c];
                     h1[r] = hb[s1 * FDI + c];
                     h2[r] = hb[s2 * FDI + c];
@@ -315,27 +315,27 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
         {
             const int c = tid;
             float av[FNS], wr[FR];
-            const float* Ag = w.Aneg;
+            const gptr<float> Ag = G(w.Aneg);
 #pragma unroll
             for (int n = 0; n < FNS; n += 4) {
-                const float4 p = *reinterpret_cast<const float4*>(Ag + ((int64_t)(n / 4) * FDI + c) * 4);
+                const float4 p = ldg_f4(Ag + ((int64_t)(n / 4) * FDI + c) * 4);
                 av[n] = p.x; av[n + 1] = p.y; av[n + 2] = p.z; av[n + 3] = p.w;
             }
 #pragma unroll
             for (int r = 0; r < FR; r += 4) {
-                const float4 q = *reinterpret_cast<const float4*>(w.dt_w + (int64_t)c * FR + r);
+                const float4 q = ldg_f4(G(w.dt_w) + (int64_t)c * FR + r);
                 wr[r] = q.x; wr[r + 1] = q.y; wr[r + 2] = q.z; wr[r + 3] = q.w;
             }
-            const float bdt = w.dt_b[c], Dc = w.D[c];
-            float* sl = a.ssm + (int64_t)l * a.max_lanes * FDI * FNS + 4 * c;
+            const float bdt = G(w.dt_b)[c], Dc = G(w.D)[c];
+            const gmut<float> sl = GM(a.ssm) + (int64_t)l * a.max_lanes * FDI * FNS + 4 * c;
             constexpr int PD = 4;  // lanes of state in flight
             float hr[PD][FNS];
             auto load_h = [&](int r, float (&h)[FNS]) {
                 if (r < nb) {
-                    const float* hp = sl + (b0 + r) * FDI * FNS;
+                    const gptr<float> hp = sl + (b0 + r) * FDI * FNS;
 #pragma unroll
                     for (int n = 0; n < FNS; n += 4) {
-                        const float4 q = *reinterpret_cast<const float4*>(hp + (int64_t)(n / 4) * FDI * 4);
+                        const float4 q = ldg_f4(hp + (int64_t)(n / 4) * FDI * 4);
                         h[n] = q.x; h[n + 1] = q.y; h[n + 2] = q.z; h[n + 3] = q.w;
                     }
                 } else {
@@ -353,11 +353,10 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
                 const float y = scan_position<FNS, FR>(sDbc + r * FW, wr, bdt, av, Dc, x, z, h);
                 put_split(sAh, sAl, r * LA + c, y);
                 if (r < nb) {
-                    float* hp = sl + (b0 + r) * FDI * FNS;
+                    const gmut<float> hp = sl + (b0 + r) * FDI * FNS;
 #pragma unroll
                     for (int n = 0; n < FNS; n += 4)
-                        *reinterpret_cast<float4*>(hp + (int64_t)(n / 4) * FDI * 4) =
-                            make_float4(h[n], h[n + 1], h[n + 2], h[n + 3]);
+                        stg_f4(hp + (int64_t)(n / 4) * FDI * 4, make_float4(h[n], h[n + 1], h[n + 2], h[n + 3]));
                 }
             }
         }
@@ -369,7 +368,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
 #pragma unroll
             for (int j = 0; j < FPW_S; ++j) {
                 const int n = 16 * frag_of<NWAVE>(0, wave, j, FD / 16, rot16) + n_of;
-                const float bias = w.out_b[n];
+                const float bias = G(w.out_b)[n];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) sX[(m_of + r) * LRES + n] = epi_value<EPI_BIAS>(acc[j][r], bias);
             }
@@ -386,7 +385,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
 #pragma unroll
             for (int j = 0; j < FPW_B; ++j) {
                 const int n = 16 * frag_of<NWAVE>(f0, wave, j, 4 * FD / 16, rot64) + n_of;
-                const float bias = w.ff1_b[n];
+                const float bias = G(w.ff1_b)[n];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) put_split(sHh, sHl, (m_of + r) * LH + n, epi_value<EPI_GELU>(acc[j][r], bias));
             }
@@ -399,7 +398,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
 #pragma unroll
             for (int j = 0; j < FPW_S; ++j) {
                 const int n = 16 * frag_of<NWAVE>(0, wave, j, FD / 16, rot16) + n_of;
-                const float bias = w.ff2_b[n];
+                const float bias = G(w.ff2_b)[n];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int idx = (m_of + r) * LRES + n;
@@ -424,7 +423,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
 #pragma unroll
         for (int j = 0; j < FPW_S; ++j) {
             const int n = 16 * frag_of<NWAVE>(0, wave, j, FD / 16, rot16) + n_of;
-            const float bias = a.h1_b[n];
+            const float bias = G(a.h1_b)[n];
 #pragma unroll
             for (int r = 0; r < 4; ++r) put_split(sGh, sGl, (m_of + r) * LH1 + n, epi_value<EPI_RELU>(acc[j][r], bias));
         }
@@ -438,7 +437,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
             const int f = wave + NWAVE * j;
             if (f < V / 16) {
                 const int n = 16 * f + n_of;
-                const float bias = a.h2_b[n];
+                const float bias = G(a.h2_b)[n];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) sLog[(m_of + r) * LRES + n] = epi_value<EPI_BIAS>(acc[j][r], bias);
             }

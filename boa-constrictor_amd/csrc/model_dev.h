@@ -11,6 +11,25 @@ namespace boa {
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
+// Pointers into device global memory (address space 1).  A pointer the kernel reads from memory (a per-layer
+// table, say) is generic to the compiler, which then emits FLAT loads; FLAT loads also count against the LDS
+// counter, so every wait on an LDS read would also wait on them.  Casting to the global space gives global
+// loads and stores.
+template <class T> using gptr = __attribute__((address_space(1))) const T*;
+template <class T> using gmut = __attribute__((address_space(1))) T*;
+template <class T> __device__ __forceinline__ gptr<T> G(const T* p) { return (gptr<T>)p; }
+template <class T> __device__ __forceinline__ gmut<T> GM(T* p) { return (gmut<T>)p; }
+// 16-byte global loads and stores through native vector types (HIP's float4 / uint4 are classes, whose
+// members cannot be used on an address-space-qualified object)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+template <class T> __device__ __forceinline__ u32x4 ldg16(gptr<T> p) { return *(gptr<u32x4>)p; }
+template <class T> __device__ __forceinline__ float4 ldg_f4(gptr<T> p) {
+    const f32x4 v = *(gptr<f32x4>)p;
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+template <class T> __device__ __forceinline__ void stg_f4(gmut<T> p, float4 v) { *(gmut<f32x4>)p = f32x4{v.x, v.y, v.z, v.w}; }
+
 // GEMM epilogues: none | +bias | +bias,GELU(erf) | +bias,ReLU | residual + (acc + bias)
 enum { EPI_NONE = 0, EPI_BIAS = 1, EPI_GELU = 2, EPI_RELU = 3, EPI_RESID = 4 };
 
