@@ -256,17 +256,17 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
             const int c = tid;
             const float4 cw = ldg_f4(G(w.conv_w) + 4 * c);
             const float cb = G(w.conv_b)[c];
-            const gmut<float> hl = GM(a.hist) + (int64_t)l * a.max_lanes * 3 * FDI;
+            // history ring of this workgroup's valid lanes [b0, b0 + nb): rows past the last lane read 0 and
+            // are not written (buffer range check), so no access is under a branch
+            const __amdgpu_buffer_rsrc_t hr3 =
+                buf_rsrc(a.hist + ((int64_t)l * a.max_lanes + b0) * 3 * FDI, (uint32_t)nb * 3 * FDI * 4);
             float h0[ROWS], h1[ROWS], h2[ROWS];
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) {
-                h0[r] = h1[r] = h2[r] = 0.0f;
-                if (r < nb) {
-                    const gptr<float> hb = hl + (b0 + r) * 3 * FDI;
-                    h0[r] = hb[p0m3 * FDI + c];
-                    h1[r] = hb[s1 * FDI + c];
-                    h2[r] = hb[s2 * FDI + c];
-                }
+                const uint32_t o = (uint32_t)(r * 3 * FDI + c) * 4;
+                h0[r] = buf_ld1(hr3, o + p0m3 * FDI * 4);
+                h1[r] = buf_ld1(hr3, o + s1 * FDI * 4);
+                h2[r] = buf_ld1(hr3, o + s2 * FDI * 4);
             }
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) {
@@ -274,7 +274,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
                 const float y = conv_point(cw, cb, h0[r], h1[r], h2[r], x);
                 sX[r * LXZ + c] = y;
                 put_split(sAh, sAl, r * LA + c, y);
-                if (r < nb) hl[(b0 + r) * 3 * FDI + p0m3 * FDI + c] = x;
+                buf_st1(hr3, (uint32_t)(r * 3 * FDI + p0m3 * FDI + c) * 4, x);
             }
             // the partial reads only split values this wavefront wrote (channels 64 wave .. 64 wave + 63 of
             // every row); LDS operations of one wavefront complete in order
@@ -327,37 +327,37 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
                 wr[r] = q.x; wr[r + 1] = q.y; wr[r + 2] = q.z; wr[r + 3] = q.w;
             }
             const float bdt = G(w.dt_b)[c], Dc = G(w.D)[c];
-            const gmut<float> sl = GM(a.ssm) + (int64_t)l * a.max_lanes * FDI * FNS + 4 * c;
+            // SSM state of this workgroup's valid lanes [b0, b0 + nb): rows past the last lane read 0 and are not
+            // written (buffer range check).  No load or store is under a branch: the compiler's wait counts treat
+            // a memory operation under a branch as possibly not issued, and every row would then wait for all
+            // loads in flight.
+            const __amdgpu_buffer_rsrc_t sr =
+                buf_rsrc(a.ssm + ((int64_t)l * a.max_lanes + b0) * FDI * FNS, (uint32_t)nb * FDI * FNS * 4);
             constexpr int PD = 4;  // lanes of state in flight
             float hr[PD][FNS];
+            auto h_off = [&](int r, int n) { return (uint32_t)((r * FNS / 4 + n / 4) * FDI + c) * 16; };
             auto load_h = [&](int r, float (&h)[FNS]) {
-                if (r < nb) {
-                    const gptr<float> hp = sl + (b0 + r) * FDI * FNS;
 #pragma unroll
-                    for (int n = 0; n < FNS; n += 4) {
-                        const float4 q = ldg_f4(hp + (int64_t)(n / 4) * FDI * 4);
-                        h[n] = q.x; h[n + 1] = q.y; h[n + 2] = q.z; h[n + 3] = q.w;
-                    }
-                } else {
-#pragma unroll
-                    for (int n = 0; n < FNS; ++n) h[n] = 0.0f;
+                for (int n = 0; n < FNS; n += 4) {
+                    const f32x4 q = buf_ld4(sr, h_off(r, n));
+                    h[n] = q.x; h[n + 1] = q.y; h[n + 2] = q.z; h[n + 3] = q.w;
                 }
             };
 #pragma unroll
             for (int q = 0; q < PD - 1; ++q) load_h(q, hr[q]);
+            // the scheduler would otherwise sink each prefetch down to its use (the kernel is at its register
+            // limit) and every row would wait out a full memory round trip
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) {
                 if (r + PD - 1 < ROWS) load_h(r + PD - 1, hr[(r + PD - 1) % PD]);
+                __builtin_amdgcn_sched_barrier(0);
                 float (&h)[FNS] = hr[r % PD];
                 const float x = sX[r * LXZ + c], z = sX[r * LXZ + FDI + c];
                 const float y = scan_position<FNS, FR>(sDbc + r * FW, wr, bdt, av, Dc, x, z, h);
                 put_split(sAh, sAl, r * LA + c, y);
-                if (r < nb) {
-                    const gmut<float> hp = sl + (b0 + r) * FDI * FNS;
 #pragma unroll
-                    for (int n = 0; n < FNS; n += 4)
-                        stg_f4(hp + (int64_t)(n / 4) * FDI * 4, make_float4(h[n], h[n + 1], h[n + 2], h[n + 3]));
-                }
+                for (int n = 0; n < FNS; n += 4) buf_st4(sr, h_off(r, n), f32x4{h[n], h[n + 1], h[n + 2], h[n + 3]});
             }
         }
         __syncthreads();

@@ -985,10 +985,10 @@ struct boa_ctx {
     int64_t pos = 0;                   // positions processed since the last state reset (conv history ring)
     bool fused = false;                // decompress / step through k_fused_step
     int fused_steps = 128;             // decode steps per k_fused_step launch
-    // k_fused_step workgroup classes (sets of XCDs) start this far apart, so that one class runs its
-    // HBM-bound scans while the other streams weights from L2.  Offsets below ~2 layers' time (~250 us at
-    // d256x8L, 4096 lanes) do not hold: the follower catches up on the leader's cached weights.
-    int stagger_us = 320;
+    // k_fused_step workgroup classes (sets of XCDs) can start this far apart, so that one class runs its
+    // HBM-bound scans while the other streams weights from L2.  Off by default: with the recurrent state
+    // streamed non-temporally the weights stay in L2 and offsets of 0-450 us measure the same.
+    int stagger_us = 0;
     int stagger_classes = 2;
     uint16_t* wfrag = nullptr;         // fragment-packed GEMM weights (fused)
     FusedLayer* d_layers = nullptr;    // per-layer pointer table (fused)

@@ -30,6 +30,32 @@ template <class T> __device__ __forceinline__ float4 ldg_f4(gptr<T> p) {
 }
 template <class T> __device__ __forceinline__ void stg_f4(gmut<T> p, float4 v) { *(gmut<f32x4>)p = f32x4{v.x, v.y, v.z, v.w}; }
 
+// Raw buffer access (no swizzle, stride 0) over [base, base + nbytes): a load past the end returns 0 and a store
+// past the end is dropped, so loads and stores of rows that may not exist need no branch.  The whole byte
+// offset goes in the vector operand (the range check does not include the scalar offset).  Word 3 of the
+// descriptor for the gfx9 family (gfx950): 32-bit data format.
+// All of these accesses are non-temporal (cache policy bit NT): they are used for recurrent state that each
+// step reads once and writes once, and the streaming policy keeps that traffic from evicting the GEMM weights,
+// which every workgroup re-reads from L2.
+constexpr int BUF_WORD3 = 0x00020000;
+constexpr int CPOL_NT = 2;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t nbytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)nbytes, BUF_WORD3);
+}
+typedef uint32_t bufv4 __attribute__((vector_size(16)));
+__device__ __forceinline__ f32x4 buf_ld4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CPOL_NT));
+}
+__device__ __forceinline__ void buf_st4(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(bufv4, v), r, off, 0, CPOL_NT);
+}
+__device__ __forceinline__ float buf_ld1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, CPOL_NT));
+}
+__device__ __forceinline__ void buf_st1(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, off, 0, CPOL_NT);
+}
+
 // GEMM epilogues: none | +bias | +bias,GELU(erf) | +bias,ReLU | residual + (acc + bias)
 enum { EPI_NONE = 0, EPI_BIAS = 1, EPI_GELU = 2, EPI_RELU = 3, EPI_RESID = 4 };
 
