@@ -137,6 +137,24 @@ __device__ __forceinline__ floatx4 mfma_split_step(floatx4 acc, bf16x8 ah, bf16x
 // a workgroup barrier; the compress and per-layer decode paths compute the same partials and the same fold.
 constexpr int XPROJ_KB = 64;
 
+// Activations on the hardware transcendental units (v_exp_f32 = 2^x, v_log_f32 = log2 x, v_rcp_f32 = 1/x,
+// each within about 1 ulp).  Relative error of the results below is a few 1e-7, far inside the 1e-4
+// logits tolerance against the fp32 reference, and a fraction of the instructions of expf / log1pf / IEEE
+// division.  Encoder and decoder share these functions, so their logits stay bit-identical.
+__device__ __forceinline__ float hw_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+// x * sigmoid(x) = x / (1 + e^-x)
+__device__ __forceinline__ float hw_silu(float x) { return x * __builtin_amdgcn_rcpf(1.0f + hw_exp(-x)); }
+// softplus(x) = log(1 + e^x) (F.softplus: x itself above 20), as max(x, 0) + log1p(e^-|x|); log1p(e) for
+// e in (0, 1] as log(u) * e / (u - 1) with u = 1 + e (Goldberg), exact to rounding also when u rounds to 1.
+__device__ __forceinline__ float hw_softplus(float x) {
+    if (x > 20.0f) return x;
+    const float e = hw_exp(-fabsf(x));
+    const float u = 1.0f + e;
+    const float d = u - 1.0f;
+    const float l1p = (d == 0.0f) ? e : (__builtin_amdgcn_logf(u) * 0.693147180559945309f) * (e * __builtin_amdgcn_rcpf(d));
+    return fmaxf(x, 0.0f) + l1p;
+}
+
 // Depthwise causal conv (d_conv = 4) + bias + SiLU of one channel at one position:
 // xc = b + w0*x[t-3] + w1*x[t-2] + w2*x[t-1] + w3*x[t] (model.py:72, PyTorch Conv1d cross-correlation).
 __device__ __forceinline__ float conv_point(const float4 w, float bias, float h0, float h1, float h2, float x) {
@@ -145,7 +163,7 @@ __device__ __forceinline__ float conv_point(const float4 w, float bias, float h0
     v = __builtin_fmaf(w.y, h1, v);
     v = __builtin_fmaf(w.z, h2, v);
     v = __builtin_fmaf(w.w, x, v);
-    return v / (1.0f + expf(-v));
+    return hw_silu(v);
 }
 
 // Selective scan, one position of one channel (Mamba's selective_scan_fn on one step):
@@ -160,7 +178,7 @@ __device__ __forceinline__ float scan_position(const float* row, const float (&w
 #pragma unroll
     for (int r = 0; r < R; ++r) dt = __builtin_fmaf(row[r], wr[r], dt);
     dt = dt + bdt;
-    dt = (dt > 20.0f) ? dt : log1pf(expf(dt));
+    dt = hw_softplus(dt);
     float y = 0.0f;
 #pragma unroll
     for (int n = 0; n < NS; ++n) {
@@ -170,7 +188,7 @@ __device__ __forceinline__ float scan_position(const float* row, const float (&w
         y = __builtin_fmaf(h[n], row[R + NS + n], y);
     }
     y = __builtin_fmaf(Dc, x, y);
-    return y * (z / (1.0f + expf(-z)));
+    return y * hw_silu(z);
 }
 
 // Logits of one lane (a V-wide row) as held by one wavefront: lane j gets elements 4j .. 4j + 3 (0 beyond V).
