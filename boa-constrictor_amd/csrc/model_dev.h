@@ -56,13 +56,14 @@ __device__ __forceinline__ void buf_st1(__amdgpu_buffer_rsrc_t r, uint32_t off, 
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, off, 0, CPOL_NT);
 }
 
+__device__ __forceinline__ float gelu_erf(float v);  // below
+
 // GEMM epilogues: none | +bias | +bias,GELU(erf) | +bias,ReLU | residual + (acc + bias)
 enum { EPI_NONE = 0, EPI_BIAS = 1, EPI_GELU = 2, EPI_RELU = 3, EPI_RESID = 4 };
 
 // Quantiser precision of the fused coder (bits of the CDF total).
 static constexpr int CODER_P = 24;
 
-__device__ __forceinline__ float gelu_erf(float v) { return (v * 0.5f) * (1.0f + erff(v * 0.70710678118654752f)); }
 
 // Epilogue value of one accumulator before the residual add (EPI_RESID adds bias here, residual later).
 template <int EPI>
@@ -153,6 +154,22 @@ __device__ __forceinline__ float hw_softplus(float x) {
     const float d = u - 1.0f;
     const float l1p = (d == 0.0f) ? e : (__builtin_amdgcn_logf(u) * 0.693147180559945309f) * (e * __builtin_amdgcn_rcpf(d));
     return fmaxf(x, 0.0f) + l1p;
+}
+
+// GELU (erf form, nn.GELU()) = (x / 2) (1 + erf(x / sqrt 2)), with erf from Abramowitz & Stegun 7.1.26:
+// erf(u) = 1 - q, q = t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) e^{-u^2}, t = 1 / (1 + p u), u >= 0 (absolute
+// error below 1.5e-7).  1 + erf is formed as 2 - q or q directly, so there is no cancellation for negative x.
+// Absolute error of the result below 5e-7 (checked against float64 on [-12, 12]).
+__device__ __forceinline__ float gelu_erf(float v) {
+    const float u = fabsf(v) * 0.70710678118654752f;
+    const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * u);
+    float p = 1.061405429f;
+    p = p * t + -1.453152027f;
+    p = p * t + 1.421413741f;
+    p = p * t + -0.284496736f;
+    p = p * t + 0.254829592f;
+    const float q = (p * t) * hw_exp(-(u * u));
+    return (v * 0.5f) * (v >= 0.0f ? 2.0f - q : q);
 }
 
 // Depthwise causal conv (d_conv = 4) + bias + SiLU of one channel at one position:
