@@ -20,6 +20,7 @@
 #include <stdlib.h>
 #include <string.h>
 #include <algorithm>
+#include <type_traits>
 #include <string>
 #include <vector>
 
@@ -232,7 +233,15 @@ __global__ void __launch_bounds__(256, 2) k_gemm(GemmArgs g) {
 // 32-wide MFMA K steps in ascending order, so results do not depend on BK, BM or BN.
 template <int BM, int BN, int BK, int EPI, int NT, bool ASPLIT, bool OUTS>
 __global__ void __launch_bounds__(256, (BK > 32) ? 1 : 2) k_gemm_bf(GemmArgs g) {
-    constexpr int LDK = BK + 8;
+    // LDS rows: BK = 32 tiles are unpadded (64 B per part-row) with the 16-byte chunk c of row r stored at
+    // chunk c ^ ((r >> 2) & 3), so a 16-lane group of stores (4 rows x 4 chunks) and of fragment reads (16 rows,
+    // one chunk) each touch every bank once; BK = 128 rows are padded by 8 (272 B, also conflict-free reads).
+    constexpr bool SWZ = (BK == 32);
+    constexpr int LDK = SWZ ? BK : BK + 8;
+    auto lds_off = [](int r, int k) {  // element (row r, column k) of an operand tile, k % 8 == 0 or a half chunk
+        if constexpr (SWZ) return r * 32 + ((((k >> 3) ^ (r >> 2)) & 3) << 3) + (k & 7);
+        else return r * LDK + k;
+    };
     constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 16, FN = WN / 16;
     constexpr int A_LD = ASPLIT ? BM * BK / 8 / 256 : BM * BK / 4 / 256;  // per thread: 8-bf16 or float4 loads
     constexpr int B_LD = BN * BK / 8 / 256;
@@ -258,69 +267,73 @@ __global__ void __launch_bounds__(256, (BK > 32) ? 1 : 2) k_gemm_bf(GemmArgs g) 
     const int64_t M = g.M;
     const int N = g.N, K = g.K;
 
-    // A staging registers: pre-split (uint4 = 8 bf16 of each part) or fp32 split on load (uint2 = 4 bf16)
-    uint4 rah4[ASPLIT ? A_LD : 1], ral4[ASPLIT ? A_LD : 1];
-    uint2 rah2[ASPLIT ? 1 : A_LD], ral2[ASPLIT ? 1 : A_LD];
-    uint4 rbh[B_LD], rbl[NT == 3 ? B_LD : 1];
-    auto load_tiles = [&](int k0) {
-        if constexpr (ASPLIT) {
+    // Operand tiles through range-checked buffer descriptors over this tile's rows of A and of W: rows past M
+    // (or N) read 0 with no branch around the load, so the compiler's wait counts see every load as issued.
+    const int rows_a = (int)((M - m0) < BM ? (M - m0) : BM);
+    const int rows_b = (N - n0) < BN ? (N - n0) : BN;
+    const __amdgpu_buffer_rsrc_t rA =
+        ASPLIT ? buf_rsrc(g.Ah + m0 * g.lda, (uint32_t)(rows_a * g.lda * 2)) : buf_rsrc(g.A + m0 * g.lda, (uint32_t)(rows_a * g.lda * 4));
+    const __amdgpu_buffer_rsrc_t rAl = ASPLIT ? buf_rsrc(g.Al + m0 * g.lda, (uint32_t)(rows_a * g.lda * 2)) : rA;
+    const __amdgpu_buffer_rsrc_t rBh = buf_rsrc(g.Wh + (int64_t)n0 * K, (uint32_t)(rows_b * K * 2));
+    const __amdgpu_buffer_rsrc_t rBl = (NT == 3) ? buf_rsrc(g.Wl + (int64_t)n0 * K, (uint32_t)(rows_b * K * 2)) : rBh;
+
+    // Two register stages: the loads of K step kt + 2 are issued while step kt multiplies from LDS and step
+    // kt + 1 (loaded during step kt - 1) is stored to the other LDS buffer, so each load has about two K
+    // steps of MFMA work to arrive in.  Stage indices are compile-time (the K loop is unrolled by two).
+    // A: pre-split (8 bf16 of each part per load) or fp32 split on store (4 values per load).
+    u32x4 sa_h[2][A_LD], sa_l[2][ASPLIT ? A_LD : 1];
+    u32x4 sb_h[2][B_LD], sb_l[2][NT == 3 ? B_LD : 1];
+    auto load_tiles = [&](auto stage, int k0) {
+        constexpr int S = decltype(stage)::value;
 #pragma unroll
-            for (int i = 0; i < A_LD; ++i) {
-                const int q = tid + 256 * i;
+        for (int i = 0; i < A_LD; ++i) {
+            const int q = tid + 256 * i;
+            if constexpr (ASPLIT) {
                 const int r = q / (BK / 8), c = (q % (BK / 8)) * 8;
-                const int64_t m = m0 + r;
-                const bool ok = m < M;
-                rah4[i] = ok ? *reinterpret_cast<const uint4*>(g.Ah + m * g.lda + k0 + c) : make_uint4(0, 0, 0, 0);
-                ral4[i] = ok ? *reinterpret_cast<const uint4*>(g.Al + m * g.lda + k0 + c) : make_uint4(0, 0, 0, 0);
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < A_LD; ++i) {
-                const int q = tid + 256 * i;
+                const uint32_t off = (uint32_t)((r * g.lda + k0 + c) * 2);
+                sa_h[S][i] = buf_ld16(rA, off);
+                sa_l[S][i] = buf_ld16(rAl, off);
+            } else {
                 const int r = q / (BK / 4), c = (q % (BK / 4)) * 4;
-                const int64_t m = m0 + r;
-                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (m < M) v = *reinterpret_cast<const float4*>(g.A + m * g.lda + k0 + c);
-                uint32_t h0, h1, h2, h3, l0, l1, l2, l3;
-                split2(v.x, h0, l0);
-                split2(v.y, h1, l1);
-                split2(v.z, h2, l2);
-                split2(v.w, h3, l3);
-                rah2[i] = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
-                ral2[i] = make_uint2(l0 | (l1 << 16), l2 | (l3 << 16));
+                sa_h[S][i] = buf_ld16(rA, (uint32_t)((r * g.lda + k0 + c) * 4));
             }
         }
 #pragma unroll
         for (int i = 0; i < B_LD; ++i) {
             const int q = tid + 256 * i;
             const int r = q / (BK / 8), c = (q % (BK / 8)) * 8;
-            const int n = n0 + r;
-            const bool ok = n < N;
-            rbh[i] = ok ? *reinterpret_cast<const uint4*>(g.Wh + (int64_t)n * K + k0 + c) : make_uint4(0, 0, 0, 0);
-            if constexpr (NT == 3)
-                rbl[i] = ok ? *reinterpret_cast<const uint4*>(g.Wl + (int64_t)n * K + k0 + c) : make_uint4(0, 0, 0, 0);
+            const uint32_t off = (uint32_t)((r * K + k0 + c) * 2);
+            sb_h[S][i] = buf_ld16(rBh, off);
+            if constexpr (NT == 3) sb_l[S][i] = buf_ld16(rBl, off);
         }
     };
-    auto store_tiles = [&](int buf) {
+    auto store_tiles = [&](auto stage, int buf) {
+        constexpr int S = decltype(stage)::value;
 #pragma unroll
         for (int i = 0; i < A_LD; ++i) {
             const int q = tid + 256 * i;
             if constexpr (ASPLIT) {
-                const int off = (q / (BK / 8)) * LDK + (q % (BK / 8)) * 8;
-                *reinterpret_cast<uint4*>(&sAh[buf][off]) = rah4[i];
-                *reinterpret_cast<uint4*>(&sAl[buf][off]) = ral4[i];
+                const int off = lds_off(q / (BK / 8), (q % (BK / 8)) * 8);
+                *reinterpret_cast<u32x4*>(&sAh[buf][off]) = sa_h[S][i];
+                *reinterpret_cast<u32x4*>(&sAl[buf][off]) = sa_l[S][i];
             } else {
-                const int off = (q / (BK / 4)) * LDK + (q % (BK / 4)) * 4;
-                *reinterpret_cast<uint2*>(&sAh[buf][off]) = rah2[i];
-                *reinterpret_cast<uint2*>(&sAl[buf][off]) = ral2[i];
+                const int off = lds_off(q / (BK / 4), (q % (BK / 4)) * 4);
+                const u32x4 v = sa_h[S][i];
+                uint32_t h0, h1, h2, h3, l0, l1, l2, l3;
+                split2(__uint_as_float(v.x), h0, l0);
+                split2(__uint_as_float(v.y), h1, l1);
+                split2(__uint_as_float(v.z), h2, l2);
+                split2(__uint_as_float(v.w), h3, l3);
+                *reinterpret_cast<uint2*>(&sAh[buf][off]) = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
+                *reinterpret_cast<uint2*>(&sAl[buf][off]) = make_uint2(l0 | (l1 << 16), l2 | (l3 << 16));
             }
         }
 #pragma unroll
         for (int i = 0; i < B_LD; ++i) {
             const int q = tid + 256 * i;
-            const int off = (q / (BK / 8)) * LDK + (q % (BK / 8)) * 8;
-            *reinterpret_cast<uint4*>(&sBh[buf][off]) = rbh[i];
-            if constexpr (NT == 3) *reinterpret_cast<uint4*>(&sBl[buf][off]) = rbl[i];
+            const int off = lds_off(q / (BK / 8), (q % (BK / 8)) * 8);
+            *reinterpret_cast<u32x4*>(&sBh[buf][off]) = sb_h[S][i];
+            if constexpr (NT == 3) *reinterpret_cast<u32x4*>(&sBl[buf][off]) = sb_l[S][i];
         }
     };
 
@@ -331,42 +344,62 @@ __global__ void __launch_bounds__(256, (BK > 32) ? 1 : 2) k_gemm_bf(GemmArgs g) 
         for (int j = 0; j < FN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
     const int KT = K / BK;
-    load_tiles(0);
-    store_tiles(0);
-    __syncthreads();
     const int arow = wm * WM + (lane & 15);
     const int brow = wn * WN + (lane & 15);
     const int kq = 8 * (lane >> 4);
-    for (int kt = 0; kt < KT; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < KT) load_tiles((kt + 1) * BK);
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    auto multiply = [&](int cur) {
 #pragma unroll
         for (int ks = 0; ks < BK; ks += 32) {
             bf16x8 ah[FM], al[FM], bh[FN], bl[FN];
 #pragma unroll
             for (int i = 0; i < FM; ++i) {
-                ah[i] = *reinterpret_cast<const bf16x8*>(&sAh[cur][(arow + 16 * i) * LDK + ks + kq]);
-                al[i] = *reinterpret_cast<const bf16x8*>(&sAl[cur][(arow + 16 * i) * LDK + ks + kq]);
+                ah[i] = *reinterpret_cast<const bf16x8*>(&sAh[cur][lds_off(arow + 16 * i, ks + kq)]);
+                al[i] = *reinterpret_cast<const bf16x8*>(&sAl[cur][lds_off(arow + 16 * i, ks + kq)]);
             }
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
-                bh[j] = *reinterpret_cast<const bf16x8*>(&sBh[cur][(brow + 16 * j) * LDK + ks + kq]);
+                bh[j] = *reinterpret_cast<const bf16x8*>(&sBh[cur][lds_off(brow + 16 * j, ks + kq)]);
+                bl[j] = bh[j];
                 if constexpr (NT == 3)
-                    bl[j] = *reinterpret_cast<const bf16x8*>(&sBl[cur][(brow + 16 * j) * LDK + ks + kq]);
+                    bl[j] = *reinterpret_cast<const bf16x8*>(&sBl[cur][lds_off(brow + 16 * j, ks + kq)]);
             }
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll
-                for (int j = 0; j < FN; ++j) {
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bh[j], acc[i][j], 0, 0, 0);
-                    if constexpr (NT == 3)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bl[j], acc[i][j], 0, 0, 0);
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bh[j], acc[i][j], 0, 0, 0);
-                }
+                for (int j = 0; j < FN; ++j) acc[i][j] = mfma_split_step<NT>(acc[i][j], ah[i], al[i], bh[j], bl[j]);
         }
-        if (kt + 1 < KT) store_tiles(cur ^ 1);
+    };
+    // One K step kt with compile-time stage parity P = kt & 1: LDS buffer P holds step kt, register stage 1 - P
+    // holds step kt + 1 in flight, register stage P is free.  LOAD / STORE are compile-time too: the last two
+    // steps are peeled off the loop, so no load is under a branch (the compiler's wait counts would otherwise
+    // make every store wait for all loads in flight).  KT is even (checked at launch).
+    auto kstep = [&](auto parity, auto load, auto store, int kt) {
+        constexpr int P = decltype(parity)::value;
+        using SP = std::integral_constant<int, P>;
+        using SQ = std::integral_constant<int, 1 - P>;
+        if constexpr (decltype(load)::value) load_tiles(SP{}, (kt + 2) * BK);
+        // keep the loads ahead of this step's MFMAs and the stores after them (the scheduler would sink the
+        // loads below the stores, leaving them one step instead of two to arrive)
+        __builtin_amdgcn_sched_barrier(0);
+        multiply(P);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (decltype(store)::value) store_tiles(SQ{}, 1 - P);
         __syncthreads();
+    };
+    using T = std::true_type;
+    using F = std::false_type;
+    load_tiles(S0{}, 0);
+    load_tiles(S1{}, BK);
+    store_tiles(S0{}, 0);
+    __syncthreads();
+    for (int kt = 0; kt + 2 < KT; kt += 2) {
+        kstep(S0{}, T{}, T{}, kt);
+        kstep(S1{}, T{}, T{}, kt + 1);
     }
+    kstep(S0{}, F{}, T{}, KT - 2);
+    kstep(S1{}, F{}, F{}, KT - 1);
 
     // Epilogue through LDS (the operand buffers are free after the last barrier): fragments are written
     // to an fp32 tile [BM][BN + 4] (bias and activation applied here), then rows leave in 16-byte pieces.
@@ -440,7 +473,7 @@ static int launch_gemm_f32(const GemmArgs& g, hipStream_t s) {
 
 template <int BM, int BN, int BK, int EPI, bool ASPLIT, bool OUTS>
 static int launch_gemm_bf_cfg(GemmArgs g, hipStream_t s) {
-    if (g.K % BK != 0) return boa_fail(BOA_ERR_ARG, "internal: K=%d not a multiple of BK=%d", g.K, BK);
+    if (g.K % (2 * BK) != 0) return boa_fail(BOA_ERR_ARG, "internal: K=%d not a multiple of 2 BK=%d", g.K, 2 * BK);
     int64_t grid;
     tile_grid(g, BM, BN, grid);
     if (g.Wl)
