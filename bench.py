@@ -33,11 +33,11 @@ PEAK_HBM_GBPS = 8000.0
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_fused_step_d256x8L_4096lanes.json")
 
 # rocprof names of the kernel instances each profiled class launches at the benchmark's shapes, default
-# precision bf16x3 (k_gemm_bf<BM, BN, BK, EPI, NT, A split, C split>: EPI 0 none, 1 bias, 2 GELU, 4 residual)
+# precision bf16x3 (k_gemm_bf<BM, BN, BK, EPI, NT, A split, C split>: EPI 0 none, 1 bias, 2 GELU, 4 residual;
+# k_ffn: LN2 + FF1 + GELU + FF2 + residual in one kernel)
 KERNEL_NAMES = {
     ("compress", "gemm_in_proj"): "k_gemm_bf<128, 128, 32, 1, 3, true, false>",
-    ("compress", "gemm_ff1"): "k_gemm_bf<128, 128, 32, 2, 3, true, true>",
-    ("compress", "gemm_ff2"): "k_gemm_bf<128, 128, 32, 4, 3, true, false>",
+    ("compress", "ffn"): "k_ffn<3>",
     ("compress", "gemm_out_proj"): "k_gemm_bf<128, 128, 32, 1, 3, true, false>",
     ("compress", "gemm_x_proj"): "k_xproj<3, 3>",
     ("compress", "scan"): "k_scan<16, 16, true>",

@@ -722,6 +722,176 @@ __global__ void __launch_bounds__(256) k_xproj(const float* __restrict__ xs, int
         }
 }
 
+// ================================================================================================
+// Feed-forward half of a block in one kernel (split modes, d_model 256, d_ff 1024), for row tiles:
+//   x <- x + FF2(GELU(FF1(LN2(mm))))        (model.py:60-65: Linear -> GELU -> Linear, then the block residual)
+// A workgroup owns 64 rows.  LN2 of its rows goes to LDS as the split operand; then, per 64-wide chunk of the
+// hidden layer, FF1 (+bias, GELU, split) writes the chunk to LDS and FF2 accumulates it into registers, so the
+// hidden activations never leave the chip (the unfused path writes and reads back 4 KiB of them per row).
+// Arithmetic per output is that of the tiled GEMMs and of the fused decode kernel: LN by ln_stats_row /
+// ln_apply / split2; FF1 outputs accumulate their 8 K steps in ascending order through mfma_split_step then
+// epi_value<GELU>; FF2 outputs accumulate all 32 K steps in ascending order (chunk by chunk), then
+// x + epi_value<RESID>.  So the rows equal those of the layer-by-layer path bit for bit.
+// LDS: A [64][256] (hi, lo) and H [64][64] (hi, lo), bf16, 16-byte chunks XOR-swizzled by row so that 16-row
+// fragment reads touch every bank once; 80 KB, two workgroups per CU.
+namespace ffn {
+constexpr int BM = 64, D = 256, DF = 1024, HC = 64;
+__device__ __forceinline__ int a_off(int r, int k) { return r * D + ((((k >> 3) ^ r) & 15) | ((k >> 3) & 16)) * 8 + (k & 7); }
+__device__ __forceinline__ int h_off(int r, int k) { return r * HC + (((k >> 3) ^ (r >> 1)) & 7) * 8 + (k & 7); }
+}  // namespace ffn
+
+template <int NT>
+__global__ void __launch_bounds__(256, 2) k_ffn(const float* __restrict__ mm, const float* __restrict__ ln_w,
+                                               const float* __restrict__ ln_b, const uint16_t* __restrict__ W1p,
+                                               const float* __restrict__ b1, const uint16_t* __restrict__ W2p,
+                                               const float* __restrict__ b2, float* __restrict__ x, int64_t M) {
+    using namespace ffn;
+    __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * D];
+    __shared__ __attribute__((aligned(16))) uint16_t sH[2][BM * HC];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t m0 = (int64_t)blockIdx.x * BM;
+    const int rows = (int)((M - m0) < BM ? (M - m0) : BM);
+    // ---- LN2 of this tile's rows (rows past M: zeros, never stored)
+    {
+        const __amdgpu_buffer_rsrc_t rm = buf_rsrc(mm + m0 * D, (uint32_t)rows * D * 4);
+        const float4 wv = ldg_f4(G(ln_w) + 4 * lane), bv = ldg_f4(G(ln_b) + 4 * lane);
+#pragma unroll 4
+        for (int q = 0; q < BM / 4; ++q) {
+            const int r = 16 * wave + q;
+            const u32x4 u = buf_ld16(rm, (uint32_t)((r * D + 4 * lane) * 4));
+            const float v[4] = {__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w)};
+            float mu, rs;
+            ln_stats_row<1>(v, mu, rs);
+            const float y[4] = {ln_apply(v[0], mu, rs, wv.x, bv.x), ln_apply(v[1], mu, rs, wv.y, bv.y),
+                                ln_apply(v[2], mu, rs, wv.z, bv.z), ln_apply(v[3], mu, rs, wv.w, bv.w)};
+            uint32_t h[4], l[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) split2(y[j], h[j], l[j]);
+            const int o = a_off(r, 4 * lane);
+            *reinterpret_cast<uint2*>(&sA[0][o]) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+            *reinterpret_cast<uint2*>(&sA[1][o]) = make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
+        }
+    }
+    __syncthreads();
+
+    const int ar = lane & 15, kq = 8 * (lane >> 4), m_of = 4 * (lane >> 4);
+    // weights fragment-packed (layout in model_internal.h): block (f, s) of W1 [DF][D] and of W2 [D][DF], each
+    // one coalesced 16-byte load per lane (hi part, then the lo part 512 elements further)
+    constexpr int BLK = (NT == 3) ? 1024 : 512;
+    const gptr<uint16_t> w1p = G(W1p), w2p = G(W2p);
+    // FF1 of a chunk: wave w computes rows 32 (w & 1) .. + 31 (M fragments mh + 0, 1) x chunk columns
+    // 32 (w >> 1) .. + 31 (N fragments nh + 0, 1).  Its W1 blocks (fragment j, K step s; i = 2 s + j) stream
+    // through a ring of R1 register slots that runs on into the next chunk, so those loads are in flight
+    // during the GELU epilogue, the barriers and FF2.
+    const int mh = 2 * (wave & 1), nh = 2 * (wave >> 1);
+    constexpr int R1 = 4, NB1 = 16;  // ring slots; W1 blocks per wave per chunk
+    u32x4 r1h[R1], r1l[R1];
+    auto issue_w1 = [&](int c, int i) {  // block i of chunk c into slot i % R1
+        const int f = (HC * c) / 16 + nh + (i & 1);
+        const gptr<uint16_t> q = w1p + ((int64_t)f * (D / 32) + (i >> 1)) * BLK + lane * 8;
+        r1h[i % R1] = ldg16(q);
+        r1l[i % R1] = r1h[i % R1];
+        if constexpr (NT == 3) r1l[i % R1] = ldg16(q + 512);
+    };
+    floatx4 out[4][4];  // FF2: M fragment i, output fragment 4 wave + j
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) out[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < R1; ++i) issue_w1(0, i);
+
+#pragma unroll 1
+    for (int c = 0; c < DF / HC; ++c) {
+        // ---- FF1
+        floatx4 hacc[2][2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) hacc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        const int cn = c + 1 < DF / HC ? c + 1 : c;  // the ring runs on into the next chunk (the last reloads)
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            bf16x8 ah[2], al[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int o = a_off(16 * (mh + i) + ar, 32 * s + kq);
+                ah[i] = *reinterpret_cast<const bf16x8*>(&sA[0][o]);
+                al[i] = *reinterpret_cast<const bf16x8*>(&sA[1][o]);
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int b = 2 * s + j;
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                    hacc[i][j] = mfma_split_step<NT>(hacc[i][j], ah[i], al[i], __builtin_bit_cast(bf16x8, r1h[b % R1]),
+                                                     __builtin_bit_cast(bf16x8, r1l[b % R1]));
+                if (b + R1 < NB1) issue_w1(c, b + R1);
+                else issue_w1(cn, b + R1 - NB1);
+            }
+        }
+        // FF2 weights of this chunk: outputs 16 (4 wave + j) + lane % 16, K steps 2c, 2c + 1 (they load during the GELU epilogue and the barrier)
+        u32x4 b2h[4][2], b2l[4][2];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                const gptr<uint16_t> q = w2p + ((int64_t)(4 * wave + j) * (DF / 32) + (HC * c) / 32 + s) * BLK + lane * 8;
+                b2h[j][s] = ldg16(q);
+                b2l[j][s] = b2h[j][s];
+                if constexpr (NT == 3) b2l[j][s] = ldg16(q + 512);
+            }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int hc = 16 * (nh + j) + ar;  // column within the chunk
+            const float bias = G(b1)[HC * c + hc];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    uint32_t hi, lo;
+                    split2(epi_value<EPI_GELU>(hacc[i][j][r], bias), hi, lo);
+                    const int o = h_off(16 * (mh + i) + m_of + r, hc);
+                    sH[0][o] = (uint16_t)hi;
+                    sH[1][o] = (uint16_t)lo;
+                }
+        }
+        __syncthreads();
+        // ---- FF2: accumulate this chunk (K steps 2c, 2c + 1) into all 64 rows x this wave's 64 outputs
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int o = h_off(16 * i + ar, 32 * s + kq);
+                const bf16x8 ah = *reinterpret_cast<const bf16x8*>(&sH[0][o]);
+                const bf16x8 al = *reinterpret_cast<const bf16x8*>(&sH[1][o]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    out[i][j] = mfma_split_step<NT>(out[i][j], ah, al, __builtin_bit_cast(bf16x8, b2h[j][s]),
+                                                    __builtin_bit_cast(bf16x8, b2l[j][s]));
+            }
+        }
+        __syncthreads();  // the next chunk rewrites H
+    }
+    // ---- x <- x + (acc + b2), rows past M dropped by the buffer range check
+    const __amdgpu_buffer_rsrc_t rx = buf_rsrc(x + m0 * D, (uint32_t)rows * D * 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int col = 16 * (4 * wave + j) + ar;
+        const float bias = G(b2)[col];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t o = (uint32_t)(((16 * i + m_of + r) * D + col) * 4);
+                const float res = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, o, 0, 0));
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, res + epi_value<EPI_RESID>(out[i][j][r], bias)),
+                                                      rx, o, 0, 0);
+            }
+    }
+}
+
 static int launch_xproj(const float* xs, int64_t M, int di, const uint16_t* Wh, const uint16_t* Wl, float* dbc, int ldd,
                         hipStream_t s) {
     const unsigned grid = (unsigned)((M + 63) / 64);
@@ -980,12 +1150,12 @@ static GemmArgs gemm_args(const float* A, int64_t lda, const MatW& W, const floa
 // Per-kernel-class event timing (boa_profile / boa_profile_read).
 enum ProfClass {
     PC_EMBED, PC_IN, PC_CONV, PC_XPROJ, PC_SCAN, PC_OUT, PC_FF1, PC_FF2, PC_HEAD1, PC_HEAD2, PC_ENCODE, PC_DECODE,
-    PC_LN, PC_FUSED, PC_COUNT
+    PC_LN, PC_FUSED, PC_FFN, PC_COUNT
 };
 static const char* kProfNames[PC_COUNT] = {"embed",    "gemm_in_proj", "conv",     "gemm_x_proj",
                                            "scan",     "gemm_out_proj", "gemm_ff1", "gemm_ff2",
                                            "gemm_head1", "gemm_head2", "encode",   "decode",
-                                           "ln_stats", "fused_step"};
+                                           "ln_stats", "fused_step", "ffn"};
 struct ProfClassState {
     int64_t launches = 0;
     int64_t used = 0;
@@ -1505,6 +1675,21 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc) {
             PROF(PC_OUT, gemm_flops(M, d, di), gemm_bytes(M, d, di), rc = (launch_gemm_f32<0, EPI_BIAS>(g, s)));
         }
         if (rc) return rc;
+    }
+    if (split && d == ffn::D && 4 * d == ffn::DF && w.ff1_w.p && w.ff2_w.p) {
+        // LN2 + FF1 + GELU + FF2 + residual in one kernel (hidden layer kept on chip)
+        const double flops = gemm_flops(M, 4 * d, d) + gemm_flops(M, d, 4 * d);
+        const double bytes = 4.0 * M * d * 3 + 2.0 * 2 * (2.0 * 4 * d * d);
+        const unsigned grid = (unsigned)((M + ffn::BM - 1) / ffn::BM);
+        if (w.ff1_w.l)
+            PROF(PC_FFN, flops, bytes,
+                 hipLaunchKernelGGL((k_ffn<3>), dim3(grid), dim3(256), 0, s, x->mm, w.ln2_w, w.ln2_b, w.ff1_w.p,
+                                    w.ff1_b, w.ff2_w.p, w.ff2_b, x->x, M));
+        else
+            PROF(PC_FFN, flops, bytes,
+                 hipLaunchKernelGGL((k_ffn<2>), dim3(grid), dim3(256), 0, s, x->mm, w.ln2_w, w.ln2_b, w.ff1_w.p,
+                                    w.ff1_b, w.ff2_w.p, w.ff2_b, x->x, M));
+        return BOA_OK;
     }
     // LN2 + FF1 + GELU -> g [M][4d]
     {
