@@ -38,6 +38,7 @@ TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_fused_step_d256x8L_4096la
 KERNEL_NAMES = {
     ("compress", "gemm_in_proj"): "k_gemm_bf<128, 128, 32, 1, 3, true, false>",
     ("compress", "ffn"): "k_ffn<3>",
+    ("compress", "mixin"): "k_mixin<3>",
     ("compress", "gemm_out_proj"): "k_gemm_bf<128, 128, 32, 1, 3, true, false>",
     ("compress", "gemm_x_proj"): "k_xproj<3, 3>",
     ("compress", "scan"): "k_scan<16, 16, true>",

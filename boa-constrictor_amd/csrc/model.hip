@@ -892,6 +892,207 @@ __global__ void __launch_bounds__(256, 2) k_ffn(const float* __restrict__ mm, co
     }
 }
 
+// ================================================================================================
+// Input half of the mixer in one kernel (split modes, d_model 256, compress tiles of 64 positions):
+//   LN1 -> in_proj (+bias) -> z to HBM; x -> causal conv + SiLU over the 64 positions -> xs to HBM ->
+//   x_proj -> dbc to HBM; the conv history ring of the lane advanced by 64 positions.
+// A workgroup owns one lane's tile (rows b*64 .. b*64 + 63, positions p0 .. p0 + 63).  LN1 output is the split
+// operand in LDS (as in k_ffn).  in_proj runs in 64-column chunks (each wave a 32 x 32 block, fragment-packed
+// weights through a register ring running on across chunks): the 8 z chunks are stored as they finish; each
+// x chunk goes through LDS for the conv over time (the conv output, split, then replaces it in place) and
+// into x_proj's partial over those 64 channels, which is exactly x_proj's K block, folded into dbc in
+// registers (dbc = P_0 + P_1 + ...).  Arithmetic per value is that of the layer-by-layer kernels (ln_*,
+// mfma_split_step, epi_value, conv_point, split2), so outputs equal theirs bit for bit.
+namespace mixin {
+constexpr int BM = 64, D = 256, DI = 512, CH = 64, FW = 48;
+__device__ __forceinline__ int x_off(int r, int k) { return r * CH + (((k >> 3) ^ (r >> 1)) & 7) * 8 + (k & 7); }
+}  // namespace mixin
+
+template <int NT>
+__global__ void __launch_bounds__(256, 2) k_mixin(const float* __restrict__ x, const float* __restrict__ ln_w,
+                                                 const float* __restrict__ ln_b, const uint16_t* __restrict__ Wip,
+                                                 const float* __restrict__ bin, const float* __restrict__ conv_w,
+                                                 const float* __restrict__ conv_b, const uint16_t* __restrict__ Wxp,
+                                                 float* __restrict__ xz, float* __restrict__ xs,
+                                                 float* __restrict__ dbc, float* __restrict__ hist, int p0m3) {
+    using namespace mixin;
+    constexpr int BLK = (NT == 3) ? 1024 : 512;
+    __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * D];  // LN1 output (hi, lo)
+    __shared__ __attribute__((aligned(16))) float sX[BM * CH];        // x chunk fp32; then its conv output split
+    uint16_t* sXh = reinterpret_cast<uint16_t*>(sX);
+    uint16_t* sXl = sXh + BM * CH;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t b = blockIdx.x, m0 = b * BM;
+    // ---- LN1
+    {
+        const float4 wv = ldg_f4(G(ln_w) + 4 * lane), bv = ldg_f4(G(ln_b) + 4 * lane);
+#pragma unroll 4
+        for (int q = 0; q < BM / 4; ++q) {
+            const int r = 16 * wave + q;
+            const float4 u = ldg_f4(G(x) + (m0 + r) * D + 4 * lane);
+            const float v[4] = {u.x, u.y, u.z, u.w};
+            float mu, rs;
+            ln_stats_row<1>(v, mu, rs);
+            const float y[4] = {ln_apply(v[0], mu, rs, wv.x, bv.x), ln_apply(v[1], mu, rs, wv.y, bv.y),
+                                ln_apply(v[2], mu, rs, wv.z, bv.z), ln_apply(v[3], mu, rs, wv.w, bv.w)};
+            uint32_t h[4], l[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) split2(y[j], h[j], l[j]);
+            const int o = ffn::a_off(r, 4 * lane);
+            *reinterpret_cast<uint2*>(&sA[0][o]) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+            *reinterpret_cast<uint2*>(&sA[1][o]) = make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
+        }
+    }
+    __syncthreads();
+
+    const int ar = lane & 15, kq = 8 * (lane >> 4), m_of = 4 * (lane >> 4);
+    const gptr<uint16_t> wip = G(Wip), wxp = G(Wxp);
+    // in_proj chunk k (columns CH k .. CH k + 63; chunks 0..7 are x, 8..15 are z): wave w computes rows
+    // 32 (w & 1) .. + 31 x chunk columns 32 (w >> 1) .. + 31.  Chunk order: z first (8..15), then x (0..7).
+    const int mh = 2 * (wave & 1), nh = 2 * (wave >> 1);
+    constexpr int R1 = 4, NB1 = 16, NCH = 2 * DI / CH;
+    auto chunk_of = [](int i) { return i < NCH / 2 ? NCH / 2 + i : i - NCH / 2; };  // i-th chunk processed
+    u32x4 r1h[R1], r1l[R1];
+    auto issue_w = [&](int k, int i) {  // block i (fragment nh + (i & 1), K step i >> 1) of chunk k
+        const int f = (CH * k) / 16 + nh + (i & 1);
+        const gptr<uint16_t> q = wip + ((int64_t)f * (D / 32) + (i >> 1)) * BLK + lane * 8;
+        r1h[i % R1] = ldg16(q);
+        r1l[i % R1] = r1h[i % R1];
+        if constexpr (NT == 3) r1l[i % R1] = ldg16(q + 512);
+    };
+#pragma unroll
+    for (int i = 0; i < R1; ++i) issue_w(chunk_of(0), i);
+    floatx4 dacc[3];  // x_proj (dbc) of rows 16 wave .. + 15, fragments 0..2
+#pragma unroll
+    for (int j = 0; j < 3; ++j) dacc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const int s1 = p0m3 == 2 ? 0 : p0m3 + 1, s2 = p0m3 == 0 ? 2 : p0m3 - 1;
+
+#pragma unroll 1
+    for (int ci = 0; ci < NCH; ++ci) {
+        const int k = chunk_of(ci);
+        const int kn = chunk_of(ci + 1 < NCH ? ci + 1 : ci);
+        floatx4 acc[2][2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < D / 32; ++s) {
+            bf16x8 ah[2], al[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int o = ffn::a_off(16 * (mh + i) + ar, 32 * s + kq);
+                ah[i] = *reinterpret_cast<const bf16x8*>(&sA[0][o]);
+                al[i] = *reinterpret_cast<const bf16x8*>(&sA[1][o]);
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int bi = 2 * s + j;
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                    acc[i][j] = mfma_split_step<NT>(acc[i][j], ah[i], al[i], __builtin_bit_cast(bf16x8, r1h[bi % R1]),
+                                                    __builtin_bit_cast(bf16x8, r1l[bi % R1]));
+                if (bi + R1 < NB1) issue_w(k, bi + R1);
+                else issue_w(kn, bi + R1 - NB1);
+            }
+        }
+        if (k >= NCH / 2) {
+            // z chunk: straight to HBM (the scan reads it)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int col = CH * k + 16 * (nh + j) + ar;
+                const float bias = G(bin)[col];
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        GM(xz)[(m0 + 16 * (mh + i) + m_of + r) * (2 * DI) + col] = epi_value<EPI_BIAS>(acc[i][j][r], bias);
+            }
+            continue;
+        }
+        // x chunk: fp32 to LDS for the conv over time
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int cl = 16 * (nh + j) + ar;
+            const float bias = G(bin)[CH * k + cl];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sX[(16 * (mh + i) + m_of + r) * CH + cl] = epi_value<EPI_BIAS>(acc[i][j][r], bias);
+        }
+        __syncthreads();
+        // conv + SiLU: thread = (channel cl, rows 16 g .. 16 g + 15); inputs read before the barrier, the split
+        // output written over them after it
+        {
+            const int cl = tid & (CH - 1), g = tid >> 6;
+            const int c = CH * k + cl;
+            float xv[19];
+            if (g == 0) {
+                const gptr<float> hb = G(hist) + b * 3 * DI;
+                xv[0] = hb[p0m3 * DI + c];
+                xv[1] = hb[s1 * DI + c];
+                xv[2] = hb[s2 * DI + c];
+            } else {
+#pragma unroll
+                for (int e = 0; e < 3; ++e) xv[e] = sX[(16 * g - 3 + e) * CH + cl];
+            }
+#pragma unroll
+            for (int e = 0; e < 16; ++e) xv[3 + e] = sX[(16 * g + e) * CH + cl];
+            __syncthreads();
+            const float4 cw = ldg_f4(G(conv_w) + 4 * c);
+            const float cb = G(conv_b)[c];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int r = 16 * g + e;
+                const float y = conv_point(cw, cb, xv[e], xv[e + 1], xv[e + 2], xv[e + 3]);
+                GM(xs)[(m0 + r) * DI + c] = y;
+                uint32_t hi, lo;
+                split2(y, hi, lo);
+                sXh[x_off(r, cl)] = (uint16_t)hi;
+                sXl[x_off(r, cl)] = (uint16_t)lo;
+            }
+            if (g == BM / 16 - 1) {
+                // history ring: inputs of positions p0 + 61, 62, 63 in slots (p0 + 64) mod 3, + 1, + 2
+                const int e0 = (p0m3 + BM) % 3, e1 = (e0 + 1) % 3, e2 = (e0 + 2) % 3;
+                const gmut<float> hb = GM(hist) + b * 3 * DI;
+                hb[e0 * DI + c] = xv[16];
+                hb[e1 * DI + c] = xv[17];
+                hb[e2 * DI + c] = xv[18];
+            }
+        }
+        __syncthreads();
+        // x_proj partial over this chunk's 64 channels (K block k): rows 16 wave .. + 15, fragments 0..2
+        {
+            floatx4 part[3];
+#pragma unroll
+            for (int j = 0; j < 3; ++j) part[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                const int o = x_off(16 * wave + ar, 32 * s + kq);
+                const bf16x8 ah = *reinterpret_cast<const bf16x8*>(&sXh[o]);
+                const bf16x8 al = *reinterpret_cast<const bf16x8*>(&sXl[o]);
+#pragma unroll
+                for (int j = 0; j < 3; ++j) {
+                    const gptr<uint16_t> q = wxp + ((int64_t)j * (DI / 32) + 2 * k + s) * BLK + lane * 8;
+                    const u32x4 bh = ldg16(q);
+                    const u32x4 bl = NT == 3 ? ldg16(q + 512) : bh;
+                    part[j] = mfma_split_step<NT>(part[j], ah, al, __builtin_bit_cast(bf16x8, bh),
+                                                  __builtin_bit_cast(bf16x8, bl));
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 3; ++j) dacc[j] = k == 0 ? part[j] : dacc[j] + part[j];
+        }
+        __syncthreads();  // the next x chunk rewrites sX
+    }
+    // dbc rows 16 wave .. + 15
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) GM(dbc)[(m0 + 16 * wave + m_of + r) * FW + 16 * j + ar] = dacc[j][r];
+}
+
 static int launch_xproj(const float* xs, int64_t M, int di, const uint16_t* Wh, const uint16_t* Wl, float* dbc, int ldd,
                         hipStream_t s) {
     const unsigned grid = (unsigned)((M + 63) / 64);
@@ -1150,12 +1351,12 @@ static GemmArgs gemm_args(const float* A, int64_t lda, const MatW& W, const floa
 // Per-kernel-class event timing (boa_profile / boa_profile_read).
 enum ProfClass {
     PC_EMBED, PC_IN, PC_CONV, PC_XPROJ, PC_SCAN, PC_OUT, PC_FF1, PC_FF2, PC_HEAD1, PC_HEAD2, PC_ENCODE, PC_DECODE,
-    PC_LN, PC_FUSED, PC_FFN, PC_COUNT
+    PC_LN, PC_FUSED, PC_FFN, PC_MIXIN, PC_COUNT
 };
 static const char* kProfNames[PC_COUNT] = {"embed",    "gemm_in_proj", "conv",     "gemm_x_proj",
                                            "scan",     "gemm_out_proj", "gemm_ff1", "gemm_ff2",
                                            "gemm_head1", "gemm_head2", "encode",   "decode",
-                                           "ln_stats", "fused_step", "ffn"};
+                                           "ln_stats", "fused_step", "ffn", "mixin"};
 struct ProfClassState {
     int64_t launches = 0;
     int64_t used = 0;
@@ -1606,6 +1807,22 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc) {
     uint16_t* gh = reinterpret_cast<uint16_t*>(x->xz);
     uint16_t* gl = gh + M * 4 * d;
     int rc = 0;
+    float* hist = x->conv_hist + (int64_t)l * x->max_lanes * 3 * di;
+    const bool mix = split && d == mixin::D && di == mixin::DI && R + 2 * NS == mixin::FW && Tc == mixin::BM &&
+                     w.in_w.p && w.x_w.p;
+    if (mix) {
+        // LN1 + in_proj + conv + SiLU + x_proj in one kernel per lane tile
+        const double flops = gemm_flops(M, 2 * di, d) + gemm_flops(M, R + 2 * NS, di) + 8.0 * M * di;
+        const double bytes = 4.0 * M * (d + di + di + R + 2 * NS) + 4.0 * 6 * B * di;
+        if (w.in_w.l)
+            PROF(PC_MIXIN, flops, bytes,
+                 hipLaunchKernelGGL((k_mixin<3>), dim3((unsigned)B), dim3(256), 0, s, x->x, w.ln1_w, w.ln1_b, w.in_w.p,
+                                    w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs, x->dbc, hist, (int)(x->pos % 3)));
+        else
+            PROF(PC_MIXIN, flops, bytes,
+                 hipLaunchKernelGGL((k_mixin<2>), dim3((unsigned)B), dim3(256), 0, s, x->x, w.ln1_w, w.ln1_b, w.in_w.p,
+                                    w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs, x->dbc, hist, (int)(x->pos % 3)));
+    } else {
     // LN1 + in_proj -> xz [M][2di]
     {
         GemmArgs g = gemm_args(x->x, d, w.in_w, w.in_b, x->xz, 2 * di, M, 2 * di, d);
@@ -1622,7 +1839,6 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc) {
         }
         if (rc) return rc;
     }
-    float* hist = x->conv_hist + (int64_t)l * x->max_lanes * 3 * di;
     if (split && Tc == 1) {
         // decompress step: conv + SiLU + x_proj in one kernel (same arithmetic as the two kernels below)
         const size_t lds = sizeof(float) * 16 * (size_t)(di + 4);
@@ -1650,6 +1866,7 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc) {
              rc = split ? launch_xproj(x->xs, M, di, w.x_w.h, w.x_w.l, x->dbc, R + 2 * NS, s)
                         : (launch_gemm_f32_cfg<64, 64, 0, EPI_NONE>(g, s)));
         if (rc) return rc;
+    }
     }
     }
     // dt_proj + softplus + scan + D + gate: y in place of xs (fp32) or split into ah/al
