@@ -1112,7 +1112,7 @@ static int launch_xproj(const float* xs, int64_t M, int di, const uint16_t* Wh, 
 // ================================================================================================
 // Selective scan, fused with dt_proj + softplus, the D skip and the SiLU(z) gate (App. A of the mixer):
 //   dt = softplus(W_dt . dr + b_dt)                  (torch threshold 20)
-//   h_n <- exp(dt * A_n) * h_n + (dt * B_n) * x      A = -exp(A_log), precomputed as A * log2(e) so the
+//   h_n <- exp(dt * A_n) * h_n + B_n * (dt * x)      A = -exp(A_log), precomputed as A * log2(e) so the
 //                                                    16 exponentials per position are exp2 (v_exp_f32)
 //   y = sum_n h_n * C_n + D * x ;  y <- y * SiLU(z)
 // One thread per (lane, channel), h[16] in registers across the Tc positions; the [dr | B | C] rows of the

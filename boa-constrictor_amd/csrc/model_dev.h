@@ -189,7 +189,7 @@ __device__ __forceinline__ float conv_point(const float4 w, float bias, float h0
 
 // Selective scan, one position of one channel (Mamba's selective_scan_fn on one step):
 //   dt = softplus(dr . dt_w[c] + dt_b[c])     (threshold 20 as F.softplus)
-//   h_n <- exp(dt * A_n) * h_n + dt * B_n * x ;  with a[n] = A_n * log2(e) so exp(dt*A_n) = exp2(dt*a[n])
+//   h_n <- exp(dt * A_n) * h_n + B_n * (dt * x) ;  with a[n] = A_n * log2(e) so exp(dt*A_n) = exp2(dt*a[n])
 //   y = sum_n h_n * C_n + D * x ;  y <- y * SiLU(z)
 // row = [dr (R) | B (NS) | C (NS)] of the position.
 template <int NS, int R>
@@ -201,10 +201,11 @@ __device__ __forceinline__ float scan_position(const float* row, const float (&w
     dt = dt + bdt;
     dt = hw_softplus(dt);
     float y = 0.0f;
+    const float dtx = dt * x;
 #pragma unroll
     for (int n = 0; n < NS; ++n) {
         const float dA = __builtin_amdgcn_exp2f(dt * a[n]);  // v_exp_f32
-        const float dBx = (dt * row[R + n]) * x;
+        const float dBx = row[R + n] * dtx;
         h[n] = __builtin_fmaf(dA, h[n], dBx);
         y = __builtin_fmaf(h[n], row[R + NS + n], y);
     }
