@@ -729,8 +729,8 @@ __global__ void __launch_bounds__(256) k_xproj(const float* __restrict__ xs, int
 // hidden layer, FF1 (+bias, GELU, split) writes the chunk to LDS and FF2 accumulates it into registers, so the
 // hidden activations never leave the chip (the unfused path writes and reads back 4 KiB of them per row).
 // Arithmetic per output is that of the tiled GEMMs and of the fused decode kernel: LN by ln_stats_row /
-// ln_apply / split2; FF1 outputs accumulate their 8 K steps in ascending order through mfma_split_step then
-// epi_value<GELU>; FF2 outputs accumulate all 32 K steps in ascending order (chunk by chunk), then
+// ln_apply / split2; FF1 outputs accumulate their 8 K steps in ascending order through mfma_split_step (its
+// transposed form, same value) then epi_value<GELU>; FF2 outputs accumulate all 32 K steps in ascending order (chunk by chunk), then
 // x + epi_value<RESID>.  So the rows equal those of the layer-by-layer path bit for bit.
 // LDS: A [64][256] (hi, lo) and H [64][64] (hi, lo), bf16, 16-byte chunks XOR-swizzled by row so that 16-row
 // fragment reads touch every bank once; 80 KB, two workgroups per CU.
@@ -780,19 +780,23 @@ __global__ void __launch_bounds__(256, 2) k_ffn(const float* __restrict__ mm, co
     // one coalesced 16-byte load per lane (hi part, then the lo part 512 elements further)
     constexpr int BLK = (NT == 3) ? 1024 : 512;
     const gptr<uint16_t> w1p = G(W1p), w2p = G(W2p);
-    // FF1 of a chunk: wave w computes rows 32 (w & 1) .. + 31 (M fragments mh + 0, 1) x chunk columns
-    // 32 (w >> 1) .. + 31 (N fragments nh + 0, 1).  Its W1 blocks (fragment j, K step s; i = 2 s + j) stream
-    // through a ring of R1 register slots that runs on into the next chunk, so those loads are in flight
-    // during the GELU epilogue, the barriers and FF2.
-    const int mh = 2 * (wave & 1), nh = 2 * (wave >> 1);
-    constexpr int R1 = 4, NB1 = 16;  // ring slots; W1 blocks per wave per chunk
-    u32x4 r1h[R1], r1l[R1];
-    auto issue_w1 = [&](int c, int i) {  // block i of chunk c into slot i % R1
-        const int f = (HC * c) / 16 + nh + (i & 1);
-        const gptr<uint16_t> q = w1p + ((int64_t)f * (D / 32) + (i >> 1)) * BLK + lane * 8;
-        r1h[i % R1] = ldg16(q);
-        r1l[i % R1] = r1h[i % R1];
-        if constexpr (NT == 3) r1l[i % R1] = ldg16(q + 512);
+    // Per chunk c (hidden units 64 c .. 64 c + 63) a wave streams 16 weight blocks through one ring of R
+    // register slots, in the order it uses them:
+    //   i < 8:  W1 block (fragment 4 c + wave, K step i): FF1 of hidden units 64 c + 16 wave .. + 15, all 64 rows;
+    //   i >= 8: W2 block (fragment 4 wave + (i - 8) % 4, K step 2 c + (i - 8) / 4): FF2 of outputs 64 wave .. + 63.
+    // Block i goes to slot i % R and is reloaded with block i + R as soon as it is used, so R blocks are always
+    // in flight: FF2's weights load during FF1, and the next chunk's W1 during FF2, the GELU and the barriers.
+    // FF1 takes the W1 block as the A operand (mfma_split_step_t), so a lane's 4 outputs are 4 consecutive
+    // hidden units of one row: GELU'd and split, they go to LDS as one 8-byte store per part.
+    constexpr int R = 8;
+    u32x4 rh[R], rl[R];
+    auto issue = [&](int c, int i) {
+        const int64_t blk = i < 8 ? (int64_t)(4 * c + wave) * (D / 32) + i
+                                  : (int64_t)(4 * wave + ((i - 8) & 3)) * (DF / 32) + 2 * c + ((i - 8) >> 2);
+        const gptr<uint16_t> q = (i < 8 ? w1p : w2p) + blk * BLK + lane * 8;
+        rh[i % R] = ldg16(q);
+        rl[i % R] = rh[i % R];
+        if constexpr (NT == 3) rl[i % R] = ldg16(q + 512);
     };
     floatx4 out[4][4];  // FF2: M fragment i, output fragment 4 wave + j
 #pragma unroll
@@ -800,76 +804,62 @@ __global__ void __launch_bounds__(256, 2) k_ffn(const float* __restrict__ mm, co
 #pragma unroll
         for (int j = 0; j < 4; ++j) out[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < R1; ++i) issue_w1(0, i);
+    for (int i = 0; i < R; ++i) issue(0, i);
 
 #pragma unroll 1
     for (int c = 0; c < DF / HC; ++c) {
-        // ---- FF1
-        floatx4 hacc[2][2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) hacc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
         const int cn = c + 1 < DF / HC ? c + 1 : c;  // the ring runs on into the next chunk (the last reloads)
+        // ---- FF1 (transposed fragments): hacc[i] lane l = hidden unit 16 wave + m_of + r, row 16 i + ar
+        floatx4 hacc[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) hacc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-            bf16x8 ah[2], al[2];
+            bf16x8 ah[4], al[4];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int o = a_off(16 * (mh + i) + ar, 32 * s + kq);
+            for (int i = 0; i < 4; ++i) {
+                const int o = a_off(16 * i + ar, 32 * s + kq);
                 ah[i] = *reinterpret_cast<const bf16x8*>(&sA[0][o]);
                 al[i] = *reinterpret_cast<const bf16x8*>(&sA[1][o]);
             }
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int b = 2 * s + j;
-#pragma unroll
-                for (int i = 0; i < 2; ++i)
-                    hacc[i][j] = mfma_split_step<NT>(hacc[i][j], ah[i], al[i], __builtin_bit_cast(bf16x8, r1h[b % R1]),
-                                                     __builtin_bit_cast(bf16x8, r1l[b % R1]));
-                if (b + R1 < NB1) issue_w1(c, b + R1);
-                else issue_w1(cn, b + R1 - NB1);
-            }
+            for (int i = 0; i < 4; ++i)
+                hacc[i] = mfma_split_step_t<NT>(hacc[i], ah[i], al[i], __builtin_bit_cast(bf16x8, rh[s % R]),
+                                                __builtin_bit_cast(bf16x8, rl[s % R]));
+            issue(c, s + 8);
         }
-        // FF2 weights of this chunk: outputs 16 (4 wave + j) + lane % 16, K steps 2c, 2c + 1 (they load during the GELU epilogue and the barrier)
-        u32x4 b2h[4][2], b2l[4][2];
+        {
+            const float4 bias = ldg_f4(G(b1) + HC * c + 16 * wave + m_of);
+            const float bv[4] = {bias.x, bias.y, bias.z, bias.w};
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+            for (int i = 0; i < 4; ++i) {
+                uint32_t hi[4], lo[4];
 #pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                const gptr<uint16_t> q = w2p + ((int64_t)(4 * wave + j) * (DF / 32) + (HC * c) / 32 + s) * BLK + lane * 8;
-                b2h[j][s] = ldg16(q);
-                b2l[j][s] = b2h[j][s];
-                if constexpr (NT == 3) b2l[j][s] = ldg16(q + 512);
+                for (int r = 0; r < 4; ++r) split2(epi_value<EPI_GELU>(hacc[i][r], bv[r]), hi[r], lo[r]);
+                const int o = h_off(16 * i + ar, 16 * wave + m_of);
+                *reinterpret_cast<uint2*>(&sH[0][o]) = make_uint2(hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16));
+                *reinterpret_cast<uint2*>(&sH[1][o]) = make_uint2(lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16));
             }
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int hc = 16 * (nh + j) + ar;  // column within the chunk
-            const float bias = G(b1)[HC * c + hc];
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    uint32_t hi, lo;
-                    split2(epi_value<EPI_GELU>(hacc[i][j][r], bias), hi, lo);
-                    const int o = h_off(16 * (mh + i) + m_of + r, hc);
-                    sH[0][o] = (uint16_t)hi;
-                    sH[1][o] = (uint16_t)lo;
-                }
         }
         __syncthreads();
         // ---- FF2: accumulate this chunk (K steps 2c, 2c + 1) into all 64 rows x this wave's 64 outputs
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
+        for (int t = 0; t < 2; ++t) {
+            bf16x8 ah[4], al[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int o = h_off(16 * i + ar, 32 * s + kq);
-                const bf16x8 ah = *reinterpret_cast<const bf16x8*>(&sH[0][o]);
-                const bf16x8 al = *reinterpret_cast<const bf16x8*>(&sH[1][o]);
+                const int o = h_off(16 * i + ar, 32 * t + kq);
+                ah[i] = *reinterpret_cast<const bf16x8*>(&sH[0][o]);
+                al[i] = *reinterpret_cast<const bf16x8*>(&sH[1][o]);
+            }
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    out[i][j] = mfma_split_step<NT>(out[i][j], ah, al, __builtin_bit_cast(bf16x8, b2h[j][s]),
-                                                    __builtin_bit_cast(bf16x8, b2l[j][s]));
+            for (int j = 0; j < 4; ++j) {
+                const int slot = (8 + 4 * t + j) % R;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    out[i][j] = mfma_split_step<NT>(out[i][j], ah[i], al[i], __builtin_bit_cast(bf16x8, rh[slot]),
+                                                    __builtin_bit_cast(bf16x8, rl[slot]));
+                issue(cn, 4 * t + j);
             }
         }
         __syncthreads();  // the next chunk rewrites H
@@ -951,7 +941,7 @@ __global__ void __launch_bounds__(256, 2) k_mixin(const float* __restrict__ x, c
     // in_proj chunk k (columns CH k .. CH k + 63; chunks 0..7 are x, 8..15 are z): wave w computes rows
     // 32 (w & 1) .. + 31 x chunk columns 32 (w >> 1) .. + 31.  Chunk order: z first (8..15), then x (0..7).
     const int mh = 2 * (wave & 1), nh = 2 * (wave >> 1);
-    constexpr int R1 = 4, NB1 = 16, NCH = 2 * DI / CH;
+    constexpr int R1 = 8, NB1 = 16, NCH = 2 * DI / CH;
     auto chunk_of = [](int i) { return i < NCH / 2 ? NCH / 2 + i : i - NCH / 2; };  // i-th chunk processed
     u32x4 r1h[R1], r1l[R1];
     auto issue_w = [&](int k, int i) {  // block i (fragment nh + (i & 1), K step i >> 1) of chunk k

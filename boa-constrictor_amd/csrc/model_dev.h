@@ -135,6 +135,17 @@ __device__ __forceinline__ floatx4 mfma_split_step(floatx4 acc, bf16x8 ah, bf16x
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
 }
 
+// The same step with the operand roles swapped: acc^T += B^T A^T, i.e. the output fragment transposed (lane l
+// holds column 4 (l / 16) + r, row l % 16).  Each output element gets the same three products (exact in fp32)
+// summed over the same K slice in the same order, so it equals mfma_split_step's bit for bit.  Used where the
+// fragment-packed weight block is the A operand, which makes a lane's 4 outputs consecutive columns.
+template <int NT>
+__device__ __forceinline__ floatx4 mfma_split_step_t(floatx4 acc, bf16x8 ah, bf16x8 al, bf16x8 bh, bf16x8 bl) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bh, al, acc, 0, 0, 0);
+    if constexpr (NT == 3) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bl, ah, acc, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(bh, ah, acc, 0, 0, 0);
+}
+
 // x_proj (d_inner -> dt_rank + 2 d_state) in the split modes is a sum of K-block partials:
 //   dbc = P_0 + P_1 + ... + P_{d_inner/64 - 1}   (left to right, fp32 adds)
 // where P_q accumulates the two 32-wide K steps of channels 64q .. 64q + 63 from zero.  The fused decode
@@ -151,8 +162,9 @@ __device__ __forceinline__ float hw_exp(float x) { return __builtin_amdgcn_exp2f
 __device__ __forceinline__ float hw_silu(float x) { return x * __builtin_amdgcn_rcpf(1.0f + hw_exp(-x)); }
 // softplus(x) = log(1 + e^x) (F.softplus: x itself above 20), as max(x, 0) + log1p(e^-|x|); log1p(e) for
 // e in (0, 1] as log(u) * e / (u - 1) with u = 1 + e (Goldberg), exact to rounding also when u rounds to 1.
+// No branch for F.softplus's threshold: above 20, e < 2^-28 rounds u to 1, so l1p = e, and x + e rounds to x
+// (e is below half an ulp of x), which is the thresholded value bit for bit.
 __device__ __forceinline__ float hw_softplus(float x) {
-    if (x > 20.0f) return x;
     const float e = hw_exp(-fabsf(x));
     const float u = 1.0f + e;
     const float d = u - 1.0f;
