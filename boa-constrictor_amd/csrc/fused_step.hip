@@ -130,11 +130,10 @@ __device__ __forceinline__ void ln_rows(const float* src, const float* __restric
         ln_stats_row<1>(v, mu, rs);
         const float y[4] = {ln_apply(v[0], mu, rs, wv.x, bv.x), ln_apply(v[1], mu, rs, wv.y, bv.y),
                             ln_apply(v[2], mu, rs, wv.z, bv.z), ln_apply(v[3], mu, rs, wv.w, bv.w)};
-        uint32_t h[4], l[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) split2(y[j], h[j], l[j]);
-        *reinterpret_cast<uint2*>(sAh + r * LA + 4 * lane) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
-        *reinterpret_cast<uint2*>(sAl + r * LA + 4 * lane) = make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
+        uint2 hp, lp;
+        split4(y[0], y[1], y[2], y[3], hp, lp);
+        *reinterpret_cast<uint2*>(sAh + r * LA + 4 * lane) = hp;
+        *reinterpret_cast<uint2*>(sAl + r * LA + 4 * lane) = lp;
     }
 }
 

@@ -319,13 +319,10 @@ __global__ void __launch_bounds__(256, (BK > 32) ? 1 : 2) k_gemm_bf(GemmArgs g) 
             } else {
                 const int off = lds_off(q / (BK / 4), (q % (BK / 4)) * 4);
                 const u32x4 v = sa_h[S][i];
-                uint32_t h0, h1, h2, h3, l0, l1, l2, l3;
-                split2(__uint_as_float(v.x), h0, l0);
-                split2(__uint_as_float(v.y), h1, l1);
-                split2(__uint_as_float(v.z), h2, l2);
-                split2(__uint_as_float(v.w), h3, l3);
-                *reinterpret_cast<uint2*>(&sAh[buf][off]) = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
-                *reinterpret_cast<uint2*>(&sAl[buf][off]) = make_uint2(l0 | (l1 << 16), l2 | (l3 << 16));
+                uint2 hp, lp;
+                split4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w), hp, lp);
+                *reinterpret_cast<uint2*>(&sAh[buf][off]) = hp;
+                *reinterpret_cast<uint2*>(&sAl[buf][off]) = lp;
             }
         }
 #pragma unroll
@@ -430,13 +427,10 @@ __global__ void __launch_bounds__(256, (BK > 32) ? 1 : 2) k_gemm_bf(GemmArgs g) 
             v = make_float4(rv.x + v.x, rv.y + v.y, rv.z + v.z, rv.w + v.w);
         }
         if constexpr (OUTS) {
-            uint32_t h0, h1, h2, h3, l0, l1, l2, l3;
-            split2(v.x, h0, l0);
-            split2(v.y, h1, l1);
-            split2(v.z, h2, l2);
-            split2(v.w, h3, l3);
-            *reinterpret_cast<uint2*>(g.Ch + row * g.ldc + col) = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
-            *reinterpret_cast<uint2*>(g.Cl + row * g.ldc + col) = make_uint2(l0 | (l1 << 16), l2 | (l3 << 16));
+            uint2 hp, lp;
+            split4(v.x, v.y, v.z, v.w, hp, lp);
+            *reinterpret_cast<uint2*>(g.Ch + row * g.ldc + col) = hp;
+            *reinterpret_cast<uint2*>(g.Cl + row * g.ldc + col) = lp;
         } else {
             *reinterpret_cast<float4*>(g.C + row * g.ldc + col) = v;
         }
@@ -543,11 +537,10 @@ __global__ void __launch_bounds__(256) k_ln_split(const float* __restrict__ A, i
         const float4 bv = *reinterpret_cast<const float4*>(bvec + c);
         const float y[4] = {ln_apply(v[4 * i + 0], mu, rs, wv.x, bv.x), ln_apply(v[4 * i + 1], mu, rs, wv.y, bv.y),
                             ln_apply(v[4 * i + 2], mu, rs, wv.z, bv.z), ln_apply(v[4 * i + 3], mu, rs, wv.w, bv.w)};
-        uint32_t h[4], l[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) split2(y[j], h[j], l[j]);
-        *reinterpret_cast<uint2*>(Ah + m * lda + c) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
-        *reinterpret_cast<uint2*>(Al + m * lda + c) = make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
+        uint2 hp, lp;
+        split4(y[0], y[1], y[2], y[3], hp, lp);
+        *reinterpret_cast<uint2*>(Ah + m * lda + c) = hp;
+        *reinterpret_cast<uint2*>(Al + m * lda + c) = lp;
     }
 }
 
@@ -765,12 +758,11 @@ __global__ void __launch_bounds__(256, 2) k_ffn(const float* __restrict__ mm, co
             ln_stats_row<1>(v, mu, rs);
             const float y[4] = {ln_apply(v[0], mu, rs, wv.x, bv.x), ln_apply(v[1], mu, rs, wv.y, bv.y),
                                 ln_apply(v[2], mu, rs, wv.z, bv.z), ln_apply(v[3], mu, rs, wv.w, bv.w)};
-            uint32_t h[4], l[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) split2(y[j], h[j], l[j]);
+            uint2 hp, lp;
+            split4(y[0], y[1], y[2], y[3], hp, lp);
             const int o = a_off(r, 4 * lane);
-            *reinterpret_cast<uint2*>(&sA[0][o]) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
-            *reinterpret_cast<uint2*>(&sA[1][o]) = make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
+            *reinterpret_cast<uint2*>(&sA[0][o]) = hp;
+            *reinterpret_cast<uint2*>(&sA[1][o]) = lp;
         }
     }
     __syncthreads();
@@ -833,12 +825,14 @@ __global__ void __launch_bounds__(256, 2) k_ffn(const float* __restrict__ mm, co
             const float bv[4] = {bias.x, bias.y, bias.z, bias.w};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                uint32_t hi[4], lo[4];
+                float g[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) split2(epi_value<EPI_GELU>(hacc[i][r], bv[r]), hi[r], lo[r]);
+                for (int r = 0; r < 4; ++r) g[r] = epi_value<EPI_GELU>(hacc[i][r], bv[r]);
+                uint2 hp, lp;
+                split4(g[0], g[1], g[2], g[3], hp, lp);
                 const int o = h_off(16 * i + ar, 16 * wave + m_of);
-                *reinterpret_cast<uint2*>(&sH[0][o]) = make_uint2(hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16));
-                *reinterpret_cast<uint2*>(&sH[1][o]) = make_uint2(lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16));
+                *reinterpret_cast<uint2*>(&sH[0][o]) = hp;
+                *reinterpret_cast<uint2*>(&sH[1][o]) = lp;
             }
         }
         __syncthreads();
@@ -887,8 +881,9 @@ __global__ void __launch_bounds__(256, 2) k_ffn(const float* __restrict__ mm, co
 //   LN1 -> in_proj (+bias) -> z to HBM; x -> causal conv + SiLU over the 64 positions -> xs to HBM ->
 //   x_proj -> dbc to HBM; the conv history ring of the lane advanced by 64 positions.
 // A workgroup owns one lane's tile (rows b*64 .. b*64 + 63, positions p0 .. p0 + 63).  LN1 output is the split
-// operand in LDS (as in k_ffn).  in_proj runs in 64-column chunks (each wave a 32 x 32 block, fragment-packed
-// weights through a register ring running on across chunks): the 8 z chunks are stored as they finish; each
+// operand in LDS (as in k_ffn).  in_proj runs in 64-column chunks (each wave 16 columns x all 64 rows, the
+// fragment-packed weight block as the MFMA A operand, through a register ring running on across chunks; a
+// lane's 4 outputs are 4 consecutive columns of one row): the 8 z chunks are stored as they finish; each
 // x chunk goes through LDS for the conv over time (the conv output, split, then replaces it in place) and
 // into x_proj's partial over those 64 channels, which is exactly x_proj's K block, folded into dbc in
 // registers (dbc = P_0 + P_1 + ...).  Arithmetic per value is that of the layer-by-layer kernels (ln_*,
@@ -896,6 +891,9 @@ __global__ void __launch_bounds__(256, 2) k_ffn(const float* __restrict__ mm, co
 namespace mixin {
 constexpr int BM = 64, D = 256, DI = 512, CH = 64, FW = 48;
 __device__ __forceinline__ int x_off(int r, int k) { return r * CH + (((k >> 3) ^ (r >> 1)) & 7) * 8 + (k & 7); }
+// fp32 x chunk [64][64]: 16-byte groups XOR-swizzled by row, so both the in_proj stores (a lane's 4 columns, 16
+// rows per instruction) and the conv's column reads (64 channels of one row) are free of bank conflicts
+__device__ __forceinline__ int sx_off(int r, int c) { return r * CH + ((((c >> 2) ^ r) & 15) << 2) + (c & 3); }
 }  // namespace mixin
 
 template <int NT>
@@ -926,33 +924,33 @@ __global__ void __launch_bounds__(256, 2) k_mixin(const float* __restrict__ x, c
             ln_stats_row<1>(v, mu, rs);
             const float y[4] = {ln_apply(v[0], mu, rs, wv.x, bv.x), ln_apply(v[1], mu, rs, wv.y, bv.y),
                                 ln_apply(v[2], mu, rs, wv.z, bv.z), ln_apply(v[3], mu, rs, wv.w, bv.w)};
-            uint32_t h[4], l[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) split2(y[j], h[j], l[j]);
+            uint2 hp, lp;
+            split4(y[0], y[1], y[2], y[3], hp, lp);
             const int o = ffn::a_off(r, 4 * lane);
-            *reinterpret_cast<uint2*>(&sA[0][o]) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
-            *reinterpret_cast<uint2*>(&sA[1][o]) = make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
+            *reinterpret_cast<uint2*>(&sA[0][o]) = hp;
+            *reinterpret_cast<uint2*>(&sA[1][o]) = lp;
         }
     }
     __syncthreads();
 
     const int ar = lane & 15, kq = 8 * (lane >> 4), m_of = 4 * (lane >> 4);
     const gptr<uint16_t> wip = G(Wip), wxp = G(Wxp);
-    // in_proj chunk k (columns CH k .. CH k + 63; chunks 0..7 are x, 8..15 are z): wave w computes rows
-    // 32 (w & 1) .. + 31 x chunk columns 32 (w >> 1) .. + 31.  Chunk order: z first (8..15), then x (0..7).
-    const int mh = 2 * (wave & 1), nh = 2 * (wave >> 1);
-    constexpr int R1 = 8, NB1 = 16, NCH = 2 * DI / CH;
+    // in_proj chunk k (columns CH k .. CH k + 63; chunks 0..7 are x, 8..15 are z): wave w computes columns
+    // CH k + 16 w .. + 15 for all 64 rows, with the weight block (fragment 4 k + w, K step s) as the A operand
+    // (mfma_split_step_t): lane l holds columns 16 w + m_of + r of row 16 i + ar.  The 8 blocks of a chunk
+    // stream through 8 register slots, slot s reloaded with K step s of the next chunk right after its use.
+    // Chunk order: z first (8..15), then x (0..7).
+    constexpr int R1 = 8, NCH = 2 * DI / CH;
     auto chunk_of = [](int i) { return i < NCH / 2 ? NCH / 2 + i : i - NCH / 2; };  // i-th chunk processed
     u32x4 r1h[R1], r1l[R1];
-    auto issue_w = [&](int k, int i) {  // block i (fragment nh + (i & 1), K step i >> 1) of chunk k
-        const int f = (CH * k) / 16 + nh + (i & 1);
-        const gptr<uint16_t> q = wip + ((int64_t)f * (D / 32) + (i >> 1)) * BLK + lane * 8;
-        r1h[i % R1] = ldg16(q);
-        r1l[i % R1] = r1h[i % R1];
-        if constexpr (NT == 3) r1l[i % R1] = ldg16(q + 512);
+    auto issue_w = [&](int k, int s) {  // block (fragment 4 k + wave, K step s) into slot s
+        const gptr<uint16_t> q = wip + ((int64_t)((CH / 16) * k + wave) * (D / 32) + s) * BLK + lane * 8;
+        r1h[s] = ldg16(q);
+        r1l[s] = r1h[s];
+        if constexpr (NT == 3) r1l[s] = ldg16(q + 512);
     };
 #pragma unroll
-    for (int i = 0; i < R1; ++i) issue_w(chunk_of(0), i);
+    for (int s = 0; s < R1; ++s) issue_w(chunk_of(0), s);
     floatx4 dacc[3];  // x_proj (dbc) of rows 16 wave .. + 15, fragments 0..2
 #pragma unroll
     for (int j = 0; j < 3; ++j) dacc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -962,55 +960,41 @@ __global__ void __launch_bounds__(256, 2) k_mixin(const float* __restrict__ x, c
     for (int ci = 0; ci < NCH; ++ci) {
         const int k = chunk_of(ci);
         const int kn = chunk_of(ci + 1 < NCH ? ci + 1 : ci);
-        floatx4 acc[2][2];
+        floatx4 acc[4];
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < 4; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < D / 32; ++s) {
-            bf16x8 ah[2], al[2];
+            bf16x8 ah[4], al[4];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int o = ffn::a_off(16 * (mh + i) + ar, 32 * s + kq);
+            for (int i = 0; i < 4; ++i) {
+                const int o = ffn::a_off(16 * i + ar, 32 * s + kq);
                 ah[i] = *reinterpret_cast<const bf16x8*>(&sA[0][o]);
                 al[i] = *reinterpret_cast<const bf16x8*>(&sA[1][o]);
             }
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int bi = 2 * s + j;
-#pragma unroll
-                for (int i = 0; i < 2; ++i)
-                    acc[i][j] = mfma_split_step<NT>(acc[i][j], ah[i], al[i], __builtin_bit_cast(bf16x8, r1h[bi % R1]),
-                                                    __builtin_bit_cast(bf16x8, r1l[bi % R1]));
-                if (bi + R1 < NB1) issue_w(k, bi + R1);
-                else issue_w(kn, bi + R1 - NB1);
-            }
+            for (int i = 0; i < 4; ++i)
+                acc[i] = mfma_split_step_t<NT>(acc[i], ah[i], al[i], __builtin_bit_cast(bf16x8, r1h[s]),
+                                               __builtin_bit_cast(bf16x8, r1l[s]));
+            issue_w(kn, s);
         }
+        const int cl0 = 16 * wave + m_of;  // first of this lane's 4 columns within the chunk
+        const float4 bias = ldg_f4(G(bin) + CH * k + cl0);
         if (k >= NCH / 2) {
             // z chunk: straight to HBM (the scan reads it)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int col = CH * k + 16 * (nh + j) + ar;
-                const float bias = G(bin)[col];
-#pragma unroll
-                for (int i = 0; i < 2; ++i)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        GM(xz)[(m0 + 16 * (mh + i) + m_of + r) * (2 * DI) + col] = epi_value<EPI_BIAS>(acc[i][j][r], bias);
-            }
+            for (int i = 0; i < 4; ++i)
+                stg_f4(GM(xz) + (m0 + 16 * i + ar) * (2 * DI) + CH * k + cl0,
+                       make_float4(epi_value<EPI_BIAS>(acc[i][0], bias.x), epi_value<EPI_BIAS>(acc[i][1], bias.y),
+                                   epi_value<EPI_BIAS>(acc[i][2], bias.z), epi_value<EPI_BIAS>(acc[i][3], bias.w)));
             continue;
         }
         // x chunk: fp32 to LDS for the conv over time
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int cl = 16 * (nh + j) + ar;
-            const float bias = G(bin)[CH * k + cl];
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) sX[(16 * (mh + i) + m_of + r) * CH + cl] = epi_value<EPI_BIAS>(acc[i][j][r], bias);
-        }
+        for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<float4*>(&sX[sx_off(16 * i + ar, cl0)]) =
+                make_float4(epi_value<EPI_BIAS>(acc[i][0], bias.x), epi_value<EPI_BIAS>(acc[i][1], bias.y),
+                            epi_value<EPI_BIAS>(acc[i][2], bias.z), epi_value<EPI_BIAS>(acc[i][3], bias.w));
         __syncthreads();
         // conv + SiLU: thread = (channel cl, rows 16 g .. 16 g + 15); inputs read before the barrier, the split
         // output written over them after it
@@ -1025,10 +1009,10 @@ __global__ void __launch_bounds__(256, 2) k_mixin(const float* __restrict__ x, c
                 xv[2] = hb[s2 * DI + c];
             } else {
 #pragma unroll
-                for (int e = 0; e < 3; ++e) xv[e] = sX[(16 * g - 3 + e) * CH + cl];
+                for (int e = 0; e < 3; ++e) xv[e] = sX[sx_off(16 * g - 3 + e, cl)];
             }
 #pragma unroll
-            for (int e = 0; e < 16; ++e) xv[3 + e] = sX[(16 * g + e) * CH + cl];
+            for (int e = 0; e < 16; ++e) xv[3 + e] = sX[sx_off(16 * g + e, cl)];
             __syncthreads();
             const float4 cw = ldg_f4(G(conv_w) + 4 * c);
             const float cb = G(conv_b)[c];
