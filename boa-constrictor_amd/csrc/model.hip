@@ -801,6 +801,9 @@ __global__ void __launch_bounds__(256, 2) k_ffn(const float* __restrict__ mm, co
 #pragma unroll 1
     for (int c = 0; c < DF / HC; ++c) {
         const int cn = c + 1 < DF / HC ? c + 1 : c;  // the ring runs on into the next chunk (the last reloads)
+        // FF1 bias of this lane's 4 hidden units, loaded ahead of the ring's W2 blocks (memory loads complete in
+        // issue order as far as the wait counter goes: a later load would make its use wait for all 8 blocks)
+        const float4 bias = ldg_f4(G(b1) + HC * c + 16 * wave + m_of);
         // ---- FF1 (transposed fragments): hacc[i] lane l = hidden unit 16 wave + m_of + r, row 16 i + ar
         floatx4 hacc[4];
 #pragma unroll
@@ -819,9 +822,9 @@ __global__ void __launch_bounds__(256, 2) k_ffn(const float* __restrict__ mm, co
                 hacc[i] = mfma_split_step_t<NT>(hacc[i], ah[i], al[i], __builtin_bit_cast(bf16x8, rh[s % R]),
                                                 __builtin_bit_cast(bf16x8, rl[s % R]));
             issue(c, s + 8);
+            pin_loads();
         }
         {
-            const float4 bias = ldg_f4(G(b1) + HC * c + 16 * wave + m_of);
             const float bv[4] = {bias.x, bias.y, bias.z, bias.w};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -854,6 +857,7 @@ __global__ void __launch_bounds__(256, 2) k_ffn(const float* __restrict__ mm, co
                     out[i][j] = mfma_split_step<NT>(out[i][j], ah[i], al[i], __builtin_bit_cast(bf16x8, rh[slot]),
                                                     __builtin_bit_cast(bf16x8, rl[slot]));
                 issue(cn, 4 * t + j);
+                pin_loads();
             }
         }
         __syncthreads();  // the next chunk rewrites H
@@ -960,6 +964,9 @@ __global__ void __launch_bounds__(256, 2) k_mixin(const float* __restrict__ x, c
     for (int ci = 0; ci < NCH; ++ci) {
         const int k = chunk_of(ci);
         const int kn = chunk_of(ci + 1 < NCH ? ci + 1 : ci);
+        const int cl0 = 16 * wave + m_of;  // first of this lane's 4 columns within the chunk
+        // loaded ahead of the ring's next blocks: its use must not wait for them (in-order wait counter)
+        const float4 bias = ldg_f4(G(bin) + CH * k + cl0);
         floatx4 acc[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -977,9 +984,8 @@ __global__ void __launch_bounds__(256, 2) k_mixin(const float* __restrict__ x, c
                 acc[i] = mfma_split_step_t<NT>(acc[i], ah[i], al[i], __builtin_bit_cast(bf16x8, r1h[s]),
                                                __builtin_bit_cast(bf16x8, r1l[s]));
             issue_w(kn, s);
+            pin_loads();
         }
-        const int cl0 = 16 * wave + m_of;  // first of this lane's 4 columns within the chunk
-        const float4 bias = ldg_f4(G(bin) + CH * k + cl0);
         if (k >= NCH / 2) {
             // z chunk: straight to HBM (the scan reads it)
 #pragma unroll
@@ -997,25 +1003,40 @@ __global__ void __launch_bounds__(256, 2) k_mixin(const float* __restrict__ x, c
                             epi_value<EPI_BIAS>(acc[i][2], bias.z), epi_value<EPI_BIAS>(acc[i][3], bias.w));
         __syncthreads();
         // conv + SiLU: thread = (channel cl, rows 16 g .. 16 g + 15); inputs read before the barrier, the split
-        // output written over them after it
+        // output written over them after it.  g is the wave index, so the history descriptors below are
+        // wave-uniform: wave 0 reads the 3 history inputs (the others read nothing: empty range, value 0) and
+        // wave 3 writes the ring back; no memory access sits under a branch.
+        bf16x8 xwh[2][3], xwl[2][3];  // x_proj weight blocks of K block k (in flight during the conv)
         {
-            const int cl = tid & (CH - 1), g = tid >> 6;
+            const int cl = tid & (CH - 1), g = wave;
             const int c = CH * k + cl;
-            float xv[19];
-            if (g == 0) {
-                const gptr<float> hb = G(hist) + b * 3 * DI;
-                xv[0] = hb[p0m3 * DI + c];
-                xv[1] = hb[s1 * DI + c];
-                xv[2] = hb[s2 * DI + c];
-            } else {
+            const float4 cw = ldg_f4(G(conv_w) + 4 * c);
+            const float cb = G(conv_b)[c];
+            const __amdgpu_buffer_rsrc_t hr =
+                buf_rsrc(hist + b * 3 * DI, g == 0 ? 3 * DI * 4 : 0);
+            const float h0 = buf_ld1(hr, (uint32_t)(p0m3 * DI + c) * 4), h1 = buf_ld1(hr, (uint32_t)(s1 * DI + c) * 4),
+                        h2 = buf_ld1(hr, (uint32_t)(s2 * DI + c) * 4);
 #pragma unroll
-                for (int e = 0; e < 3; ++e) xv[e] = sX[sx_off(16 * g - 3 + e, cl)];
-            }
+            for (int s = 0; s < 2; ++s)
+#pragma unroll
+                for (int j = 0; j < 3; ++j) {
+                    const gptr<uint16_t> q = wxp + ((int64_t)j * (DI / 32) + 2 * k + s) * BLK + lane * 8;
+                    const u32x4 bh = ldg16(q);
+                    xwh[s][j] = __builtin_bit_cast(bf16x8, bh);
+                    xwl[s][j] = NT == 3 ? __builtin_bit_cast(bf16x8, ldg16(q + 512)) : xwh[s][j];
+                }
+            pin_loads();
+            float xv[19];
+#pragma unroll
+            for (int e = 0; e < 3; ++e) xv[e] = sX[sx_off(g == 0 ? 0 : 16 * g - 3 + e, cl)];
 #pragma unroll
             for (int e = 0; e < 16; ++e) xv[3 + e] = sX[sx_off(16 * g + e, cl)];
             __syncthreads();
-            const float4 cw = ldg_f4(G(conv_w) + 4 * c);
-            const float cb = G(conv_b)[c];
+            if (g == 0) {
+                xv[0] = h0;
+                xv[1] = h1;
+                xv[2] = h2;
+            }
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int r = 16 * g + e;
@@ -1026,14 +1047,12 @@ __global__ void __launch_bounds__(256, 2) k_mixin(const float* __restrict__ x, c
                 sXh[x_off(r, cl)] = (uint16_t)hi;
                 sXl[x_off(r, cl)] = (uint16_t)lo;
             }
-            if (g == BM / 16 - 1) {
-                // history ring: inputs of positions p0 + 61, 62, 63 in slots (p0 + 64) mod 3, + 1, + 2
-                const int e0 = (p0m3 + BM) % 3, e1 = (e0 + 1) % 3, e2 = (e0 + 2) % 3;
-                const gmut<float> hb = GM(hist) + b * 3 * DI;
-                hb[e0 * DI + c] = xv[16];
-                hb[e1 * DI + c] = xv[17];
-                hb[e2 * DI + c] = xv[18];
-            }
+            // history ring: inputs of positions p0 + 61, 62, 63 in slots (p0 + 64) mod 3, + 1, + 2 (wave 3)
+            const int e0 = (p0m3 + BM) % 3, e1 = (e0 + 1) % 3, e2 = (e0 + 2) % 3;
+            const __amdgpu_buffer_rsrc_t hw = buf_rsrc(hist + b * 3 * DI, g == BM / 16 - 1 ? 3 * DI * 4 : 0);
+            buf_st1(hw, (uint32_t)(e0 * DI + c) * 4, xv[16]);
+            buf_st1(hw, (uint32_t)(e1 * DI + c) * 4, xv[17]);
+            buf_st1(hw, (uint32_t)(e2 * DI + c) * 4, xv[18]);
         }
         __syncthreads();
         // x_proj partial over this chunk's 64 channels (K block k): rows 16 wave .. + 15, fragments 0..2
@@ -1047,13 +1066,7 @@ __global__ void __launch_bounds__(256, 2) k_mixin(const float* __restrict__ x, c
                 const bf16x8 ah = *reinterpret_cast<const bf16x8*>(&sXh[o]);
                 const bf16x8 al = *reinterpret_cast<const bf16x8*>(&sXl[o]);
 #pragma unroll
-                for (int j = 0; j < 3; ++j) {
-                    const gptr<uint16_t> q = wxp + ((int64_t)j * (DI / 32) + 2 * k + s) * BLK + lane * 8;
-                    const u32x4 bh = ldg16(q);
-                    const u32x4 bl = NT == 3 ? ldg16(q + 512) : bh;
-                    part[j] = mfma_split_step<NT>(part[j], ah, al, __builtin_bit_cast(bf16x8, bh),
-                                                  __builtin_bit_cast(bf16x8, bl));
-                }
+                for (int j = 0; j < 3; ++j) part[j] = mfma_split_step<NT>(part[j], ah, al, xwh[s][j], xwl[s][j]);
             }
 #pragma unroll
             for (int j = 0; j < 3; ++j) dacc[j] = k == 0 ? part[j] : dacc[j] + part[j];

@@ -157,6 +157,11 @@ __device__ __forceinline__ floatx4 mfma_split_step_t(floatx4 acc, bf16x8 ah, bf1
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(bh, ah, acc, 0, 0, 0);
 }
 
+// Keeps the memory loads issued so far at this point of the schedule (ALU, MFMA and LDS instructions may still
+// move across).  Without it the scheduler sinks a register ring's prefetches down to their uses, and the ring
+// no longer hides any latency.
+__device__ __forceinline__ void pin_loads() { asm volatile("" ::: "memory"); }
+
 // x_proj (d_inner -> dt_rank + 2 d_state) in the split modes is a sum of K-block partials:
 //   dbc = P_0 + P_1 + ... + P_{d_inner/64 - 1}   (left to right, fp32 adds)
 // where P_q accumulates the two 32-wide K steps of channels 64q .. 64q + 63 from zero.  The fused decode
