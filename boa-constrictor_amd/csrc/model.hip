@@ -1102,9 +1102,11 @@ static int launch_xproj(const float* xs, int64_t M, int di, const uint16_t* Wh, 
 //   h_n <- exp(dt * A_n) * h_n + B_n * (dt * x)      A = -exp(A_log), precomputed as A * log2(e) so the
 //                                                    16 exponentials per position are exp2 (v_exp_f32)
 //   y = sum_n h_n * C_n + D * x ;  y <- y * SiLU(z)
-// One thread per (lane, channel), h[16] in registers across the Tc positions; the [dr | B | C] rows of the
-// lane's positions are staged in LDS (uniform across the workgroup).  State [lane][di][NS] in HBM between
-// launches.  y overwrites x in place.
+// One thread per (lane, channel), h[16] in registers across the Tc positions.  The [dr | B | C] row of a
+// position is uniform across the workgroup and read-only here, so the compiler reads it with scalar loads
+// into SGPRs (3 x 16 dwords per position): no LDS staging, no per-position LDS reads, and 77 VGPRs, which
+// gives 6 waves per SIMD instead of 5 (the scan is latency-bound at that occupancy: 346 -> 316 ms per
+// 16 MiB).  State [lane][di][NS] in HBM between launches.  y overwrites x in place.
 // The per-position arithmetic is scan_position (shared with the fused decompress-step kernel).
 
 template <int NS, int R>
@@ -1152,16 +1154,9 @@ __global__ void __launch_bounds__(256) k_scan(float* __restrict__ xs_y, const fl
                                              const float* __restrict__ Aneg, const float* __restrict__ Dp,
                                              float* __restrict__ ssm, int di, int Tc, uint16_t* __restrict__ yh,
                                              uint16_t* __restrict__ yl) {
-    extern __shared__ float s_dbc[];
-    constexpr int W = R + 2 * NS;
     const int64_t b = blockIdx.y;
     const int c = blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t row0 = b * Tc;
-    for (int i = threadIdx.x; i < Tc * W; i += blockDim.x) {
-        const int t = i / W, k = i - t * W;
-        s_dbc[i] = dbc[(row0 + t) * ldd + k];
-    }
-    __syncthreads();
     if (c >= di) return;
     float h[NS], a[NS], wr[R];
     float* hp = ssm + b * di * NS + 4 * c;
@@ -1172,11 +1167,12 @@ __global__ void __launch_bounds__(256) k_scan(float* __restrict__ xs_y, const fl
     for (int t = 0; t < Tc; ++t) {
         const int64_t m = row0 + t;
         const float x = xn, z = zn;
-        if (t + 1 < Tc) {  // next position's inputs in flight while this one computes
-            xn = xs_y[(m + 1) * di + c];
-            zn = xz[(m + 1) * ldxz + di + c];
-        }
-        scan_store_y<OUTS>(xs_y, yh, yl, m * di + c, scan_position<NS, R>(s_dbc + t * W, wr, bdt, a, Dc, x, z, h));
+        // next position's inputs in flight while this one computes (the last position reloads its own: no
+        // load under a branch, and a loop the register allocator keeps free of copies)
+        const int64_t mn = t + 1 < Tc ? m + 1 : m;
+        xn = xs_y[mn * di + c];
+        zn = xz[mn * ldxz + di + c];
+        scan_store_y<OUTS>(xs_y, yh, yl, m * di + c, scan_position<NS, R>(dbc + m * ldd, wr, bdt, a, Dc, x, z, h));
     }
     scan_store_channel<NS>(hp, di, h);
 }
@@ -1769,13 +1765,12 @@ static void launch_ln_split(boa_ctx* x, const float* A, int64_t M, const float* 
 template <int NS, int R, bool OUTS>
 static void launch_scan(boa_ctx* x, const LayerW& w, float* ssm, int B, int Tc) {
     const int di = x->di;
-    const size_t lds = sizeof(float) * (size_t)Tc * (R + 2 * NS);
     const dim3 grid((di + 255) / 256, B);
     if (Tc == 1)
         hipLaunchKernelGGL((k_scan_step<NS, R, OUTS>), grid, dim3(256), 0, x->stream, x->xs, x->dbc, R + 2 * NS, x->xz,
                            (int64_t)2 * di, w.dt_w, w.dt_b, w.Aneg, w.D, ssm, di, x->ah, x->al);
     else
-        hipLaunchKernelGGL((k_scan<NS, R, OUTS>), grid, dim3(256), lds, x->stream, x->xs, x->dbc, R + 2 * NS, x->xz,
+        hipLaunchKernelGGL((k_scan<NS, R, OUTS>), grid, dim3(256), 0, x->stream, x->xs, x->dbc, R + 2 * NS, x->xz,
                            (int64_t)2 * di, w.dt_w, w.dt_b, w.Aneg, w.D, ssm, di, Tc, x->ah, x->al);
 }
 
