@@ -116,11 +116,11 @@ __device__ __forceinline__ void put_split(uint16_t* h, uint16_t* l, int idx, flo
 }
 
 // LayerNorm of rows RPW*wave .. RPW*wave + RPW-1 of src (fp32, stride LRES) into the split operand (stride LA).
+// wv, bv: this lane's 4 weights and biases, loaded by the caller ahead of the barrier before the LN phase, so
+// their L2 round trip (behind the pointer load from the layer table) overlaps the previous phase's tail.
 template <int RPW>
-__device__ __forceinline__ void ln_rows(const float* src, const float* __restrict__ w, const float* __restrict__ b,
-                                       uint16_t* sAh, uint16_t* sAl, int wave, int lane) {
-    const float4 wv = ldg_f4(G(w) + 4 * lane);
-    const float4 bv = ldg_f4(G(b) + 4 * lane);
+__device__ __forceinline__ void ln_rows(const float* src, float4 wv, float4 bv, uint16_t* sAh, uint16_t* sAl, int wave,
+                                       int lane) {
 #pragma unroll
     for (int q = 0; q < RPW; ++q) {
         const int r = RPW * wave + q;
@@ -214,6 +214,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
         }
         *reinterpret_cast<float4*>(sRes + r * LRES + c4) = v;
     }
+    float4 lnw = ldg_f4(G(a.layers[0].ln1_w) + 4 * lane), lnb = ldg_f4(G(a.layers[0].ln1_b) + 4 * lane);
     __syncthreads();
 
     const int s1 = p0m3 == 2 ? 0 : p0m3 + 1, s2 = p0m3 == 0 ? 2 : p0m3 - 1;
@@ -221,17 +222,20 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
     for (int l = 0; l < a.L; ++l) {
         const FusedLayer& w = a.layers[l];
         // ---- LN1 -> split operand
-        ln_rows<RPW>(sRes, w.ln1_w, w.ln1_b, sAh, sAl, wave, lane);
+        ln_rows<RPW>(sRes, lnw, lnb, sAh, sAl, wave, lane);
         __syncthreads();
         // ---- in_proj (+bias) -> xz fp32
 #pragma unroll 1
         for (int f0 = 0; f0 < 2 * FDI / 16; f0 += FPW_B * NWAVE) {
             floatx4 acc[FPW_B];
+            float bias_j[FPW_B];  // loaded ahead of the weight ring (in-order wait counter)
+#pragma unroll
+            for (int j = 0; j < FPW_B; ++j) bias_j[j] = G(w.in_b)[16 * frag_of<NWAVE>(f0, wave, j, 2 * FDI / 16, rot64) + n_of];
             mgemm<NT, NWAVE, FPW_B, FD, D_B>(sAh, sAl, LA, w.in_p, f0, 2 * FDI / 16, wave, lane, rot64, acc);
 #pragma unroll
             for (int j = 0; j < FPW_B; ++j) {
                 const int n = 16 * frag_of<NWAVE>(f0, wave, j, 2 * FDI / 16, rot64) + n_of;
-                const float bias = G(w.in_b)[n];
+                const float bias = bias_j[j];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) sX[(m_of + r) * LXZ + n] = epi_value<EPI_BIAS>(acc[j][r], bias);
             }
@@ -357,28 +361,36 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
         // ---- out_proj (+bias) -> mixer output fp32 (stride LRES, in the xz region)
         {
             floatx4 acc[FPW_S];
+            float bias_j[FPW_S];
+#pragma unroll
+            for (int j = 0; j < FPW_S; ++j) bias_j[j] = G(w.out_b)[16 * frag_of<NWAVE>(0, wave, j, FD / 16, rot16) + n_of];
             mgemm<NT, NWAVE, FPW_S, FDI, D_S>(sAh, sAl, LA, w.out_p, 0, FD / 16, wave, lane, rot16, acc);
 #pragma unroll
             for (int j = 0; j < FPW_S; ++j) {
                 const int n = 16 * frag_of<NWAVE>(0, wave, j, FD / 16, rot16) + n_of;
-                const float bias = G(w.out_b)[n];
+                const float bias = bias_j[j];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) sX[(m_of + r) * LRES + n] = epi_value<EPI_BIAS>(acc[j][r], bias);
             }
         }
+        lnw = ldg_f4(G(w.ln2_w) + 4 * lane);
+        lnb = ldg_f4(G(w.ln2_b) + 4 * lane);
         __syncthreads();
         // ---- LN2 -> split operand
-        ln_rows<RPW>(sX, w.ln2_w, w.ln2_b, sAh, sAl, wave, lane);
+        ln_rows<RPW>(sX, lnw, lnb, sAh, sAl, wave, lane);
         __syncthreads();
         // ---- FF1 (+bias, GELU) -> hidden split (xz region)
 #pragma unroll 1
         for (int f0 = 0; f0 < 4 * FD / 16; f0 += FPW_B * NWAVE) {
             floatx4 acc[FPW_B];
+            float bias_j[FPW_B];
+#pragma unroll
+            for (int j = 0; j < FPW_B; ++j) bias_j[j] = G(w.ff1_b)[16 * frag_of<NWAVE>(f0, wave, j, 4 * FD / 16, rot64) + n_of];
             mgemm<NT, NWAVE, FPW_B, FD, D_B>(sAh, sAl, LA, w.ff1_p, f0, 4 * FD / 16, wave, lane, rot64, acc);
 #pragma unroll
             for (int j = 0; j < FPW_B; ++j) {
                 const int n = 16 * frag_of<NWAVE>(f0, wave, j, 4 * FD / 16, rot64) + n_of;
-                const float bias = G(w.ff1_b)[n];
+                const float bias = bias_j[j];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) put_split(sHh, sHl, (m_of + r) * LH + n, epi_value<EPI_GELU>(acc[j][r], bias));
             }
@@ -387,17 +399,25 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
         // ---- FF2 (+bias) + block residual -> residual stream
         {
             floatx4 acc[FPW_S];
+            float bias_j[FPW_S];
+#pragma unroll
+            for (int j = 0; j < FPW_S; ++j) bias_j[j] = G(w.ff2_b)[16 * frag_of<NWAVE>(0, wave, j, FD / 16, rot16) + n_of];
             mgemm<NT, NWAVE, FPW_S, 4 * FD, D_S>(sHh, sHl, LH, w.ff2_p, 0, FD / 16, wave, lane, rot16, acc);
 #pragma unroll
             for (int j = 0; j < FPW_S; ++j) {
                 const int n = 16 * frag_of<NWAVE>(0, wave, j, FD / 16, rot16) + n_of;
-                const float bias = G(w.ff2_b)[n];
+                const float bias = bias_j[j];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int idx = (m_of + r) * LRES + n;
                     sRes[idx] = sRes[idx] + epi_value<EPI_RESID>(acc[j][r], bias);
                 }
             }
+        }
+        {
+            const FusedLayer& wn = a.layers[l + 1 < a.L ? l + 1 : l];  // the last layer reloads its own (unused)
+            lnw = ldg_f4(G(wn.ln1_w) + 4 * lane);
+            lnb = ldg_f4(G(wn.ln1_b) + 4 * lane);
         }
         __syncthreads();
     }
