@@ -8,12 +8,12 @@
 // gpu_rc_decode_fused_step_batch), done here without leaving the chip between layers.
 //
 // Design (gfx950): 512 threads (8 waves) own 16 lanes = the M of one v_mfma_f32_16x16x32_bf16 fragment.
-// Activations stay in LDS for the whole step (~116 KB: residual stream, split-bf16 GEMM operand, xz / FF
-// hidden, dt|B|C rows); GEMM weights stream from L2 in fragment-packed blocks (one coalesced 16-byte load
-// per lane per block); the only HBM traffic is the recurrent state (SSM state and the conv history ring)
-// and the step's inputs and outputs.  Lanes are independent, so a workgroup runs its steps without any
-// grid-wide synchronisation; workgroup classes start at fixed offsets (stagger_us) so that at any moment
-// some CUs are in their HBM-bound scan while others stream weights from L2.  GEMM phases: wave w computes output fragments w, w + 8, ...; each
+// Activations stay in LDS for the whole step (141 KB: residual stream, split-bf16 GEMM operand, xz / FF
+// hidden, x_proj partials and dt|B|C rows); GEMM weights stream from L2 in fragment-packed blocks (one
+// coalesced 16-byte load per lane per block); the only HBM traffic is the recurrent state (SSM state and the
+// conv history ring) and the step's inputs and outputs.  Lanes are independent, so a workgroup runs its
+// steps without any grid-wide synchronisation (workgroup classes can start at offsets, stagger_us, off by
+// default).  GEMM phases: wave w computes output fragments w, w + 8, ...; each
 // output accumulates 32-wide K steps in ascending order, lo*hi, hi*lo, hi*hi per step, exactly as the tiled
 // split-precision GEMM does, and every elementwise phase calls the same device function as the tiled
 // path (model_dev.h).  The logits of a lane are therefore bit-identical to those the compress path
