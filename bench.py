@@ -271,7 +271,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (chunks are independent and would "
-              "shard by range with one size exchange; see DESIGN.md)", file=sys.stderr)
+              "shard by contiguous chunk range with one exchange of payload sizes)", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np

@@ -48,7 +48,8 @@ def lib():
 
 
 def _cap(T: int) -> int:
-    # at most one word per symbol plus the finalize words (see DESIGN: pitch bound)
+    # word capacity of a stream of T symbols: at most one word per coded symbol plus the few finalize
+    # words; the device pitch uses the same T + 8 bound
     return int(T) + 8
 
 
