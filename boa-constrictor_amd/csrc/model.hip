@@ -234,12 +234,14 @@ __global__ void __launch_bounds__(256, 2) k_gemm(GemmArgs g) {
 template <int BM, int BN, int BK, int EPI, int NT, bool ASPLIT, bool OUTS>
 __global__ void __launch_bounds__(256, (BK > 32) ? 1 : 2) k_gemm_bf(GemmArgs g) {
     // LDS rows: BK = 32 tiles are unpadded (64 B per part-row) with the 16-byte chunk c of row r stored at
-    // chunk c ^ ((r >> 2) & 3), so a 16-lane group of stores (4 rows x 4 chunks) and of fragment reads (16 rows,
-    // one chunk) each touch every bank once; BK = 128 rows are padded by 8 (272 B, also conflict-free reads).
+    // chunk c ^ ((r >> 1) & 3).  A 16-byte fragment read is served 8 lanes (128 B) at a time: 8 rows of one
+    // chunk, which this puts in 8 different 16-byte bank groups (c ^ ((r >> 2) & 3) put row pairs together and
+    // measured bank conflicts on 92% of LDS cycles; this, none).  Stores (rows x 4 chunks) are a permutation
+    // within each row.  BK = 128 rows are padded by 8 (272 B).
     constexpr bool SWZ = (BK == 32);
     constexpr int LDK = SWZ ? BK : BK + 8;
     auto lds_off = [](int r, int k) {  // element (row r, column k) of an operand tile, k % 8 == 0 or a half chunk
-        if constexpr (SWZ) return r * 32 + ((((k >> 3) ^ (r >> 2)) & 3) << 3) + (k & 7);
+        if constexpr (SWZ) return r * 32 + ((((k >> 3) ^ (r >> 1)) & 3) << 3) + (k & 7);
         else return r * LDK + k;
     };
     constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 16, FN = WN / 16;
