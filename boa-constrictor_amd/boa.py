@@ -18,7 +18,6 @@ Only ``device="cuda"`` (the ROCm GPU under torch-ROCm) is supported; the referen
 from __future__ import annotations
 
 import hashlib
-import math
 import os
 import struct
 import zlib
@@ -62,6 +61,33 @@ def _streams_env() -> int:
         return 5000
 
 
+# BOA2 fixed header: magic, version, flags, uncompressed length, chunk length, chunk count, last chunk
+# length, fingerprint length (the fingerprint bytes follow).
+_HEADER = struct.Struct("<4sIIQIIIB")
+_CRC = struct.Struct("<I")
+
+
+def _uvarints(buf: bytes, lo: int, hi: int, count: int) -> np.ndarray:
+    """The first `count` LEB128 values of buf[lo:hi] as uint64, decoded without a per-value loop: a value ends
+    at each byte below 0x80; each byte contributes its low 7 bits shifted by 7 x (its index in the value)."""
+    if count == 0:
+        return np.zeros(0, dtype=np.uint64)
+    raw = np.frombuffer(buf, dtype=np.uint8, count=hi - lo, offset=lo)
+    ends = np.flatnonzero(raw < 0x80)
+    if ends.size < count:
+        raise ValueError("BOA2 payload out of range")
+    ends = ends[:count]
+    heads = np.empty(count, dtype=np.int64)
+    heads[0] = 0
+    heads[1:] = ends[:-1] + 1
+    used = raw[:ends[-1] + 1].astype(np.uint64)
+    rank = np.arange(used.size, dtype=np.int64) - np.repeat(heads, ends - heads + 1)
+    if int(rank.max()) > 9:
+        raise ValueError("BOA2 payload out of range")
+    parts = (used & np.uint64(0x7F)) << (np.uint64(7) * rank.astype(np.uint64))
+    return np.add.reduceat(parts, heads)
+
+
 class BoaFile:
     MAGIC = b"BOA2"
     IDX = b"IDX1"
@@ -83,61 +109,54 @@ class BoaFile:
 
     @staticmethod
     def _chunking(total_size: int, seq_size: int, chunks_count: int):
-        # boa.py:169-178
-        if seq_size and chunks_count:
-            chunk_len = int(seq_size); n_chunks = math.ceil(total_size / chunk_len)
-        elif seq_size:
-            chunk_len = int(seq_size); n_chunks = math.ceil(total_size / chunk_len)
+        """(chunk_len, n_chunks, last_chunk_len) for a file of total_size bytes (boa.py:169-178 semantics).
+
+        seq_size, when given, is the chunk length (it wins over chunks_count); otherwise the file is cut into
+        chunks_count pieces of ceil(total / chunks_count) bytes.  A count so large that the tail would hold
+        empty chunks yields fewer chunks: the reference's compress would pass empty chunks on to
+        compress_GPU's length assertion (boa.py:224-233, codec.py:25), its _split_to_chunks drops them
+        (boa.py:73-77), and so does this."""
+        if seq_size:
+            step = int(seq_size)
         elif chunks_count:
-            n_chunks = max(int(chunks_count), 1); chunk_len = math.ceil(total_size / n_chunks)
+            step = -(-int(total_size) // max(int(chunks_count), 1))
         else:
             raise ValueError("Provide either 'seq_size' or 'chunks_count'.")
-        # chunks_count larger than ceil(n / chunk_len) would leave empty trailing chunks, which the reference's
-        # compress passes on to compress_GPU's length assertion (boa.py:224-233, codec.py:25); they are dropped
-        # here instead, as _split_to_chunks does (boa.py:73-77)
-        n_chunks = min(n_chunks, math.ceil(total_size / chunk_len))
-        last = int(total_size - (n_chunks - 1) * chunk_len) if n_chunks > 1 else int(total_size)
-        return int(chunk_len), int(n_chunks), int(last)
+        count = max(-(-int(total_size) // step), 1)
+        return step, count, int(total_size) - (count - 1) * step
 
     def _read_file(self):
-        # boa.py:114-157
-        data = Path(self.filepath).read_bytes()
-        mm = memoryview(data)
-        p = 0
-        if bytes(mm[p:p + 4]) != self.MAGIC:
+        """Parses a BOA2 file into compressed_data / first_bytes / lengths / metadata (boa.py:114-157).
+
+        Layout: a fixed header `_HEADER` followed by fp_len fingerprint bytes, the payload, then the index
+        b"IDX1" | first_bytes[n] | n uvarint offset deltas | n uvarint stream lengths | u32 CRC32 of the
+        index.  The index is located with rfind(b"IDX1"), as the reference reader does (boa.py:130); the
+        uvarints are decoded in one vectorised pass; every stream must lie inside the payload and hold
+        whole u32 words."""
+        blob = Path(self.filepath).read_bytes()
+        if len(blob) < _HEADER.size or blob[:4] != self.MAGIC:
             raise ValueError("Bad file magic")
-        p += 4
-        version, = struct.unpack_from("<I", mm, p); p += 4
+        _magic, version, _flags, ulen, chunk_len, n, last_chunk_len, fp_len = _HEADER.unpack_from(blob, 0)
         if version != self.VERSION:
             raise ValueError(f"Unsupported version {version}")
-        _flags, = struct.unpack_from("<I", mm, p); p += 4
-        ulen, = struct.unpack_from("<Q", mm, p); p += 8
-        chunk_len, = struct.unpack_from("<I", mm, p); p += 4
-        n, = struct.unpack_from("<I", mm, p); p += 4
-        last_chunk_len, = struct.unpack_from("<I", mm, p); p += 4
-        hlen = mm[p]; p += 1
-        _fp = bytes(mm[p:p + hlen]); p += hlen
-
-        crc = struct.unpack_from("<I", mm, len(mm) - 4)[0]
-        idx_pos = data.rfind(self.IDX)
-        if idx_pos < 0:
+        body = _HEADER.size + fp_len
+        at = blob.rfind(self.IDX)
+        if at < 0:
             raise ValueError("Index not found")
-        if (zlib.crc32(data[idx_pos:len(data) - 4]) & 0xFFFFFFFF) != crc:
+        (crc,) = _CRC.unpack_from(blob, len(blob) - _CRC.size)
+        if zlib.crc32(blob[at:len(blob) - _CRC.size]) & 0xFFFFFFFF != crc:
             raise ValueError("Bad index CRC")
-        q = idx_pos + len(self.IDX)
-        first_bytes = list(mm[q:q + n]); q += n
-        offsets = [0] * n; pos = q; prev = 0
-        for i in range(n):
-            d, pos = uvarint_decode(mm, pos); prev += d; offsets[i] = prev
-        comp_lens = [0] * n
-        for i in range(n):
-            L, pos = uvarint_decode(mm, pos); comp_lens[i] = L
-        payload = mm[p:idx_pos]
-        for i in range(n):  # boa.cpp:240 bounds check (the Python reader slices silently)
-            if offsets[i] + comp_lens[i] > len(payload) or comp_lens[i] % 4:
-                raise ValueError("BOA2 payload out of range")
-        self.compressed_data = [bytes(payload[offsets[i]:offsets[i] + comp_lens[i]]) for i in range(n)]
-        self.first_bytes = first_bytes
+        fb_at = at + len(self.IDX)
+        first = list(blob[fb_at:fb_at + n])
+        fields = _uvarints(blob, fb_at + n, len(blob) - _CRC.size, 2 * n)
+        starts = np.cumsum(fields[:n])
+        sizes = fields[n:]
+        room = at - body
+        if n and (int((starts + sizes).max()) > room or bool((sizes & 3).any())):
+            raise ValueError("BOA2 payload out of range")  # boa.cpp:240's check; the Python reader has none
+        view = memoryview(blob)[body:at]
+        self.compressed_data = [bytes(view[s:s + z]) for s, z in zip(starts.tolist(), sizes.tolist())]
+        self.first_bytes = first
         self.lengths = [int(chunk_len)] * (n - 1) + [int(last_chunk_len)] if n else []
         self.metadata = {
             "chunk_len": int(chunk_len),

@@ -115,3 +115,37 @@ def test_cpu_device_refused():
         return
     with pytest.raises(RuntimeError):
         boa.BOA("cpu", "/tmp/x.boa", object())
+
+
+def test_vectorised_uvarints_match_scalar_decoder():
+    import boa
+
+    rng = np.random.default_rng(5)
+    vals = [0, 1, 127, 128, 16383, 16384, 2**32 - 1, 2**32, 2**56 + 3] + [
+        int(v) for v in rng.integers(0, 2**40, 500)]
+    buf = b"junk" + b"".join(boa.uvarint_encode(v) for v in vals) + b"tail"
+    got = boa._uvarints(buf, 4, len(buf) - 4, len(vals))
+    assert [int(v) for v in got] == vals
+    pos, ref = 4, []
+    for _ in vals:
+        v, pos = boa.uvarint_decode(buf, pos)
+        ref.append(v)
+    assert ref == vals
+    with pytest.raises(ValueError, match="out of range"):
+        boa._uvarints(buf, 4, 8, len(vals))  # index truncated
+
+
+def test_reader_many_streams_property(tmp_path):
+    import boa
+
+    rng = np.random.default_rng(9)
+    streams = [rng.integers(0, 2**32, int(k), dtype=np.uint64).astype("<u4").tobytes()
+               for k in rng.integers(0, 300, 257)]
+    first = [int(v) for v in rng.integers(0, 256, len(streams))]
+    p = tmp_path / "m.boa"
+    _write_boa2(p, streams, first, 5000, 17, 5000 * 256 + 17)
+    f = boa.BoaFile(str(p), object())
+    f._read_file()
+    assert f.compressed_data == streams
+    assert f.first_bytes == first
+    assert f.lengths == [5000] * 256 + [17]
