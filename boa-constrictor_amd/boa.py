@@ -7,10 +7,11 @@ Reference: boa.py:7-311.  Same BOA2 container, byte for byte:
     payload (every chunk's u32 little-endian words, back to back) |
     b"IDX1" | first_bytes[n] | n x uvarint(offset delta) | n x uvarint(stream bytes) | u32 CRC32(IDX1..)
 
-Chunking: chunk_len = ceil(n / chunks_count), or seq_size; chunks are processed in waves of
-BOA_GPU_STREAMS (default 5000) lanes.  The payload of a wave comes back from the GPU already compacted
-(one device-to-host copy), and is written in one piece.  As in the reference, the reader finds the index
-with rfind(b"IDX1") (boa.py:130).
+Chunking: chunk_len = ceil(n / chunks_count), or seq_size.  Chunks are processed in waves of
+BOA_GPU_STREAMS lanes if that is set (as in the reference), otherwise of as many lanes as free device
+memory holds.  The payload of a wave comes back from the GPU already compacted (one device-to-host copy),
+and is written in one piece.  As in the reference, the reader finds the index with rfind(b"IDX1")
+(boa.py:130).
 
 Only ``device="cuda"`` (the ROCm GPU under torch-ROCm) is supported; the reference's CPU branch
 (mambapy + constriction) is not part of this build and raises.
@@ -54,11 +55,19 @@ def uvarint_decode(buf, pos: int):
         s += 7
 
 
-def _streams_env() -> int:
-    try:
-        return int(os.getenv("BOA_GPU_STREAMS", "5000"))
-    except Exception:
-        return 5000
+def _wave_lanes(model, n_chunks: int, chunk_len: int) -> int:
+    """Chunks per GPU wave.  BOA_GPU_STREAMS, when set, fixes it as in the reference (boa.py:207-210; an
+    unparsable value means 5000); otherwise it is sized from free device memory (the model's
+    plan_wave_lanes, after boa.cpp:103-150).  Always within [1, n_chunks]."""
+    env = os.getenv("BOA_GPU_STREAMS")
+    if env is not None:
+        try:
+            lanes = int(env)
+        except ValueError:
+            lanes = 5000
+    else:
+        lanes = model.plan_wave_lanes(n_chunks, chunk_len)
+    return max(1, min(int(lanes), int(n_chunks)))
 
 
 # BOA2 fixed header: magic, version, flags, uncompressed length, chunk length, chunk count, last chunk
@@ -182,7 +191,7 @@ class BoaFile:
         }
         fp = self._model_fingerprint()
         mm = np.memmap(p, dtype=np.uint8, mode="r")
-        streams = max(1, min(_streams_env(), n_chunks))
+        streams = _wave_lanes(self.model, n_chunks, chunk_len)
         if progress:
             print(f"[compress] gpu_streams={streams} (chunk_len={chunk_len})")
         lengths, first_bytes = [], []
@@ -232,7 +241,7 @@ class BoaFile:
         if progress:
             print(f"Total compressed size from disk: {sum(len(c) for c in self.compressed_data)} bytes")
         n = len(self.compressed_data)
-        streams = max(1, min(_streams_env(), max(n, 1)))
+        streams = _wave_lanes(self.model, max(n, 1), max(self.lengths, default=1))
         parts = []
         with torch.inference_mode():
             for b0 in range(0, n, streams):

@@ -74,6 +74,7 @@ SIGNATURES = [
     ("boa_ctx_create", ctypes.c_int, [ctypes.POINTER(ModelCfg), _P, _I64, ctypes.c_int, _I32, _I32, _P, ctypes.POINTER(_P)]),
     ("boa_ctx_destroy", ctypes.c_int, [_P]),
     ("boa_ctx_device_bytes", _I64, [_P]),
+    ("boa_ctx_plan_bytes", ctypes.c_int, [ctypes.POINTER(ModelCfg), ctypes.c_int, _I32, _I32, ctypes.POINTER(_I64)]),
     ("boa_state_reset", ctypes.c_int, [_P, _I32]),
     ("boa_model_step", ctypes.c_int, [_P, _P, _I32, _P]),
     ("boa_model_forward", ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P]),

@@ -1486,6 +1486,48 @@ extern "C" int64_t boa_weights_nbytes(const boa_model_cfg* cfg) {
 
 extern "C" int64_t boa_ctx_device_bytes(const boa_ctx* ctx) { return ctx ? ctx->device_bytes : 0; }
 
+// Whether a context of this shape and precision decodes through k_fused_step (BOA_FUSED_STEP=0 turns it off).
+static bool want_fused(const boa_model_cfg& c, int R, int precision) {
+    const char* fenv = getenv("BOA_FUSED_STEP");
+    return precision != BOA_PREC_F32 && fused_step_supported(c.d_model, c.d_state, R, c.d_conv, c.vocab) &&
+           !(fenv && fenv[0] == '0');
+}
+
+// Device bytes boa_ctx_create allocates for this shape: the same list of buffers, in the same order, each
+// rounded as dmalloc rounds it.  boa_ctx_create checks its own total against this after allocating.
+static int64_t ctx_plan_bytes(const boa_model_cfg& c, int R, int precision, int64_t max_lanes, int64_t tile_len) {
+    const int64_t d = c.d_model, di = (int64_t)c.expand * c.d_model, NS = c.d_state, V = c.vocab, L = c.n_layers;
+    const int64_t rows = max_lanes * tile_len;
+    auto f4 = [](int64_t n) { return 4 * std::max<int64_t>(n, 1); };
+    int64_t b = f4(weights_floats(c, R)) + f4(L * di * NS) + f4(L * max_lanes * 3 * di) + f4(L * max_lanes * di * NS) +
+                f4(rows * d) + f4(rows * std::max(2 * di, 4 * d)) + f4(rows * di) + f4(rows * (R + 2 * NS)) +
+                f4(rows * d) + f4(rows * V) + 8 * std::max<int64_t>(rows, 1);
+    if (precision != BOA_PREC_F32) b += 2 * 2 * std::max<int64_t>(rows * std::max(d, di), 1);
+    b += f4(max_lanes) + (int64_t)sizeof(EncState) * max_lanes + (int64_t)sizeof(DecState) * max_lanes + 4;
+    if (precision != BOA_PREC_F32) {
+        int64_t mats = L * (2 * di * d + (R + 2 * NS) * di + d * di + 4 * d * d + 4 * d * d) + d * d + V * d;
+        b += 2 * std::max<int64_t>(2 * mats, 1);
+        if (want_fused(c, R, precision)) {
+            b += 2 * std::max<int64_t>((precision == BOA_PREC_BF16X3 ? 2 : 1) * mats, 1);
+            b += (int64_t)sizeof(FusedLayer) * L;
+        }
+    }
+    return b;
+}
+
+extern "C" int boa_ctx_plan_bytes(const boa_model_cfg* cfg, int precision, int32_t max_lanes, int32_t tile_len,
+                                  int64_t* out_bytes) {
+    boa_model_cfg c;
+    int R;
+    if (!out_bytes) return boa_fail(BOA_ERR_ARG, "boa_ctx_plan_bytes: null output");
+    int rc = resolve_cfg(cfg, c, R);
+    if (rc != BOA_OK) return rc;
+    if (max_lanes < 1 || tile_len < 1 || tile_len > 256)
+        return boa_fail(BOA_ERR_ARG, "need max_lanes >= 1 and 1 <= tile_len <= 256 (got %d, %d)", max_lanes, tile_len);
+    *out_bytes = ctx_plan_bytes(c, R, precision, max_lanes, tile_len);
+    return BOA_OK;
+}
+
 extern "C" int boa_ctx_destroy(boa_ctx* ctx) {
     if (!ctx) return BOA_OK;
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
@@ -1663,8 +1705,7 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
             m->l = (x->prec == BOA_PREC_BF16X3) ? x->wsplit + so + m->n : nullptr;
             so += 2 * m->n;
         }
-        const char* fenv = getenv("BOA_FUSED_STEP");
-        x->fused = fused_step_supported(d, NS, R, x->DC, V) && !(fenv && fenv[0] == '0');
+        x->fused = want_fused(c, R, x->prec);
         if (const char* v = getenv("BOA_FUSED_STEPS_PER_LAUNCH")) x->fused_steps = std::max(1, atoi(v));
         if (const char* v = getenv("BOA_FUSED_STAGGER_US")) x->stagger_us = std::max(0, atoi(v));
         if (const char* v = getenv("BOA_FUSED_STAGGER_CLASSES")) x->stagger_classes = std::min(8, std::max(1, atoi(v)));
@@ -1712,6 +1753,11 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
     if (e != hipSuccess) {
         boa_ctx_destroy(x);
         return boa_fail_hip(e, "boa_ctx_create upload", __FILE__, __LINE__);
+    }
+    if (x->device_bytes != ctx_plan_bytes(c, R, precision, max_lanes, tile_len)) {
+        const long long got = (long long)x->device_bytes, plan = (long long)ctx_plan_bytes(c, R, precision, max_lanes, tile_len);
+        boa_ctx_destroy(x);
+        return boa_fail(BOA_ERR_STATE, "internal: context holds %lld bytes, plan says %lld", got, plan);
     }
     *out = x;
     return BOA_OK;

@@ -1,6 +1,6 @@
 // Range-coder kernels of libboa_hip.so: the coder on precomputed tables (range coder alone), the per-step
-// batch coder with the reference's Q2 quantiser (drop-in for gpu.queue.RangeCoderBatch), bitstream
-// compaction, and the fused quantiser's table export used by the parity tests.
+// batch coder with the reference's Q2 quantiser (drop-in for gpu.queue.RangeCoderBatch; its word export
+// goes through boa_compact, compact.hip), and the fused quantiser's table export used by the parity tests.
 //
 // One chunk lane per stream throughout.  Wave-parallel work (table search, Q2 prefix sums, quantiser
 // scans) is done by one 64-wide wavefront per lane; the coder state itself is uniform across the wave.
@@ -263,42 +263,6 @@ __global__ void __launch_bounds__(64) k_rcb_decode_step(const float* __restrict_
 // ================================================================================================
 // Compaction: exclusive scan of stream sizes (one workgroup) + gather into a contiguous payload.
 
-__global__ void __launch_bounds__(1024) k_scan_sizes(const int32_t* __restrict__ nwords, int n,
-                                                    int64_t* __restrict__ off, int64_t* __restrict__ total) {
-    __shared__ int64_t part[1024];
-    const int tid = threadIdx.x;
-    const int per = (n + 1023) / 1024;
-    const int lo = tid * per;
-    const int hi = min(n, lo + per);
-    int64_t s = 0;
-    for (int i = lo; i < hi; ++i) s += (int64_t)max(nwords[i], 0);
-    part[tid] = s;
-    __syncthreads();
-    for (int o = 1; o < 1024; o <<= 1) {  // Hillis-Steele inclusive scan over the 1024 partials
-        const int64_t v = (tid >= o) ? part[tid - o] : 0;
-        __syncthreads();
-        part[tid] += v;
-        __syncthreads();
-    }
-    int64_t run = part[tid] - s;
-    for (int i = lo; i < hi; ++i) {
-        off[i] = run;
-        run += (int64_t)max(nwords[i], 0);
-    }
-    if (tid == 1023) *total = part[1023];
-}
-
-__global__ void __launch_bounds__(256) k_gather_words(const uint32_t* __restrict__ words, int64_t pitch,
-                                                     const int32_t* __restrict__ nwords,
-                                                     const int64_t* __restrict__ off,
-                                                     uint32_t* __restrict__ payload) {
-    const int b = blockIdx.x;
-    const int32_t nw = max(nwords[b], 0);
-    const uint32_t* src = words + (int64_t)b * pitch;
-    uint32_t* dst = payload + off[b];
-    for (int i = threadIdx.x; i < nw; i += blockDim.x) dst[i] = src[i];
-}
-
 // Fused-quantiser tables for parity tests: one wavefront per row.
 __global__ void __launch_bounds__(256) k_xq_cdf(const float* __restrict__ logits, int64_t rows, int V, int P,
                                                uint32_t* __restrict__ cdf) {
@@ -411,36 +375,6 @@ extern "C" int boa_xq_cdf(const float* d_logits, int64_t rows, int32_t vocab, in
     hipLaunchKernelGGL(k_xq_cdf, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), d_logits, rows, vocab,
                        precision, d_cdf);
     BOA_HIP_TRY(hipGetLastError());
-    return BOA_OK;
-}
-
-extern "C" int boa_compact(const uint32_t* d_words, int64_t pitch_words, const int32_t* d_nwords, int32_t lanes,
-                           int64_t* d_word_off, uint32_t* d_payload, int64_t payload_cap, int64_t* h_total_words,
-                           void* stream) {
-    if (!d_words || !d_nwords || !d_word_off || lanes < 0 || !h_total_words)
-        return boa_fail(BOA_ERR_ARG, "boa_compact: bad arguments");
-    *h_total_words = 0;
-    if (lanes == 0) return BOA_OK;
-    hipStream_t s = as_stream(stream);
-    int64_t* d_total = nullptr;
-    BOA_HIP_TRY(hipMalloc((void**)&d_total, sizeof(int64_t)));
-    hipLaunchKernelGGL(k_scan_sizes, dim3(1), dim3(1024), 0, s, d_nwords, lanes, d_word_off, d_total);
-    hipError_t e = hipGetLastError();
-    int64_t total = 0;
-    if (e == hipSuccess) e = hipMemcpyAsync(&total, d_total, sizeof(int64_t), hipMemcpyDeviceToHost, s);
-    if (e == hipSuccess) e = hipStreamSynchronize(s);
-    (void)hipFree(d_total);
-    if (e != hipSuccess) return boa_fail_hip(e, "boa_compact scan", __FILE__, __LINE__);
-    *h_total_words = total;
-    if (total > payload_cap) return boa_fail(BOA_ERR_OVERFLOW, "boa_compact: payload needs %lld words, capacity %lld",
-                                             (long long)total, (long long)payload_cap);
-    if (total > 0) {
-        if (!d_payload) return boa_fail(BOA_ERR_ARG, "boa_compact: null payload");
-        hipLaunchKernelGGL(k_gather_words, dim3(lanes), dim3(256), 0, s, d_words, pitch_words, d_nwords, d_word_off,
-                           d_payload);
-        BOA_HIP_TRY(hipGetLastError());
-    }
-    BOA_HIP_TRY(hipStreamSynchronize(s));
     return BOA_OK;
 }
 

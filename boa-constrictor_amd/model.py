@@ -160,7 +160,9 @@ class BoaBytePredictor(nn.Module):
     def engine(self, max_lanes: int, tile_len: int = DEFAULT_TILE_LEN) -> _Engine:
         """Cached context with capacity for max_lanes x tile_len rows (rebuilt when weights change)."""
         self._require_gpu()
-        key = (self._weights_key(), self.precision)
+        # the context runs on the stream that is current when it is created; a caller on another stream gets
+        # its own context, so its input copies and the kernels stay ordered on one stream
+        key = (self._weights_key(), self.precision, int(torch.cuda.current_stream().cuda_stream))
         e = self._engines.get("codec")
         if e is not None and e[0] == key and e[1].max_lanes >= max_lanes and e[1].tile_len >= tile_len:
             return e[1]
@@ -171,6 +173,39 @@ class BoaBytePredictor(nn.Module):
 
     def release_engines(self):
         self._engines.clear()
+
+    def plan_wave_lanes(self, n_chunks: int, chunk_len: int, cap: int = 65536) -> int:
+        """Chunks per wave sized from free device memory, as auto_size_params does (boa.cpp:103-150): the
+        most lanes (at most n_chunks and cap) whose context (boa_ctx_plan_bytes, exact) plus the wave's own
+        buffers (input bytes, pitched words, payload, output bytes: 9 B per position and lane) fit in 90% of
+        the memory that is free, counting this model's cached context and torch's cached blocks as free."""
+        self._require_gpu()
+        lib = _nat.lib()
+        cfg = self.cfg
+        c = _nat.ModelCfg(cfg.d_model, cfg.n_layers, cfg.vocab, cfg.d_state, cfg.d_conv, cfg.expand, 0)
+        prec = PRECISIONS[self.precision]
+        tile = int(min(DEFAULT_TILE_LEN, max(chunk_len - 1, 1)))
+        free, _total = torch.cuda.mem_get_info()
+        e = self._engines.get("codec")
+        free += (e[1].device_bytes if e is not None else 0)
+        free += torch.cuda.memory_reserved() - torch.cuda.memory_allocated()
+        budget = 0.9 * free
+
+        def need(lanes: int) -> float:
+            b = ctypes.c_int64(0)
+            _nat.check(lib.boa_ctx_plan_bytes(ctypes.byref(c), prec, lanes, tile, ctypes.byref(b)))
+            return float(b.value) + lanes * (9.0 * chunk_len + 80.0)
+
+        lo, hi = 1, max(1, min(int(n_chunks), int(cap)))
+        if need(hi) <= budget:
+            return hi
+        while lo < hi:  # largest lanes with need(lanes) <= budget (at least 1)
+            mid = (lo + hi + 1) // 2
+            if need(mid) <= budget:
+                lo = mid
+            else:
+                hi = mid - 1
+        return lo
 
     # ---- reference API ----------------------------------------------------------------------------
     @torch.inference_mode()

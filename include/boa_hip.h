@@ -74,6 +74,12 @@ int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights_f32, int64_t 
 int boa_ctx_destroy(boa_ctx* ctx);
 /* Bytes of device memory the context holds. */
 int64_t boa_ctx_device_bytes(const boa_ctx* ctx);
+/* Bytes of device memory boa_ctx_create would allocate for this shape (exact: creation checks its total
+ * against it).  For sizing waves of chunks from free device memory.  Replaces
+ * BoaPredictorGPU::estimate_memory_static (boa_gpu.hpp:625-662) as used by auto_size_params
+ * (boa.cpp:103-150).                                                                                  */
+int boa_ctx_plan_bytes(const boa_model_cfg* cfg, int precision, int32_t max_lanes, int32_t tile_len,
+                       int64_t* out_bytes);
 
 /* Zeroes the conv and SSM state of lanes [0, lanes) (MambaBlockGPU::reset_cache, boa_gpu.hpp:220-223;
  * model.py:68-73 zero initial cache).                                                                  */

@@ -162,11 +162,12 @@ def test_range_coder_batch_errors(gpu):
         b.load_compressed_list([np.zeros(5, np.uint32)] * N)
 
 
-def test_compaction(gpu):
+@pytest.mark.parametrize("lanes,pitch", [(1, 8), (1024, 16), (1025, 16), (3000, 64), (70000, 4)])
+def test_compaction(gpu, lanes, pitch):
+    """Multi-workgroup scan (1024 lanes per workgroup) + gather vs numpy, at one and several workgroups."""
     from boa_amd import _native as N
 
     rng = np.random.default_rng(9)
-    lanes, pitch = 3000, 64
     nw = rng.integers(0, pitch + 1, lanes).astype(np.int32)
     words = rng.integers(0, 1 << 31, (lanes, pitch)).astype(np.int32)
     d_words, d_nw = _dev(words), _dev(nw)
