@@ -140,8 +140,9 @@ int boa_xq_cdf(const float* d_logits, int64_t rows, int32_t vocab, int32_t preci
 
 /* Bitstream compaction: exclusive prefix sum of d_nwords into d_word_off (int64 [lanes]) and a gather of
  * each lane's words from the pitched buffer into the contiguous d_payload (capacity payload_cap words).
- * *h_total_words receives the total; this call synchronizes the stream.  Replaces the per-lane D2H copy
- * of the full pitch (gpu_range_coder.py:278-292; boa.cpp:388-395).                                     */
+ * *h_total_words receives the total; this call synchronizes the stream.  The scan's partial sums live in a
+ * buffer the library allocates on the first call per device and stream (and enlarges for a larger wave).
+ * Replaces the per-lane D2H copy of the full pitch (gpu_range_coder.py:278-292; boa.cpp:388-395).      */
 int boa_compact(const uint32_t* d_words, int64_t pitch_words, const int32_t* d_nwords, int32_t lanes,
                 int64_t* d_word_off, uint32_t* d_payload, int64_t payload_cap, int64_t* h_total_words,
                 void* stream);
