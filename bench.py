@@ -8,10 +8,21 @@ Workload (BASELINE.json configs[2] + configs[3]): d_model 256 x 8 Mamba layers, 
 compaction) and decompress it again (strictly sequential, one model step per byte), inputs resident in HBM.
 value = input bytes / (compress time + decompress time), in MB/s (10^6 bytes/s).
 
+GEMM arithmetic is the build's default "bf16x3" mode: fp32 values, each GEMM product formed from two-part
+bfloat16 splits of both operands (three bf16 MFMA products, fp32 accumulation, ~16 significant bits per
+operand); everything else (LayerNorm, conv, scan, activations, quantiser) is fp32/integer.  The line's
+"dtype" says so.
+
 Also reported: compress and decompress rates separately, the roofline of the dominant kernel from live HIP
 event timing (boa_profile) inside the timed region, and a CPU baseline: this repo's restatement of the
 reference CPU path (codec.compress_CPU / decompress_CPU: per-step torch-CPU model + per-lane range coding in
-a thread pool) timed on a bounded sample of configs[0] on this host.
+a thread pool) timed on a bounded sample of configs[0] on this host.  After the timed steps, untimed by the
+headline, three bounded extra measurements go into the same JSON line (--no-extras skips them):
+  f32_*      the same model and data in "f32" mode (plain fp32 MFMA, the reference's precision) on a stated
+             sub-size of the workload;
+  coder      configs[1], the range coder alone: 16384 streams x 4096 symbols, P = 16;
+  config4    configs[4]'s model (d512 x 16 layers, bf16 weights, seed 1) on its 16384 chunks of mixed
+             int16/float32 records, each chunk cut to a stated length (steady-state rates).
 """
 from __future__ import annotations
 
@@ -105,11 +116,11 @@ def markov_bytes(n: int, seed: int = 0, alpha: float = 0.1):
 CODER_METRIC = "range coder alone: symbols/s encode + decode, 16384 streams x 4096 symbols, P=16, 1 GPU"
 
 
-def coder_bench(args):
+def coder_bench(args, steps: int, warmup: int, cpu_streams: int) -> dict:
     """per-step 256-symbol tables from N(0, 3^2) logits quantised to total 2^16 (min freq 1),
-    symbols drawn from them, 16384 streams x 4096 symbols, generated on the device (not timed); then one
-    timed encode and one timed decode over tables resident in HBM.  Byte-exact decode is checked on the
-    device; the CPU leg runs this repo's C coder on a sample of streams and must produce the same words."""
+    symbols drawn from them, 16384 streams x 4096 symbols, generated on the device (not timed); then timed
+    encodes and decodes over tables resident in HBM.  Byte-exact decode is checked on the device; the CPU
+    leg runs this repo's C coder on the first cpu_streams streams and must produce the same words."""
     import numpy as np
     import torch
 
@@ -134,11 +145,11 @@ def coder_bench(args):
         N.check(lib.rc_decode_tables(P, 2, N.ptr(d_cdf), K, N.ptr(d_words), pitch, N.ptr(d_n), S, T, N.ptr(d_out),
                                      N.stream_ptr()))
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         enc()
         dec()
     te, td = [], []
-    for _ in range(args.steps):
+    for _ in range(steps):
         e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
         torch.cuda.synchronize()
         e0.record()
@@ -163,7 +174,7 @@ def coder_bench(args):
     if not args.no_cpu:
         from oracle import ora
 
-        ns = args.coder_cpu_streams
+        ns = cpu_streams
         tab = d_cdf[:ns].cpu().numpy().view(np.uint16).astype(np.uint32)
         full = np.concatenate([tab, np.full((ns, T, 1), 1 << P, np.uint32)], axis=-1)
         syms = d_syms[:ns].cpu().numpy().astype(np.int32)
@@ -186,8 +197,8 @@ def coder_bench(args):
         "value": nsym / (t_e + t_d),
         "unit": "symbols/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": (t_e + t_d) * 1e3,
         "higher_is_better": True,
         "scaling": "weak",
@@ -203,7 +214,7 @@ def coder_bench(args):
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
-    print(json.dumps(res))
+    return res
 
 
 def cpu_baseline(steps: int):
@@ -251,6 +262,148 @@ def cpu_baseline(steps: int):
     }
 
 
+def lanes_equal(out, X, lens_h) -> bool:
+    """Byte-exact round trip, lane by lane up to each lane's length (bytes past a lane's end are not
+    written by the decoder and are not compared)."""
+    import torch
+
+    T = out.shape[1]
+    L = torch.tensor(lens_h, dtype=torch.int64, device=out.device)
+    mask = torch.arange(T, device=out.device)[None, :] < L[:, None]
+    return bool(torch.equal(out[mask], X[:, :T][mask]))
+
+
+def model_macs_per_token(d: int, L: int, V: int = 256, ns: int = 16) -> int:
+    """GEMM multiply-adds per input byte: per layer in_proj, x_proj, dt_proj, out_proj, FF1, FF2; plus the
+    two head layers."""
+    di, r = 2 * d, -(-d // 16)
+    per_layer = 2 * di * d + (r + 2 * ns) * di + r * di + d * di + 2 * 4 * d * d
+    return L * per_layer + d * d + V * d
+
+
+def decode_state_bytes(d: int, L: int, ns: int = 16) -> int:
+    """Recurrent-state HBM bytes per decoded byte and lane: SSM state read + write and conv history (3 reads,
+    1 write) of every layer."""
+    di = 2 * d
+    return L * (2 * di * ns * 4 + 4 * di * 4)
+
+
+def codec_pass(lib, eng, X, lens, lens_h, chunk: int, reps: int, warm: int):
+    """Untimed warm-ups, then `reps` timed compress (+ compaction) and decompress passes of X [B, chunk] on
+    the context `eng`.  Returns mean compress and decompress seconds, compressed bytes, round-trip status."""
+    import numpy as np
+    import torch
+
+    from boa_amd import _native as N
+
+    B = X.shape[0]
+    pitch = chunk + 8
+    words = torch.empty((B, pitch), dtype=torch.int32, device="cuda")
+    nw = torch.empty(B, dtype=torch.int32, device="cuda")
+    offs = torch.empty(B, dtype=torch.int64, device="cuda")
+    payload = torch.empty(B * pitch, dtype=torch.int32, device="cuda")
+    out = torch.empty((B, chunk), dtype=torch.uint8, device="cuda")
+    first = X[:, 0].contiguous()
+    stream = N.stream_ptr()
+    tcs, tds = [], []
+    for i in range(warm + reps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        N.check(lib.boa_compress(eng.h, N.ptr(X), X.stride(0), N.ptr(lens), B, chunk, N.ptr(words), pitch,
+                                 N.ptr(nw)))
+        total = ctypes.c_int64(0)
+        N.check(lib.boa_compact(N.ptr(words), pitch, N.ptr(nw), B, N.ptr(offs), N.ptr(payload), payload.numel(),
+                                ctypes.byref(total), stream))
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        N.check(lib.boa_decompress(eng.h, N.ptr(payload), N.ptr(offs), N.ptr(nw), N.ptr(first), N.ptr(lens), B,
+                                   chunk, N.ptr(out), out.stride(0)))
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        if i >= warm:
+            tcs.append(t1 - t0)
+            tds.append(t2 - t1)
+    return float(np.mean(tcs)), float(np.mean(tds)), 4 * int(nw.sum().item()), lanes_equal(out, X, lens_h)
+
+
+def f32_extra(lib, X, lens_h, sub_len: int) -> dict:
+    """The headline's model and data in "f32" mode (fp32 MFMA GEMMs, the reference's arithmetic) on the
+    first sub_len bytes of every chunk."""
+    import torch
+
+    from boa_amd import weights as W
+    import model as M
+
+    B = X.shape[0]
+    Xs = X[:, :sub_len].contiguous()
+    ls = [min(sub_len, v) for v in lens_h]
+    lens = torch.tensor(ls, dtype=torch.int32, device="cuda")
+    cfg = W.Cfg()
+    eng = M._Engine(W.seeded_blob(cfg, 0), cfg, B, 64, precision="f32")
+    tc, td, cb, ok = codec_pass(lib, eng, Xs, lens, ls, sub_len, reps=1, warm=1)
+    nb = sum(ls)
+    del eng
+    return {"f32_compress_MBps": nb / tc / 1e6, "f32_decompress_MBps": nb / td / 1e6, "f32_round_trip_ok": ok,
+            "f32_compressed_bytes": cb, "f32_decompress_step_ms": td / (sub_len - 1) * 1e3,
+            "f32_sample": f"{B} chunks x first {sub_len} B of each (same data and model), GEMMs in fp32 MFMA, "
+                          "one warm-up and one timed pass"}
+
+
+def config4_data(n_chunks: int, chunk: int, take: int, seed: int = 1):
+    """configs[4] input: int16 N(0, 300^2) clipped to +-32767 and float32 log-normal(1, 1.5) records
+    interleaved 1:1 (6-byte pairs), n_chunks x chunk bytes in all; returns the first `take` bytes of every
+    chunk as an [n_chunks, take] uint8 array."""
+    import numpy as np
+
+    nbytes = n_chunks * chunk
+    n = -(-nbytes // 6)
+    rng = np.random.default_rng(seed)
+    rec = np.empty(n, dtype=[("i", "<i2"), ("f", "<f4")])
+    rec["i"] = np.clip(rng.normal(0.0, 300.0, n), -32767, 32767).astype(np.int16)
+    rec["f"] = rng.lognormal(1.0, 1.5, n).astype(np.float32)
+    flat = rec.view(np.uint8)[:nbytes].reshape(n_chunks, chunk)
+    return np.ascontiguousarray(flat[:, :take])
+
+
+def config4_extra(lib, lanes: int, take: int) -> dict:
+    """d512 x 16 layers, bf16 weights (fp32 state, fp32 quantiser path), seed 1, `lanes` chunks
+    of the 256 MiB mixed-record payload (chunks_count = lanes), each cut to its first `take` bytes; one
+    warm-up and one timed compress + decompress.  Rooflines: compress against the dense bf16 MFMA peak with
+    the model's multiply-adds (the bf16w mode issues two bf16 products per multiply-add: activation hi and
+    lo parts), decompress against HBM with the recurrent state plus the bf16 weights once per step."""
+    import torch
+
+    from boa_amd import weights as W
+    import model as M
+
+    cfg = W.Cfg(d_model=512, n_layers=16)
+    chunk = (256 << 20) // lanes
+    data = config4_data(lanes, chunk, take)
+    X = torch.from_numpy(data).cuda()
+    ls = [take] * lanes
+    lens = torch.tensor(ls, dtype=torch.int32, device="cuda")
+    eng = M._Engine(W.seeded_blob(cfg, 1), cfg, lanes, 64, precision="bf16w")
+    tc, td, cb, ok = codec_pass(lib, eng, X, lens, ls, take, reps=1, warm=1)
+    del eng
+    nb = lanes * take
+    macs = model_macs_per_token(512, 16)
+    flops = 2.0 * macs * lanes * (take - 1)
+    step_s = td / (take - 1)
+    step_bytes = lanes * decode_state_bytes(512, 16) + 2.0 * macs
+    return {
+        "workload": (f"configs[4]: d512x16L bf16 weights seed 1, {lanes} chunks of the 256 MiB int16/float32 "
+                     f"record payload, first {take} B of each chunk; one warm-up and one timed pass"),
+        "compress_MBps": nb / tc / 1e6, "decompress_MBps": nb / td / 1e6, "decompress_step_ms": step_s * 1e3,
+        "compressed_bytes": cb, "round_trip_ok": ok,
+        "roofline_compress": {"bound": "mfma", "achieved": flops / tc / 1e12, "peak": PEAK_BF16_MFMA_TFLOPS,
+                              "unit": "TFLOP/s", "frac": flops / tc / 1e12 / PEAK_BF16_MFMA_TFLOPS,
+                              "flops_per_byte": 2 * macs},
+        "roofline_decompress": {"bound": "hbm", "achieved": step_bytes / step_s / 1e9, "peak": PEAK_HBM_GBPS,
+                                "unit": "GB/s", "frac": step_bytes / step_s / 1e9 / PEAK_HBM_GBPS,
+                                "bytes_per_step": step_bytes},
+    }
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -266,6 +419,10 @@ def main():
     ap.add_argument("--coder-streams", type=int, default=16384)
     ap.add_argument("--coder-len", type=int, default=4096)
     ap.add_argument("--coder-cpu-streams", type=int, default=64)
+    ap.add_argument("--no-extras", action="store_true", help="skip the f32, coder and configs[4] extras")
+    ap.add_argument("--f32-len", type=int, default=1024, help="bytes per chunk of the f32-mode extra")
+    ap.add_argument("--c4-lanes", type=int, default=16384, help="chunks (= lanes) of the configs[4] extra")
+    ap.add_argument("--c4-len", type=int, default=256, help="bytes per chunk of the configs[4] extra")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy 3 times (PMC byte-counter calibration)")
     args = ap.parse_args()
@@ -292,7 +449,7 @@ def main():
                           "launches": 3}))
         return
     if args.workload == "coder":
-        coder_bench(args)
+        print(json.dumps(coder_bench(args, args.steps, args.warmup, args.coder_cpu_streams)))
         return
     lib = N.lib()
     dev = torch.device("cuda")
@@ -370,7 +527,7 @@ def main():
         log(f"[bench] step {i}: compress {t1 - t0:.2f}s decompress {t2 - t1b:.2f}s words {total.value}")
         if i == 0:
             prof = {"compress": pc, "decompress": pd}
-    ok = bool(torch.equal(out, X))
+    ok = lanes_equal(out, X, lens_h)
     comp_bytes = 4 * int(nw.sum().item())
     tc, td = float(np.mean(tcs)), float(np.mean(tds))
     # PCIe legs of the host-memory API (codec.compress_GPU / decompress_GPU): input H2D + payload D2H for
@@ -429,10 +586,29 @@ def main():
         cpu = cpu_baseline(args.cpu_steps)
         log(f"[bench] CPU baseline {cpu['value']:.5f} MB/s in {cpu['seconds']:.1f}s")
 
+    extras = {}
+    if not args.no_extras:
+        del words, payload, offs
+        log(f"[bench] extra: f32 mode on the first {args.f32_len} B of each chunk")
+        extras.update(f32_extra(lib, X, lens_h, args.f32_len))
+        log(f"[bench] extra: f32 compress {extras['f32_compress_MBps']:.3f} MB/s, decompress "
+            f"{extras['f32_decompress_MBps']:.3f} MB/s, round trip {extras['f32_round_trip_ok']}")
+        del eng
+        torch.cuda.empty_cache()
+        log("[bench] extra: range coder alone (configs[1])")
+        extras["coder"] = coder_bench(args, 3, 1, args.coder_cpu_streams if not args.no_cpu else 0)
+        log(f"[bench] extra: coder {extras['coder']['value'] / 1e9:.2f} G symbols/s, round trip "
+            f"{extras['coder']['round_trip_ok']}")
+        torch.cuda.empty_cache()
+        log(f"[bench] extra: configs[4] on {args.c4_lanes} chunks x {args.c4_len} B")
+        extras["config4"] = config4_extra(lib, args.c4_lanes, args.c4_len)
+        log(f"[bench] extra: configs[4] compress {extras['config4']['compress_MBps']:.3f} MB/s, decompress "
+            f"{extras['config4']['decompress_MBps']:.3f} MB/s, round trip {extras['config4']['round_trip_ok']}")
+
     value = nbytes / (tc + td) / 1e6
     res = {
         "metric": METRIC,
-        "value": value,
+        "value": value if ok else None,
         "unit": "MB/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -441,15 +617,18 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "bf16x3",
         "data": "synthetic",
         "config": {
             "workload": ("configs[2]+configs[3]: compress then decompress 64 MiB float32 records (seed 0), "
-                         f"{B} chunks x {chunk} B, d256x8L Mamba fp32 random init seed 0, inputs in HBM"),
+                         f"{B} chunks x {chunk} B, d256x8L Mamba random init seed 0 (fp32 weights), GEMMs in "
+                         "bf16x3 (fp32 operands split into bf16 hi+lo, three bf16 MFMA products, fp32 "
+                         "accumulation), inputs in HBM"),
             "chunks": B,
             "chunk_len": chunk,
             "payload_bytes": nbytes,
             "tile_len": args.tile_len,
+            "precision": "bf16x3",
         },
         "compress_MBps": nbytes / tc / 1e6,
         "decompress_MBps": nbytes / td / 1e6,
@@ -469,7 +648,11 @@ def main():
     if cpu:
         res["vs_cpu_compress"] = res["compress_MBps"] / cpu["compress_MBps"]
         res["vs_cpu_decompress"] = res["decompress_MBps"] / cpu["decompress_MBps"]
+    res.update(extras)
     print(json.dumps(res))
+    if not ok:
+        log("[bench] round trip FAILED: the headline value is withheld")
+        sys.exit(1)
 
 
 if __name__ == "__main__":

@@ -153,3 +153,30 @@ def test_round_trip_d512_bf16w(gpu):
     out = codec.decompress_payload(m, payload, nw, Ls, fb)
     for i, c in enumerate(chunks):
         assert (out[i, :L] == c).all(), i
+
+
+def test_wave_lanes_from_device_memory(gpu):
+    """Without BOA_GPU_STREAMS the wave holds every chunk that fits in free device memory (288 GB: all of
+    configs[4]'s 16384 chunks), never more than asked, and the context it implies is exactly what
+    boa_ctx_create allocates."""
+    import boa
+
+    m, _ = _model(2)
+    os.environ.pop("BOA_GPU_STREAMS", None)
+    assert boa._wave_lanes(m, 7, 100) == 7
+    big = boa._wave_lanes(m, 16384, 16384)
+    assert big == 16384
+    eng = m.engine(64, 64)
+    import ctypes
+
+    from boa_amd import _native as N
+
+    c = N.ModelCfg(256, 2, 256, 16, 4, 2, 0)
+    b = ctypes.c_int64(0)
+    N.check(gpu.boa_ctx_plan_bytes(ctypes.byref(c), N.BOA_PREC_BF16X3, 64, 64, ctypes.byref(b)))
+    assert b.value == eng.device_bytes
+    os.environ["BOA_GPU_STREAMS"] = "5"
+    try:
+        assert boa._wave_lanes(m, 7, 100) == 5
+    finally:
+        del os.environ["BOA_GPU_STREAMS"]
