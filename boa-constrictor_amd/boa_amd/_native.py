@@ -84,6 +84,7 @@ SIGNATURES = [
     ("boa_decompress", ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I32, _I32, _P, _I64]),
     ("boa_xq_cdf", ctypes.c_int, [_P, _I64, _I32, _I32, _P, _P]),
     ("boa_compact", ctypes.c_int, [_P, _I64, _P, _I32, _P, _P, _I64, ctypes.POINTER(_I64), _P]),
+    ("boa_compact_noalloc", ctypes.c_int, [_P, _I64, _P, _I32, _P, _P, _I64, ctypes.POINTER(_I64), _P]),
     ("rc_encode_tables", ctypes.c_int, [_I32, _I32, _P, _I32, _P, _I32, _I32, _P, _I64, _P, _P]),
     ("rc_decode_tables", ctypes.c_int, [_I32, _I32, _P, _I32, _P, _I64, _P, _I32, _I32, _P, _P]),
     ("rc_synth_tables", ctypes.c_int, [_U64, _F32, _I32, _I32, _I32, _I32, _I32, _P, _P, _P]),

@@ -7,9 +7,12 @@
 // does not depend on scheduling), then one workgroup per lane gathers its words.  Only the payload's
 // total crosses to the host.
 //
-// The scan keeps one partial sum per workgroup of 1024 lanes plus the total in a scratch buffer that the
-// library allocates once per device and stream (and grows when a larger wave arrives), kept until the
-// process ends.
+// The scan keeps one partial sum per workgroup of 1024 lanes plus the total in a scratch buffer:
+//   boa_compact          a buffer the library allocates once per device and stream (and grows when a
+//                        larger wave arrives), kept until the process ends;
+//   boa_compact_noalloc  the file-scope device array `scratch` (at most kMaxScanBlocks workgroups, i.e.
+//                        262144 lanes), for callers that cannot allocate; every call on one GPU shares it,
+//                        so calls that overlap on one GPU race.
 #include "boa_common.h"
 
 #include <map>
@@ -21,9 +24,19 @@
 using namespace boa;
 
 namespace {
+constexpr int kScanBlockLanes = 1024;  // lanes per scan workgroup
+constexpr int kStaticScanBlocks = BOA_COMPACT_NOALLOC_MAX_LANES / kScanBlockLanes;  // partials the static array holds
+static_assert(kStaticScanBlocks * kScanBlockLanes == BOA_COMPACT_NOALLOC_MAX_LANES, "static scratch size");
+}  // namespace
 
-constexpr int kScanBlock = 1024;     // lanes per scan workgroup
-constexpr int kMaxScanBlocks = 256;  // smallest scratch allocation, in workgroup partials
+// boa_compact_noalloc's scratch: [0] = total words, [1 + w] = partial of scan workgroup w.  Nothing in it
+// needs clearing between calls: every call writes each entry before it reads it.
+static __device__ __align__(256) int64_t scratch[1 + kStaticScanBlocks];
+
+namespace {
+
+constexpr int kScanBlock = kScanBlockLanes;
+constexpr int kMaxScanBlocks = kStaticScanBlocks;  // also the smallest allocation of boa_compact's scratch
 constexpr int kMaxDevices = 64;
 
 __device__ __forceinline__ int64_t lane_words(const int32_t* nwords, int n, int i) {
@@ -140,6 +153,8 @@ struct HeapScratch {
 };
 std::map<std::pair<int, hipStream_t>, HeapScratch> g_heap;  // boa_compact's scratch, per (device, stream)
 
+int64_t* g_static[kMaxDevices] = {};  // device address of `scratch`, per device
+
 int current_device(const char* who, int* dev) {
     BOA_HIP_TRY(hipGetDevice(dev));
     if (*dev < 0 || *dev >= kMaxDevices) return boa_fail(BOA_ERR_ARG, "%s: device %d out of range", who, *dev);
@@ -182,4 +197,36 @@ extern "C" int boa_compact(const uint32_t* d_words, int64_t pitch_words, const i
     }
     return compact_with("boa_compact", sc, d_words, pitch_words, d_nwords, lanes, d_word_off, d_payload, payload_cap,
                         h_total_words, s);
+}
+
+extern "C" int boa_compact_noalloc(const uint32_t* d_words, int64_t pitch_words, const int32_t* d_nwords,
+                                   int32_t lanes, int64_t* d_word_off, uint32_t* d_payload, int64_t payload_cap,
+                                   int64_t* h_total_words, void* stream) {
+    if (!d_words || !d_nwords || !d_word_off || lanes < 0 || !h_total_words)
+        return boa_fail(BOA_ERR_ARG, "boa_compact_noalloc: bad arguments");
+    *h_total_words = 0;
+    if (lanes > BOA_COMPACT_NOALLOC_MAX_LANES)
+        return boa_fail(BOA_ERR_ARG, "boa_compact_noalloc: %d lanes exceed the static scratch maximum of %d", lanes,
+                        BOA_COMPACT_NOALLOC_MAX_LANES);
+    if (lanes == 0) return BOA_OK;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    int dev = 0;
+    int rc = current_device("boa_compact_noalloc", &dev);
+    if (rc != BOA_OK) return rc;
+    int64_t* sc = nullptr;
+    {
+        // the array's own name is a host-side stand-in: its device address (one copy per GPU) is looked up
+        // once per device and used for every kernel argument and copy
+        std::lock_guard<std::mutex> g(g_mu);
+        if (!g_static[dev]) {
+            void* p = nullptr;
+            const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess) return boa_fail_hip(e, "hipGetSymbolAddress(scratch)", __FILE__, __LINE__);
+            if (!p) return boa_fail(BOA_ERR_HIP, "boa_compact_noalloc: scratch has no device address");
+            g_static[dev] = static_cast<int64_t*>(p);
+        }
+        sc = g_static[dev];
+    }
+    return compact_with("boa_compact_noalloc", sc, d_words, pitch_words, d_nwords, lanes, d_word_off, d_payload,
+                        payload_cap, h_total_words, s);
 }

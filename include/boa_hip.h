@@ -147,6 +147,17 @@ int boa_compact(const uint32_t* d_words, int64_t pitch_words, const int32_t* d_n
                 int64_t* d_word_off, uint32_t* d_payload, int64_t payload_cap, int64_t* h_total_words,
                 void* stream);
 
+/* boa_compact without any device allocation: the same scan and gather, with the scan's partial sums in a
+ * fixed array in the library's device memory (one copy per GPU, held until the process ends) instead of a
+ * buffer the library allocates.  lanes <= 262144 (BOA_COMPACT_NOALLOC_MAX_LANES), else BOA_ERR_ARG.  Calls
+ * that overlap on one GPU share that array and race: issue them one at a time per GPU.  Call it with the
+ * stream's device current.  No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc).          */
+#define BOA_COMPACT_NOALLOC_MAX_LANES 262144
+int boa_compact_noalloc(const uint32_t* d_words, int64_t pitch_words, const int32_t* d_nwords, int32_t lanes,
+                        int64_t* d_word_off, uint32_t* d_payload, int64_t payload_cap, int64_t* h_total_words,
+                        void* stream);
+
 /* ------------------------------------------------------------------------------------------------ */
 /* Range coder on precomputed CDF tables (the configs' "range coder alone" case).  d_cdf holds
  * [streams][len][K] entries of cdf_bytes (2 or 4) each: cdf[0..K-1] of each step, cdf[K] = 2^precision
