@@ -180,3 +180,28 @@ def test_wave_lanes_from_device_memory(gpu):
         assert boa._wave_lanes(m, 7, 100) == 5
     finally:
         del os.environ["BOA_GPU_STREAMS"]
+
+
+def test_compressed_size_vs_oracle_config2(gpu, ora):
+    """configs[2]'s own model (d256 x 8 layers, seed 0) and data (float32 records, the first 32 of its 4096
+    chunks, first 1024 B of each) in the default bf16x3 mode: compressed size within 0.5% of the reference
+    protocol run on the CPU oracle (fp32 model -> torch.softmax -> Q2 at P = 24 -> coder), and the round
+    trip byte-exact."""
+    import codec
+    from bench import synth_records
+
+    lanes, L = 32, 1024
+    m, blob = _model(8, seed=0)
+    assert m.precision == "bf16x3"
+    data = np.ascontiguousarray(synth_records(lanes * 16384, 0).reshape(lanes, 16384)[:, :L])
+    chunks = [data[i] for i in range(lanes)]
+    payload, nw, fb, Ls = codec.compress_payload(m, chunks)
+    ref = model_ref.RefModel(blob, weights_ref.Cfg(n_layers=8))
+    X = torch.from_numpy(data.astype(np.int64))
+    probs = torch.softmax(ref.forward(X[:, :-1]), dim=-1).to(torch.float32).numpy()
+    ref_words = sum(len(ora.encode_probs_q2(24, probs[b], X[b, 1:].numpy().astype(np.int32))) for b in range(lanes))
+    gpu_words = int(nw.sum())
+    print(f"gpu words {gpu_words}  oracle words {ref_words}", flush=True)
+    assert abs(gpu_words - ref_words) <= 0.005 * ref_words
+    out = codec.decompress_payload(m, payload, nw, Ls, fb)
+    assert np.array_equal(out, data)

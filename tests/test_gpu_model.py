@@ -205,3 +205,21 @@ def test_d512_config4_shape_vs_oracle_and_identity(gpu, precision):
     inf = m.init_stream(max_len=T, batch_size=B)
     ls = torch.stack([m.step(tok[:, t].cuda(), inf) for t in range(T)], dim=1)
     assert torch.equal(ls, lf), float((ls - lf).abs().max())
+
+
+def test_config4_model_16_layers_vs_oracle(gpu):
+    """configs[4]'s model itself: d_model 512 x 16 layers, seed 1, bf16 weights.  Teacher-forced logits
+    (compress path, > one 64-position tile) against the oracle with the same bf16-rounded weights, within
+    the 1e-4 bar, and the decode path (step by step) bit-identical to them."""
+    m, ref = _model(16, seed=1, d=512, precision="bf16w")
+    rng = np.random.default_rng(41)
+    B, T = 6, 70
+    tok = torch.from_numpy(rng.integers(0, 256, (B, T)))
+    lf = m(tok.cuda())
+    lr = ref.forward(tok)
+    err = _rel(lf.cpu(), lr)
+    print(f"d512x16L bf16w rel_err={err:.3e}", flush=True)
+    assert err <= REL_TOL
+    inf = m.init_stream(max_len=T, batch_size=B)
+    ls = torch.stack([m.step(tok[:, t].cuda(), inf) for t in range(T)], dim=1)
+    assert torch.equal(ls, lf), float((ls - lf).abs().max())
