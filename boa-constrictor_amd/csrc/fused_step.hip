@@ -263,21 +263,29 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
             // are not written (buffer range check), so no access is under a branch
             const __amdgpu_buffer_rsrc_t hr3 =
                 buf_rsrc(a.hist + ((int64_t)l * a.max_lanes + b0) * 3 * FDI, (uint32_t)nb * 3 * FDI * 4);
+            // Per-lane offsets are formed inside each unrolled iteration from an opaque copy of the channel
+            // index: precomputed for all lanes at once they would hold dozens of registers across the layer
+            // loop, which spill, and every reload of a spilled offset (a vector memory load) waits for all the
+            // state loads issued before it.
             float h0[ROWS], h1[ROWS], h2[ROWS];
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) {
-                const uint32_t o = (uint32_t)(r * 3 * FDI + c) * 4;
+                int cq = c;
+                __asm__ volatile("" : "+v"(cq));
+                const uint32_t o = (uint32_t)(r * 3 * FDI + cq) * 4;
                 h0[r] = buf_ld1(hr3, o + p0m3 * FDI * 4);
                 h1[r] = buf_ld1(hr3, o + s1 * FDI * 4);
                 h2[r] = buf_ld1(hr3, o + s2 * FDI * 4);
             }
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) {
-                const float x = sX[r * LXZ + c];
+                int cq = c;
+                __asm__ volatile("" : "+v"(cq));
+                const float x = sX[r * LXZ + cq];
                 const float y = conv_point(cw, cb, h0[r], h1[r], h2[r], x);
-                sX[r * LXZ + c] = y;
-                put_split(sAh, sAl, r * LA + c, y);
-                buf_st1(hr3, (uint32_t)(r * 3 * FDI + p0m3 * FDI + c) * 4, x);
+                sX[r * LXZ + cq] = y;
+                put_split(sAh, sAl, r * LA + cq, y);
+                buf_st1(hr3, (uint32_t)(r * 3 * FDI + p0m3 * FDI + cq) * 4, x);
             }
             // the partial reads only split values this wavefront wrote (channels 64 wave .. 64 wave + 63 of
             // every row); LDS operations of one wavefront complete in order
@@ -336,25 +344,28 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
             // loads in flight.
             const __amdgpu_buffer_rsrc_t sr =
                 buf_rsrc(a.ssm + ((int64_t)l * a.max_lanes + b0) * FDI * FNS, (uint32_t)nb * FDI * FNS * 4);
-            auto h_off = [&](int r, int n) { return (uint32_t)((r * FNS / 4 + n / 4) * FDI + c) * 16; };
+            auto h_off = [&](int r, int n, int cq) { return (uint32_t)((r * FNS / 4 + n / 4) * FDI + cq) * 16; };
             // One lane's state at a time, loaded at the top of its row (the barrier keeps the loads ahead of the
             // row's LDS reads) and stored at its end.  The two waves of a SIMD take turns waiting on memory;
-            // keeping 1-3 more lanes in flight per thread measured 2-7% slower per decode step (more registers in
-            // a kernel that is at its register limit).
+            // loading the next lane's state one row ahead (before this row's stores) measured the same, keeping
+            // 1-3 more lanes in flight per thread 2-7% slower (more registers in a kernel at its register limit).
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) {
+                int cq = c;  // opaque per lane: offsets formed here, not held across the loop (see the conv)
+                __asm__ volatile("" : "+v"(cq));
                 float h[FNS];
 #pragma unroll
                 for (int n = 0; n < FNS; n += 4) {
-                    const f32x4 q = buf_ld4(sr, h_off(r, n));
+                    const f32x4 q = buf_ld4(sr, h_off(r, n, cq));
                     h[n] = q.x; h[n + 1] = q.y; h[n + 2] = q.z; h[n + 3] = q.w;
                 }
                 __builtin_amdgcn_sched_barrier(0);
-                const float x = sX[r * LXZ + c], z = sX[r * LXZ + FDI + c];
+                const float x = sX[r * LXZ + cq], z = sX[r * LXZ + FDI + cq];
                 const float y = scan_position<FNS, FR>(sDbc + r * FW, wr, bdt, av, Dc, x, z, h);
-                put_split(sAh, sAl, r * LA + c, y);
+                put_split(sAh, sAl, r * LA + cq, y);
 #pragma unroll
-                for (int n = 0; n < FNS; n += 4) buf_st4(sr, h_off(r, n), f32x4{h[n], h[n + 1], h[n + 2], h[n + 3]});
+                for (int n = 0; n < FNS; n += 4)
+                    buf_st4(sr, h_off(r, n, cq), f32x4{h[n], h[n + 1], h[n + 2], h[n + 3]});
             }
         }
         __syncthreads();
