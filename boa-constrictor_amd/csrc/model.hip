@@ -624,19 +624,33 @@ __global__ void __launch_bounds__(256) k_convx_step(const float* __restrict__ xz
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t b0 = (int64_t)blockIdx.x * 16;
     const int s1 = p0m3 == 2 ? 0 : p0m3 + 1, s2 = p0m3 == 0 ? 2 : p0m3 - 1;
+    // History rows of lanes [b0, b0 + nb) through a range-checked buffer (rows past B read 0 and are not
+    // written), non-temporal, all 16 lanes' loads in flight before the first use; rows past B take the last
+    // lane's x and are not stored.  Offsets are formed per lane from an opaque channel index (not held).
+    const int nb = (int)((B - b0) < 16 ? (B - b0) : 16);
+    const __amdgpu_buffer_rsrc_t hr = buf_rsrc(hist + b0 * 3 * di, (uint32_t)nb * 3 * di * 4);
     for (int c = tid; c < di; c += 256) {
-        const float4 wv = *reinterpret_cast<const float4*>(w + 4 * c);
-        const float bb = bias[c];
-#pragma unroll 4
+        const float4 wv = ldg_f4(G(w) + 4 * c);
+        const float bb = G(bias)[c];
+        float h0[16], h1[16], h2[16], xv[16];
+#pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int64_t b = b0 + r;
-            if (b >= B) break;
-            float* hb = hist + b * 3 * di;
-            const float x = xz[b * ldxz + c];
-            const float y = conv_point(wv, bb, hb[p0m3 * di + c], hb[s1 * di + c], hb[s2 * di + c], x);
-            xs[b * di + c] = y;
-            sX[r * LDX + c] = y;
-            hb[p0m3 * di + c] = x;
+            int cq = c;
+            __asm__ volatile("" : "+v"(cq));
+            const uint32_t o = (uint32_t)(r * 3 * di + cq) * 4;
+            h0[r] = buf_ld1(hr, o + p0m3 * di * 4);
+            h1[r] = buf_ld1(hr, o + s1 * di * 4);
+            h2[r] = buf_ld1(hr, o + s2 * di * 4);
+            xv[r] = G(xz)[(b0 + (r < nb ? r : nb - 1)) * ldxz + cq];
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            int cq = c;
+            __asm__ volatile("" : "+v"(cq));
+            const float y = conv_point(wv, bb, h0[r], h1[r], h2[r], xv[r]);
+            if (r < nb) xs[(b0 + r) * di + cq] = y;
+            sX[r * LDX + cq] = y;
+            buf_st1(hr, (uint32_t)(r * 3 * di + p0m3 * di + cq) * 4, xv[r]);
         }
     }
     __syncthreads();
@@ -1177,25 +1191,58 @@ __global__ void __launch_bounds__(256) k_scan(float* __restrict__ xs_y, const fl
     scan_store_channel<NS>(hp, di, h);
 }
 
-// Step kernel (decompress path): one position per lane; the [dr | B | C] row is uniform across the
-// workgroup and read straight from memory.
+// Step kernel (decompress path, per-layer kernels): one position per lane.  A workgroup owns 256 channels of
+// SCAN_LPB consecutive lanes: each channel's parameters (A, its dt_proj row, biases) are loaded once for all of
+// them, and each lane's 64 B of state per channel stream through range-checked non-temporal buffer accesses
+// (lanes past B read 0 and are not written, so no state access is under a branch), the next lane's state
+// loaded before the current lane computes.  The [dr | B | C] row of a lane is uniform across the workgroup.
+constexpr int SCAN_LPB = 8;
 template <int NS, int R, bool OUTS>
 __global__ void __launch_bounds__(256) k_scan_step(float* __restrict__ xs_y, const float* __restrict__ dbc, int ldd,
                                                   const float* __restrict__ xz, int64_t ldxz,
                                                   const float* __restrict__ dt_w, const float* __restrict__ dt_b,
                                                   const float* __restrict__ Aneg, const float* __restrict__ Dp,
-                                                  float* __restrict__ ssm, int di, uint16_t* __restrict__ yh,
+                                                  float* __restrict__ ssm, int di, int B, uint16_t* __restrict__ yh,
                                                   uint16_t* __restrict__ yl) {
-    const int64_t b = blockIdx.y;
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= di) return;
-    float h[NS], a[NS], wr[R];
-    float* hp = ssm + b * di * NS + 4 * c;
-    scan_load_channel<NS, R>(c, di, hp, Aneg, dt_w, h, a, wr);
-    const float x = xs_y[b * di + c];
-    const float z = xz[b * ldxz + di + c];
-    scan_store_y<OUTS>(xs_y, yh, yl, b * di + c, scan_position<NS, R>(dbc + b * ldd, wr, dt_b[c], a, Dp[c], x, z, h));
-    scan_store_channel<NS>(hp, di, h);
+    const int c = blockIdx.x * 256 + threadIdx.x;  // di is a multiple of 256
+    const int64_t b0 = (int64_t)blockIdx.y * SCAN_LPB;
+    const int nb = (int)((B - b0) < SCAN_LPB ? (B - b0) : SCAN_LPB);
+    float a[NS], wr[R];
+#pragma unroll
+    for (int n = 0; n < NS; n += 4) {
+        const float4 p = ldg_f4(G(Aneg) + ((int64_t)(n / 4) * di + c) * 4);
+        a[n] = p.x; a[n + 1] = p.y; a[n + 2] = p.z; a[n + 3] = p.w;
+    }
+#pragma unroll
+    for (int r = 0; r < R; r += 4) {
+        const float4 q = ldg_f4(G(dt_w) + (int64_t)c * R + r);
+        wr[r] = q.x; wr[r + 1] = q.y; wr[r + 2] = q.z; wr[r + 3] = q.w;
+    }
+    const float bdt = G(dt_b)[c], Dc = G(Dp)[c];
+    const __amdgpu_buffer_rsrc_t sr = buf_rsrc(ssm + b0 * di * NS, (uint32_t)nb * di * NS * 4);
+    auto h_off = [&](int r, int n) { return (uint32_t)(((int64_t)r * NS / 4 + n / 4) * di + c) * 16; };
+    f32x4 nxt[NS / 4];
+#pragma unroll
+    for (int n = 0; n < NS; n += 4) nxt[n / 4] = buf_ld4(sr, h_off(0, n));
+#pragma unroll
+    for (int r = 0; r < SCAN_LPB; ++r) {
+        float h[NS];
+#pragma unroll
+        for (int n = 0; n < NS; n += 4) {
+            h[n] = nxt[n / 4].x; h[n + 1] = nxt[n / 4].y; h[n + 2] = nxt[n / 4].z; h[n + 3] = nxt[n / 4].w;
+        }
+        if (r + 1 < SCAN_LPB) {  // resolved at compile time
+#pragma unroll
+            for (int n = 0; n < NS; n += 4) nxt[n / 4] = buf_ld4(sr, h_off(r + 1, n));
+        }
+        const int64_t b = b0 + (r < nb ? r : nb - 1);  // rows past B repeat the last lane's inputs, unused
+        const float x = xs_y[b * di + c];
+        const float z = xz[b * ldxz + di + c];
+        const float y = scan_position<NS, R>(dbc + b * ldd, wr, bdt, a, Dc, x, z, h);
+        if (r < nb) scan_store_y<OUTS>(xs_y, yh, yl, b * di + c, y);
+#pragma unroll
+        for (int n = 0; n < NS; n += 4) buf_st4(sr, h_off(r, n), f32x4{h[n], h[n + 1], h[n + 2], h[n + 3]});
+    }
 }
 
 // ================================================================================================
@@ -1813,8 +1860,9 @@ static void launch_scan(boa_ctx* x, const LayerW& w, float* ssm, int B, int Tc) 
     const int di = x->di;
     const dim3 grid((di + 255) / 256, B);
     if (Tc == 1)
-        hipLaunchKernelGGL((k_scan_step<NS, R, OUTS>), grid, dim3(256), 0, x->stream, x->xs, x->dbc, R + 2 * NS, x->xz,
-                           (int64_t)2 * di, w.dt_w, w.dt_b, w.Aneg, w.D, ssm, di, x->ah, x->al);
+        hipLaunchKernelGGL((k_scan_step<NS, R, OUTS>), dim3(di / 256, (B + SCAN_LPB - 1) / SCAN_LPB), dim3(256), 0,
+                           x->stream, x->xs, x->dbc, R + 2 * NS, x->xz, (int64_t)2 * di, w.dt_w, w.dt_b, w.Aneg, w.D,
+                           ssm, di, B, x->ah, x->al);
     else
         hipLaunchKernelGGL((k_scan<NS, R, OUTS>), grid, dim3(256), 0, x->stream, x->xs, x->dbc, R + 2 * NS, x->xz,
                            (int64_t)2 * di, w.dt_w, w.dt_b, w.Aneg, w.D, ssm, di, Tc, x->ah, x->al);
