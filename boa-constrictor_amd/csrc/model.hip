@@ -895,6 +895,175 @@ __global__ void __launch_bounds__(512, 4) k_ffn(const float* __restrict__ mm, co
 }
 
 // ================================================================================================
+// The same feed-forward half for d_model 512 (d_ff 2048; configs[4]'s shape):
+//   x <- x + FF2(GELU(FF1(LN2(mm))))
+// A workgroup of 512 threads owns 64 rows (one workgroup per CU: the LN2 operand is 128 KB).  Per 64-wide chunk
+// of the hidden layer: FF1 (+bias, GELU, split) into LDS, then FF2 accumulates the chunk into registers, so the
+// hidden activations never leave the chip.  The arithmetic of every value is that of the layer-by-layer path
+// (ln_stats_row / ln_apply / split2; FF1 outputs accumulate their 16 K steps in ascending order through
+// mfma_split_step_t, then epi_value<GELU>; FF2 outputs accumulate all 64 K steps in ascending order, chunk by
+// chunk, then x + epi_value<RESID>), so rows equal those of the GEMM kernels bit for bit.  Used by the compress
+// tiles (64 positions of one lane) and by the per-layer decode step (64 lanes of one position).
+//   FF1: wave w computes rows 32 (w & 1) .. + 31 x hidden units 16 (w >> 1) .. + 15 of the chunk, the W1 block as
+//        the MFMA A operand (a lane's 4 outputs are 4 consecutive hidden units, one 8-byte store per part).
+//   FF2: wave w owns outputs 64 w .. + 63 (4 fragments) of all 64 rows: 16 accumulators.
+// Per chunk a wave uses 24 weight blocks (16 of W1, then 8 of W2) through a ring of R register slots in use
+// order, running on into the next chunk, so R blocks are always in flight.
+namespace ffn5 {
+constexpr int BM = 64, D = 512, DF = 2048, HC = 64;
+// 16-byte chunks XOR-swizzled by row (low 4 bits of the chunk index), so 16-row fragment reads spread over banks
+__device__ __forceinline__ int a_off(int r, int k) { return r * D + (((k >> 3) ^ (r & 15)) << 3) + (k & 7); }
+__device__ __forceinline__ int h_off(int r, int k) { return r * HC + (((k >> 3) ^ (r >> 1)) & 7) * 8 + (k & 7); }
+}  // namespace ffn5
+
+template <int NT>
+__global__ void __launch_bounds__(512, 2) k_ffn512(const float* __restrict__ mm, const float* __restrict__ ln_w,
+                                                   const float* __restrict__ ln_b, const uint16_t* __restrict__ W1p,
+                                                   const float* __restrict__ b1, const uint16_t* __restrict__ W2p,
+                                                   const float* __restrict__ b2, float* __restrict__ x, int64_t M) {
+    using namespace ffn5;
+    __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * D];
+    __shared__ __attribute__((aligned(16))) uint16_t sH[2][BM * HC];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t m0 = (int64_t)blockIdx.x * BM;
+    const int rows = (int)((M - m0) < BM ? (M - m0) : BM);
+    {
+        // LN2 of 8 rows per wave; rows past M read 0 (buffer range check) and are never stored
+        const __amdgpu_buffer_rsrc_t rm = buf_rsrc(mm + m0 * D, (uint32_t)rows * D * 4);
+        const float4 w0 = ldg_f4(G(ln_w) + 4 * lane), w1 = ldg_f4(G(ln_w) + 256 + 4 * lane);
+        const float4 c0 = ldg_f4(G(ln_b) + 4 * lane), c1 = ldg_f4(G(ln_b) + 256 + 4 * lane);
+        const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        const float bv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+#pragma unroll 2
+        for (int q = 0; q < BM / 8; ++q) {
+            const int r = 8 * wave + q;
+            const u32x4 u0 = buf_ld16(rm, (uint32_t)((r * D + 4 * lane) * 4));
+            const u32x4 u1 = buf_ld16(rm, (uint32_t)((r * D + 256 + 4 * lane) * 4));
+            const float v[8] = {__uint_as_float(u0.x), __uint_as_float(u0.y), __uint_as_float(u0.z), __uint_as_float(u0.w),
+                                __uint_as_float(u1.x), __uint_as_float(u1.y), __uint_as_float(u1.z), __uint_as_float(u1.w)};
+            float mu, rs;
+            ln_stats_row<2>(v, mu, rs);
+            float y[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) y[i] = ln_apply(v[i], mu, rs, wv[i], bv[i]);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                uint2 hp, lp;
+                split4(y[4 * h], y[4 * h + 1], y[4 * h + 2], y[4 * h + 3], hp, lp);
+                const int o = a_off(r, 256 * h + 4 * lane);
+                *reinterpret_cast<uint2*>(&sA[0][o]) = hp;
+                *reinterpret_cast<uint2*>(&sA[1][o]) = lp;
+            }
+        }
+    }
+    __syncthreads();
+    const int ar = lane & 15, kq = 8 * (lane >> 4), m_of = 4 * (lane >> 4);
+    constexpr int BLK = (NT == 3) ? 1024 : 512;
+    const gptr<uint16_t> w1p = G(W1p), w2p = G(W2p);
+    const int rh = wave & 1, cf = wave >> 1;
+    constexpr int NB1 = D / 32, NBC = NB1 + 8, R = 6;
+    static_assert(NBC % R == 0, "ring slots divide the blocks of a chunk");
+    u32x4 rhh[R], rll[R];
+    // block i of chunk c: i < 16: W1 fragment 4 c + cf, K step i; else W2 fragment 4 wave + (i - 16) % 4,
+    // K step 2 c + (i - 16) / 4
+    auto issue = [&](int c, int i) {
+        const int64_t blk = i < NB1 ? (int64_t)(4 * c + cf) * (D / 32) + i
+                                    : (int64_t)(4 * wave + ((i - NB1) & 3)) * (DF / 32) + 2 * c + ((i - NB1) >> 2);
+        const gptr<uint16_t> q = (i < NB1 ? w1p : w2p) + blk * BLK + lane * 8;
+        rhh[i % R] = ldg16(q);
+        rll[i % R] = rhh[i % R];
+        if constexpr (NT == 3) rll[i % R] = ldg16(q + 512);
+    };
+    auto refill = [&](int c, int cn, int i) {
+        if (i + R < NBC) issue(c, i + R);
+        else issue(cn, i + R - NBC);
+    };
+    floatx4 out[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) out[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < R; ++i) issue(0, i);
+#pragma unroll 1
+    for (int c = 0; c < DF / HC; ++c) {
+        const int cn = c + 1 < DF / HC ? c + 1 : c;
+        const float4 bias = ldg_f4(G(b1) + HC * c + 16 * cf + m_of);
+        floatx4 hacc[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) hacc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < NB1; ++s) {
+            bf16x8 ah[2], al[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int o = a_off(32 * rh + 16 * i + ar, 32 * s + kq);
+                ah[i] = *reinterpret_cast<const bf16x8*>(&sA[0][o]);
+                al[i] = *reinterpret_cast<const bf16x8*>(&sA[1][o]);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                hacc[i] = mfma_split_step_t<NT>(hacc[i], ah[i], al[i], __builtin_bit_cast(bf16x8, rhh[s % R]),
+                                                __builtin_bit_cast(bf16x8, rll[s % R]));
+            refill(c, cn, s);
+            pin_loads();
+        }
+        {
+            const float bv[4] = {bias.x, bias.y, bias.z, bias.w};
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                float g[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) g[r] = epi_value<EPI_GELU>(hacc[i][r], bv[r]);
+                uint2 hp, lp;
+                split4(g[0], g[1], g[2], g[3], hp, lp);
+                const int o = h_off(32 * rh + 16 * i + ar, 16 * cf + m_of);
+                *reinterpret_cast<uint2*>(&sH[0][o]) = hp;
+                *reinterpret_cast<uint2*>(&sH[1][o]) = lp;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            bf16x8 ah[4], al[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int o = h_off(16 * i + ar, 32 * t + kq);
+                ah[i] = *reinterpret_cast<const bf16x8*>(&sH[0][o]);
+                al[i] = *reinterpret_cast<const bf16x8*>(&sH[1][o]);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int bi = NB1 + 4 * t + j;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    out[i][j] = mfma_split_step<NT>(out[i][j], ah[i], al[i], __builtin_bit_cast(bf16x8, rhh[bi % R]),
+                                                    __builtin_bit_cast(bf16x8, rll[bi % R]));
+                refill(c, cn, bi);
+                pin_loads();
+            }
+        }
+        __syncthreads();
+    }
+    const __amdgpu_buffer_rsrc_t rx = buf_rsrc(x + m0 * D, (uint32_t)rows * D * 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int col = 16 * (4 * wave + j) + ar;
+        const float bias = G(b2)[col];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t o = (uint32_t)(((16 * i + m_of + r) * D + col) * 4);
+                const float res = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, o, 0, 0));
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, res + epi_value<EPI_RESID>(out[i][j][r], bias)),
+                                                      rx, o, 0, 0);
+            }
+    }
+}
+
+// ================================================================================================
 // Input half of the mixer in one kernel (split modes, d_model 256, compress tiles of 64 positions):
 //   LN1 -> in_proj (+bias) -> z to HBM; x -> causal conv + SiLU over the 64 positions -> xs to HBM ->
 //   x_proj -> dbc to HBM; the conv history ring of the lane advanced by 64 positions.
@@ -1554,10 +1723,8 @@ static int64_t ctx_plan_bytes(const boa_model_cfg& c, int R, int precision, int6
     if (precision != BOA_PREC_F32) {
         int64_t mats = L * (2 * di * d + (R + 2 * NS) * di + d * di + 4 * d * d + 4 * d * d) + d * d + V * d;
         b += 2 * std::max<int64_t>(2 * mats, 1);
-        if (want_fused(c, R, precision)) {
-            b += 2 * std::max<int64_t>((precision == BOA_PREC_BF16X3 ? 2 : 1) * mats, 1);
-            b += (int64_t)sizeof(FusedLayer) * L;
-        }
+        b += 2 * std::max<int64_t>((precision == BOA_PREC_BF16X3 ? 2 : 1) * mats, 1);
+        if (want_fused(c, R, precision)) b += (int64_t)sizeof(FusedLayer) * L;
     }
     return b;
 }
@@ -1756,13 +1923,15 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
         if (const char* v = getenv("BOA_FUSED_STEPS_PER_LAUNCH")) x->fused_steps = std::max(1, atoi(v));
         if (const char* v = getenv("BOA_FUSED_STAGGER_US")) x->stagger_us = std::max(0, atoi(v));
         if (const char* v = getenv("BOA_FUSED_STAGGER_CLASSES")) x->stagger_classes = std::min(8, std::max(1, atoi(v)));
-        if (x->fused) {
+        // fragment-packed parts of every GEMM matrix: read by the fused compress kernels (k_mixin, k_ffn,
+        // k_ffn512) and the fused decode kernel
+        {
             const bool two = x->prec == BOA_PREC_BF16X3;
             int64_t ftotal = 0;
             for (MatW* m : mats) ftotal += (two ? 2 : 1) * m->n;
             frag_host.resize((size_t)ftotal);
             if (e == hipSuccess) e = dmalloc(x, &x->wfrag, ftotal);
-            if (e == hipSuccess) e = dmalloc(x, &x->d_layers, (int64_t)L);
+            if (e == hipSuccess && x->fused) e = dmalloc(x, &x->d_layers, (int64_t)L);
             if (e != hipSuccess) {
                 boa_ctx_destroy(x);
                 return boa_fail_hip(e, "boa_ctx_create allocation", __FILE__, __LINE__);
@@ -1775,8 +1944,8 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
                 fo += (two ? 2 : 1) * m->n;
                 hs += 2 * m->n;
             }
-            layers_host.resize((size_t)L);
-            for (int l = 0; l < L; ++l) {
+            if (x->fused) layers_host.resize((size_t)L);
+            for (int l = 0; l < (x->fused ? L : 0); ++l) {
                 const LayerW& w = x->layers[l];
                 FusedLayer& f = layers_host[(size_t)l];
                 f.ln1_w = w.ln1_w; f.ln1_b = w.ln1_b; f.in_b = w.in_b; f.conv_w = w.conv_w; f.conv_b = w.conv_b;
@@ -1968,6 +2137,21 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc) {
             PROF(PC_OUT, gemm_flops(M, d, di), gemm_bytes(M, d, di), rc = (launch_gemm_f32<0, EPI_BIAS>(g, s)));
         }
         if (rc) return rc;
+    }
+    if (split && d == ffn5::D && 4 * d == ffn5::DF && w.ff1_w.p && w.ff2_w.p) {
+        // LN2 + FF1 + GELU + FF2 + residual in one kernel, d_model 512 (hidden layer kept on chip)
+        const double flops = gemm_flops(M, 4 * d, d) + gemm_flops(M, d, 4 * d);
+        const double bytes = 4.0 * M * d * 3 + 2.0 * (w.ff1_w.l ? 2 : 1) * (2.0 * 4 * d * d);
+        const unsigned grid = (unsigned)((M + ffn5::BM - 1) / ffn5::BM);
+        if (w.ff1_w.l)
+            PROF(PC_FFN, flops, bytes,
+                 hipLaunchKernelGGL((k_ffn512<3>), dim3(grid), dim3(512), 0, s, x->mm, w.ln2_w, w.ln2_b, w.ff1_w.p,
+                                    w.ff1_b, w.ff2_w.p, w.ff2_b, x->x, M));
+        else
+            PROF(PC_FFN, flops, bytes,
+                 hipLaunchKernelGGL((k_ffn512<2>), dim3(grid), dim3(512), 0, s, x->mm, w.ln2_w, w.ln2_b, w.ff1_w.p,
+                                    w.ff1_b, w.ff2_w.p, w.ff2_b, x->x, M));
+        return BOA_OK;
     }
     if (split && d == ffn::D && 4 * d == ffn::DF && w.ff1_w.p && w.ff2_w.p) {
         // LN2 + FF1 + GELU + FF2 + residual in one kernel (hidden layer kept on chip)
