@@ -1263,6 +1263,203 @@ __global__ void __launch_bounds__(256, 2) k_mixin(const float* __restrict__ x, c
         for (int r = 0; r < 4; ++r) GM(dbc)[(m0 + 16 * wave + m_of + r) * FW + 16 * j + ar] = dacc[j][r];
 }
 
+// The mixer's input half for d_model 512 (d_inner 1024, dt_rank 32, x_proj width 64; configs[4]'s shape), one
+// lane's tile of 64 positions per workgroup: LN1 -> in_proj (+bias) -> z to HBM; x -> causal conv + SiLU over the
+// tile -> xs to HBM -> x_proj, folded over 64-channel K blocks (XPROJ_KB) in registers -> dbc to HBM; the conv
+// history ring advanced by 64 positions.  The same arithmetic per value as k_mixin and the layer-by-layer
+// kernels.  The LN1 operand is 128 KB, so one workgroup runs per CU, with 8 waves (2 per SIMD):
+//   in_proj: per 64-column chunk, wave w computes rows 32 (w & 1) .. + 31 x columns 16 (w >> 1) .. + 15, the
+//            weight block as the A operand (each block read by two waves); 16 K steps through a ring of 16
+//            register slots (8 with bf16x3 weights, whose blocks are twice the size) running on into the next
+//            chunk;
+//   conv:    thread = (channel cl, rows 8 g .. 8 g + 7), g = wave: wave 0 reads the 3 history inputs, wave 7
+//            writes the ring back (wave-uniform buffer ranges, no access under a branch);
+//   x_proj:  wave w owns rows 16 (w & 3) .. + 15 x output fragments 2 (w >> 2), + 1.
+namespace mixin5 {
+constexpr int BM = 64, D = 512, DI = 1024, CH = 64, FW = 64;
+}  // namespace mixin5
+
+template <int NT>
+__global__ void __launch_bounds__(512, 2) k_mixin512(const float* __restrict__ x, const float* __restrict__ ln_w,
+                                                     const float* __restrict__ ln_b, const uint16_t* __restrict__ Wip,
+                                                     const float* __restrict__ bin, const float* __restrict__ conv_w,
+                                                     const float* __restrict__ conv_b, const uint16_t* __restrict__ Wxp,
+                                                     float* __restrict__ xz, float* __restrict__ xs,
+                                                     float* __restrict__ dbc, float* __restrict__ hist, int p0m3) {
+    using namespace mixin5;
+    using mixin::sx_off;
+    using mixin::x_off;
+    constexpr int BLK = (NT == 3) ? 1024 : 512;
+    __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * D];  // LN1 output (hi, lo)
+    __shared__ __attribute__((aligned(16))) float sX[BM * CH];        // x chunk fp32; then its conv output split
+    uint16_t* sXh = reinterpret_cast<uint16_t*>(sX);
+    uint16_t* sXl = sXh + BM * CH;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t b = blockIdx.x, m0 = b * BM;
+    // ---- LN1: 8 rows per wave
+    {
+        const float4 w0 = ldg_f4(G(ln_w) + 4 * lane), w1 = ldg_f4(G(ln_w) + 256 + 4 * lane);
+        const float4 c0 = ldg_f4(G(ln_b) + 4 * lane), c1 = ldg_f4(G(ln_b) + 256 + 4 * lane);
+        const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        const float bv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+#pragma unroll 2
+        for (int q = 0; q < BM / 8; ++q) {
+            const int r = 8 * wave + q;
+            const float4 u0 = ldg_f4(G(x) + (m0 + r) * D + 4 * lane);
+            const float4 u1 = ldg_f4(G(x) + (m0 + r) * D + 256 + 4 * lane);
+            const float v[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+            float mu, rs;
+            ln_stats_row<2>(v, mu, rs);
+            float y[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) y[i] = ln_apply(v[i], mu, rs, wv[i], bv[i]);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                uint2 hp, lp;
+                split4(y[4 * h], y[4 * h + 1], y[4 * h + 2], y[4 * h + 3], hp, lp);
+                const int o = ffn5::a_off(r, 256 * h + 4 * lane);
+                *reinterpret_cast<uint2*>(&sA[0][o]) = hp;
+                *reinterpret_cast<uint2*>(&sA[1][o]) = lp;
+            }
+        }
+    }
+    __syncthreads();
+
+    const int ar = lane & 15, kq = 8 * (lane >> 4), m_of = 4 * (lane >> 4);
+    const gptr<uint16_t> wip = G(Wip), wxp = G(Wxp);
+    const int rh = wave & 1, cf = wave >> 1;
+    constexpr int NS1 = D / 32, R1 = NT == 3 ? 8 : NS1, NCH = 2 * DI / CH;  // K steps per chunk, ring slots
+    auto chunk_of = [](int i) { return i < NCH / 2 ? NCH / 2 + i : i - NCH / 2; };  // z chunks first, then x
+    u32x4 r1h[R1], r1l[R1];
+    auto issue_w = [&](int k, int s) {  // block (fragment 4 k + cf, K step s) into slot s % R1
+        const gptr<uint16_t> q = wip + ((int64_t)((CH / 16) * k + cf) * (D / 32) + s) * BLK + lane * 8;
+        r1h[s % R1] = ldg16(q);
+        r1l[s % R1] = r1h[s % R1];
+        if constexpr (NT == 3) r1l[s % R1] = ldg16(q + 512);
+    };
+#pragma unroll
+    for (int s = 0; s < R1; ++s) issue_w(chunk_of(0), s);
+    const int xr = wave & 3, xf = 2 * (wave >> 2);  // x_proj: row fragment, first output fragment
+    floatx4 dacc[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) dacc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const int s1 = p0m3 == 2 ? 0 : p0m3 + 1, s2 = p0m3 == 0 ? 2 : p0m3 - 1;
+
+#pragma unroll 1
+    for (int ci = 0; ci < NCH; ++ci) {
+        const int k = chunk_of(ci);
+        const int kn = chunk_of(ci + 1 < NCH ? ci + 1 : ci);
+        const int cl0 = 16 * cf + m_of;  // first of this lane's 4 columns within the chunk
+        const float4 bias = ldg_f4(G(bin) + CH * k + cl0);
+        floatx4 acc[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < NS1; ++s) {
+            bf16x8 ah[2], al[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int o = ffn5::a_off(32 * rh + 16 * i + ar, 32 * s + kq);
+                ah[i] = *reinterpret_cast<const bf16x8*>(&sA[0][o]);
+                al[i] = *reinterpret_cast<const bf16x8*>(&sA[1][o]);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                acc[i] = mfma_split_step_t<NT>(acc[i], ah[i], al[i], __builtin_bit_cast(bf16x8, r1h[s % R1]),
+                                               __builtin_bit_cast(bf16x8, r1l[s % R1]));
+            if (s + R1 < NS1) issue_w(k, s + R1);  // resolved at compile time
+            else issue_w(kn, s + R1 - NS1);
+            pin_loads();
+        }
+        if (k >= NCH / 2) {
+            // z chunk: straight to HBM (the scan reads it)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                stg_f4(GM(xz) + (m0 + 32 * rh + 16 * i + ar) * (2 * DI) + CH * k + cl0,
+                       make_float4(epi_value<EPI_BIAS>(acc[i][0], bias.x), epi_value<EPI_BIAS>(acc[i][1], bias.y),
+                                   epi_value<EPI_BIAS>(acc[i][2], bias.z), epi_value<EPI_BIAS>(acc[i][3], bias.w)));
+            continue;
+        }
+        // x chunk: fp32 to LDS for the conv over time
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            *reinterpret_cast<float4*>(&sX[sx_off(32 * rh + 16 * i + ar, cl0)]) =
+                make_float4(epi_value<EPI_BIAS>(acc[i][0], bias.x), epi_value<EPI_BIAS>(acc[i][1], bias.y),
+                            epi_value<EPI_BIAS>(acc[i][2], bias.z), epi_value<EPI_BIAS>(acc[i][3], bias.w));
+        __syncthreads();
+        bf16x8 xwh[2][2], xwl[2][2];  // x_proj weight blocks of K block k for this wave's two fragments
+        {
+            const int cl = tid & (CH - 1), g = wave;
+            const int c = CH * k + cl;
+            const float4 cw = ldg_f4(G(conv_w) + 4 * c);
+            const float cb = G(conv_b)[c];
+            const __amdgpu_buffer_rsrc_t hr = buf_rsrc(hist + b * 3 * DI, g == 0 ? 3 * DI * 4 : 0);
+            const float h0 = buf_ld1(hr, (uint32_t)(p0m3 * DI + c) * 4), h1 = buf_ld1(hr, (uint32_t)(s1 * DI + c) * 4),
+                        h2 = buf_ld1(hr, (uint32_t)(s2 * DI + c) * 4);
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const gptr<uint16_t> q = wxp + ((int64_t)(xf + j) * (DI / 32) + 2 * k + s) * BLK + lane * 8;
+                    const u32x4 bh = ldg16(q);
+                    xwh[s][j] = __builtin_bit_cast(bf16x8, bh);
+                    xwl[s][j] = NT == 3 ? __builtin_bit_cast(bf16x8, ldg16(q + 512)) : xwh[s][j];
+                }
+            pin_loads();
+            float xv[11];
+#pragma unroll
+            for (int e = 0; e < 3; ++e) xv[e] = sX[sx_off(g == 0 ? 0 : 8 * g - 3 + e, cl)];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xv[3 + e] = sX[sx_off(8 * g + e, cl)];
+            __syncthreads();
+            if (g == 0) {
+                xv[0] = h0;
+                xv[1] = h1;
+                xv[2] = h2;
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int r = 8 * g + e;
+                const float y = conv_point(cw, cb, xv[e], xv[e + 1], xv[e + 2], xv[e + 3]);
+                GM(xs)[(m0 + r) * DI + c] = y;
+                uint32_t hi, lo;
+                split2(y, hi, lo);
+                sXh[x_off(r, cl)] = (uint16_t)hi;
+                sXl[x_off(r, cl)] = (uint16_t)lo;
+            }
+            // history ring: inputs of positions p0 + 61, 62, 63 in slots (p0 + 64) mod 3, + 1, + 2 (wave 7)
+            const int e0 = (p0m3 + BM) % 3, e1 = (e0 + 1) % 3, e2 = (e0 + 2) % 3;
+            const __amdgpu_buffer_rsrc_t hw = buf_rsrc(hist + b * 3 * DI, g == BM / 8 - 1 ? 3 * DI * 4 : 0);
+            buf_st1(hw, (uint32_t)(e0 * DI + c) * 4, xv[8]);
+            buf_st1(hw, (uint32_t)(e1 * DI + c) * 4, xv[9]);
+            buf_st1(hw, (uint32_t)(e2 * DI + c) * 4, xv[10]);
+        }
+        __syncthreads();
+        // x_proj partial over this chunk's 64 channels (K block k)
+        {
+            floatx4 part[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) part[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                const int o = x_off(16 * xr + ar, 32 * s + kq);
+                const bf16x8 ah = *reinterpret_cast<const bf16x8*>(&sXh[o]);
+                const bf16x8 al = *reinterpret_cast<const bf16x8*>(&sXl[o]);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) part[j] = mfma_split_step<NT>(part[j], ah, al, xwh[s][j], xwl[s][j]);
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) dacc[j] = k == 0 ? part[j] : dacc[j] + part[j];
+        }
+        __syncthreads();  // the next x chunk rewrites sX
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) GM(dbc)[(m0 + 16 * xr + m_of + r) * FW + 16 * (xf + j) + ar] = dacc[j][r];
+}
+
 static int launch_xproj(const float* xs, int64_t M, int di, const uint16_t* Wh, const uint16_t* Wl, float* dbc, int ldd,
                         hipStream_t s) {
     const unsigned grid = (unsigned)((M + 63) / 64);
@@ -2053,7 +2250,24 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc) {
     uint16_t* gl = gh + M * 4 * d;
     int rc = 0;
     float* hist = x->conv_hist + (int64_t)l * x->max_lanes * 3 * di;
-    const bool mix = split && d == mixin::D && di == mixin::DI && R + 2 * NS == mixin::FW && Tc == mixin::BM &&
+    const bool mix5 = split && d == mixin5::D && di == mixin5::DI && R + 2 * NS == mixin5::FW && Tc == mixin5::BM &&
+                      w.in_w.p && w.x_w.p;
+    if (mix5) {
+        // LN1 + in_proj + conv + SiLU + x_proj in one kernel per lane tile, d_model 512
+        const double flops = gemm_flops(M, 2 * di, d) + gemm_flops(M, R + 2 * NS, di) + 8.0 * M * di;
+        const double bytes = 4.0 * M * (d + di + di + R + 2 * NS) + 4.0 * 6 * B * di;
+        if (w.in_w.l)
+            PROF(PC_MIXIN, flops, bytes,
+                 hipLaunchKernelGGL((k_mixin512<3>), dim3((unsigned)B), dim3(512), 0, s, x->x, w.ln1_w, w.ln1_b,
+                                    w.in_w.p, w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs, x->dbc, hist,
+                                    (int)(x->pos % 3)));
+        else
+            PROF(PC_MIXIN, flops, bytes,
+                 hipLaunchKernelGGL((k_mixin512<2>), dim3((unsigned)B), dim3(512), 0, s, x->x, w.ln1_w, w.ln1_b,
+                                    w.in_w.p, w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs, x->dbc, hist,
+                                    (int)(x->pos % 3)));
+    }
+    const bool mix = !mix5 && split && d == mixin::D && di == mixin::DI && R + 2 * NS == mixin::FW && Tc == mixin::BM &&
                      w.in_w.p && w.x_w.p;
     if (mix) {
         // LN1 + in_proj + conv + SiLU + x_proj in one kernel per lane tile
@@ -2067,7 +2281,7 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc) {
             PROF(PC_MIXIN, flops, bytes,
                  hipLaunchKernelGGL((k_mixin<2>), dim3((unsigned)B), dim3(256), 0, s, x->x, w.ln1_w, w.ln1_b, w.in_w.p,
                                     w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs, x->dbc, hist, (int)(x->pos % 3)));
-    } else {
+    } else if (!mix5) {
     // LN1 + in_proj -> xz [M][2di]
     {
         GemmArgs g = gemm_args(x->x, d, w.in_w, w.in_b, x->xz, 2 * di, M, 2 * di, d);
