@@ -1790,6 +1790,13 @@ struct boa_ctx {
     // streamed non-temporally the weights stay in L2 and offsets of 0-450 us measure the same.
     int stagger_us = 0;
     int stagger_classes = 2;
+    // Per-layer decode in two halves of the lanes on two streams (contexts without the fused decode kernel):
+    // one half's state-bound groups (conv + scan) run while the other half's GEMM groups run.  lane0 shifts
+    // the per-lane state of the launches (0 outside the second half).
+    int decode_halves = 2;
+    hipStream_t stream2 = nullptr;
+    std::vector<hipEvent_t> half_ev;   // [2][L]: state group of layer l done, per half; [2L]: stream join
+    int64_t lane0 = 0;
     uint16_t* wfrag = nullptr;         // fragment-packed GEMM weights (fused)
     FusedLayer* d_layers = nullptr;    // per-layer pointer table (fused)
     int64_t device_bytes = 0;
@@ -1950,6 +1957,8 @@ extern "C" int boa_ctx_destroy(boa_ctx* ctx) {
         if (p) (void)hipFree(p);
     for (auto& p : ctx->prof)
         for (hipEvent_t e : p.ev) (void)hipEventDestroy(e);
+    for (hipEvent_t e : ctx->half_ev) (void)hipEventDestroy(e);
+    if (ctx->stream2) (void)hipStreamDestroy(ctx->stream2);
     delete ctx;
     return BOA_OK;
 }
@@ -2167,6 +2176,20 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
         boa_ctx_destroy(x);
         return boa_fail_hip(e, "boa_ctx_create upload", __FILE__, __LINE__);
     }
+    if (const char* v = getenv("BOA_DECODE_HALVES")) x->decode_halves = atoi(v) == 1 ? 1 : 2;
+    if (!x->fused && x->decode_halves == 2) {
+        // default priority (as the context's own stream): streams of different priorities are not mixed
+        e = hipStreamCreateWithFlags(&x->stream2, hipStreamNonBlocking);
+        for (int i = 0; e == hipSuccess && i < 2 * L + 1; ++i) {
+            hipEvent_t ev;
+            e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+            if (e == hipSuccess) x->half_ev.push_back(ev);
+        }
+        if (e != hipSuccess) {
+            boa_ctx_destroy(x);
+            return boa_fail_hip(e, "boa_ctx_create streams", __FILE__, __LINE__);
+        }
+    }
     if (x->device_bytes != ctx_plan_bytes(c, R, precision, max_lanes, tile_len)) {
         const long long got = (long long)x->device_bytes, plan = (long long)ctx_plan_bytes(c, R, precision, max_lanes, tile_len);
         boa_ctx_destroy(x);
@@ -2239,7 +2262,10 @@ static void launch_scan(boa_ctx* x, const LayerW& w, float* ssm, int B, int Tc) 
 //               LN stats -> FF1(LN on load, GELU) into xz -> FF2(+residual) into x
 //   split modes: LN+split -> in_proj -> conv -> x_proj -> scan (y split) -> out_proj -> LN+split ->
 //               FF1(GELU, split output into xz's memory) -> FF2(+residual) into x
-static int run_layer(boa_ctx* x, int l, int B, int Tc) {
+// part selects which of three consecutive groups of the layer to launch (bits, 7 = the whole layer):
+//   1: LN1 + in_proj;  2: conv + x_proj + scan (the state traffic);  4: out_proj + LN2 + feed-forward.
+// The fused compress-tile kernels (k_mixin, k_mixin512) span groups 1 and 2 and need both bits.
+static int run_layer(boa_ctx* x, int l, int B, int Tc, int part = 7) {
     const LayerW& w = x->layers[l];
     const int d = x->d, di = x->di, NS = x->NS, R = x->R;
     const int64_t M = (int64_t)B * Tc;
@@ -2249,8 +2275,9 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc) {
     uint16_t* gh = reinterpret_cast<uint16_t*>(x->xz);
     uint16_t* gl = gh + M * 4 * d;
     int rc = 0;
-    float* hist = x->conv_hist + (int64_t)l * x->max_lanes * 3 * di;
-    const bool mix5 = split && d == mixin5::D && di == mixin5::DI && R + 2 * NS == mixin5::FW && Tc == mixin5::BM &&
+    float* hist = x->conv_hist + ((int64_t)l * x->max_lanes + x->lane0) * 3 * di;
+    const bool both = (part & 3) == 3;
+    const bool mix5 = both && split && d == mixin5::D && di == mixin5::DI && R + 2 * NS == mixin5::FW && Tc == mixin5::BM &&
                       w.in_w.p && w.x_w.p;
     if (mix5) {
         // LN1 + in_proj + conv + SiLU + x_proj in one kernel per lane tile, d_model 512
@@ -2267,7 +2294,7 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc) {
                                     w.in_w.p, w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs, x->dbc, hist,
                                     (int)(x->pos % 3)));
     }
-    const bool mix = !mix5 && split && d == mixin::D && di == mixin::DI && R + 2 * NS == mixin::FW && Tc == mixin::BM &&
+    const bool mix = both && !mix5 && split && d == mixin::D && di == mixin::DI && R + 2 * NS == mixin::FW && Tc == mixin::BM &&
                      w.in_w.p && w.x_w.p;
     if (mix) {
         // LN1 + in_proj + conv + SiLU + x_proj in one kernel per lane tile
@@ -2283,7 +2310,7 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc) {
                                     w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs, x->dbc, hist, (int)(x->pos % 3)));
     } else if (!mix5) {
     // LN1 + in_proj -> xz [M][2di]
-    {
+    if (part & 1) {
         GemmArgs g = gemm_args(x->x, d, w.in_w, w.in_b, x->xz, 2 * di, M, 2 * di, d);
         if (split) {
             launch_ln_split(x, x->x, M, w.ln1_w, w.ln1_b);
@@ -2298,7 +2325,9 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc) {
         }
         if (rc) return rc;
     }
-    if (split && Tc == 1) {
+    if (!(part & 2)) {
+        // group 2 not requested
+    } else if (split && Tc == 1) {
         // decompress step: conv + SiLU + x_proj in one kernel (same arithmetic as the two kernels below)
         const size_t lds = sizeof(float) * 16 * (size_t)(di + 4);
         const double flops = 8.0 * M * di + gemm_flops(M, R + 2 * NS, di);
@@ -2329,8 +2358,8 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc) {
     }
     }
     // dt_proj + softplus + scan + D + gate: y in place of xs (fp32) or split into ah/al
-    {
-        float* ssm = x->ssm + (int64_t)l * x->max_lanes * di * NS;
+    if (part & 2) {
+        float* ssm = x->ssm + ((int64_t)l * x->max_lanes + x->lane0) * di * NS;
         const double flops = (double)M * di * (2.0 * R + 6.0 * NS + 8.0);
         const double bytes = 4.0 * ((double)M * (3.0 * di + R + 2 * NS) + 2.0 * B * di * NS);
         if (R == 16) {
@@ -2341,6 +2370,7 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc) {
             else PROF(PC_SCAN, flops, bytes, (launch_scan<16, 32, false>(x, w, ssm, B, Tc)));
         }
     }
+    if (!(part & 4)) return BOA_OK;
     // out_proj -> mm [M][d]
     {
         GemmArgs g = gemm_args(x->xs, di, w.out_w, w.out_b, x->mm, d, M, d, di);
@@ -2416,15 +2446,12 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc) {
 }
 
 // Full model over B x Tc rows already embedded in ctx->x; logits to `out` (ld V).
-static int run_model(boa_ctx* x, int B, int Tc, float* out) {
+// Head (Linear -> ReLU -> Linear) over B x Tc rows of ctx->x; logits to `out` (ld V).
+static int run_head(boa_ctx* x, int B, int Tc, float* out) {
     const int d = x->d, V = x->V;
     const int64_t M = (int64_t)B * Tc;
     const bool split = x->prec != BOA_PREC_F32;
     int rc = 0;
-    for (int l = 0; l < x->L; ++l) {
-        rc = run_layer(x, l, B, Tc);
-        if (rc) return rc;
-    }
     GemmArgs g1 = gemm_args(x->x, d, x->h1_w, x->h1_b, x->mm, d, M, d, d);
     GemmArgs g2 = gemm_args(x->mm, d, x->h2_w, x->h2_b, out, V, M, V, d);
     if (split) {
@@ -2444,6 +2471,50 @@ static int run_model(boa_ctx* x, int B, int Tc, float* out) {
     BOA_HIP_TRY(hipGetLastError());
     return BOA_OK;
 }
+
+static int run_model(boa_ctx* x, int B, int Tc, float* out) {
+    for (int l = 0; l < x->L; ++l) {
+        const int rc = run_layer(x, l, B, Tc);
+        if (rc) return rc;
+    }
+    return run_head(x, B, Tc, out);
+}
+
+// The context as seen by the launches of one half of the lanes in the two-stream decode: the second half's
+// per-row activations live in the upper half of every workspace buffer (each holds max_rows rows at its
+// widest row length, so any row length fits), its per-lane state starts at lane0, and it runs on stream2.
+// Restores the context on destruction.
+struct LaneView {
+    boa_ctx* x;
+    float *px, *pxz, *pxs, *pdbc, *pmm, *plog;
+    float2* pst;
+    uint16_t *pah, *pal;
+    int64_t pl0;
+    hipStream_t ps;
+    LaneView(boa_ctx* c, int half, int64_t lane0, hipStream_t s)
+        : x(c), px(c->x), pxz(c->xz), pxs(c->xs), pdbc(c->dbc), pmm(c->mm), plog(c->logits), pst(c->stats),
+          pah(c->ah), pal(c->al), pl0(c->lane0), ps(c->stream) {
+        if (half) {
+            const int64_t hr = x->max_rows / 2;
+            const int64_t d = x->d, di = x->di, V = x->V, W = x->R + 2 * x->NS;
+            x->x += hr * d;
+            x->xz += hr * std::max(2 * di, 4 * d);
+            x->xs += hr * di;
+            x->dbc += hr * W;
+            x->mm += hr * d;
+            x->logits += hr * V;
+            x->stats += hr;
+            if (x->ah) x->ah += hr * std::max(d, di);
+            if (x->al) x->al += hr * std::max(d, di);
+        }
+        x->lane0 = lane0;
+        x->stream = s;
+    }
+    ~LaneView() {
+        x->x = px; x->xz = pxz; x->xs = pxs; x->dbc = pdbc; x->mm = pmm; x->logits = plog; x->stats = pst;
+        x->ah = pah; x->al = pal; x->lane0 = pl0; x->stream = ps;
+    }
+};
 
 static unsigned row_blocks(int64_t rows) { return (unsigned)((rows + 3) / 4); }  // 4 waves per 256-thread block
 
@@ -2583,6 +2654,57 @@ extern "C" int boa_decompress(boa_ctx* x, const uint32_t* d_payload, const int64
             if (e != hipSuccess) return boa_fail_hip(e, "k_fused_step", __FILE__, __LINE__);
             x->pos += a.nsteps;
         }
+        BOA_HIP_TRY(hipStreamSynchronize(s));
+        return BOA_OK;
+    }
+    if (x->stream2 && lanes >= 512) {
+        // Two halves of the lanes on two streams.  Per layer and half: LN1 + in_proj, then conv + scan (the
+        // state traffic), then out_proj + feed-forward.  The state groups alternate between the halves (A's
+        // layer l after B's layer l - 1, B's layer l after A's layer l), so one half's HBM-bound scan runs
+        // beside the other half's GEMMs.  Each half's arithmetic is unchanged.  (configs[4], 16384 lanes:
+        // 12.96 ms per step on one stream, 12.14 alternating, 12.34 with the halves left to run freely.)
+        const int L = x->L, la = lanes / 2, lb = lanes - la;
+        hipEvent_t* evA = x->half_ev.data();
+        hipEvent_t* evB = evA + L;
+        hipEvent_t join = evA[2 * L];
+        BOA_HIP_TRY(hipEventRecord(join, s));  // the second stream starts after the decoder initialisation
+        BOA_HIP_TRY(hipStreamWaitEvent(x->stream2, join, 0));
+        for (int t = 1; t < max_len; ++t) {
+            for (int h = 0; h < 2; ++h) {
+                LaneView v(x, h, h ? la : 0, h ? x->stream2 : s);
+                launch_embed_tokens(x, x->tokens + x->lane0, 1, 0, 1, h ? lb : la);
+            }
+            for (int l = 0; l < L; ++l) {
+                for (int h = 0; h < 2; ++h) {
+                    LaneView v(x, h, h ? la : 0, h ? x->stream2 : s);
+                    const int nl = h ? lb : la;
+                    rc = run_layer(x, l, nl, 1, 1);
+                    if (rc) return rc;
+                    hipEvent_t prev = h ? evA[l] : (l > 0 ? evB[l - 1] : (t > 1 ? evB[L - 1] : nullptr));
+                    if (prev) BOA_HIP_TRY(hipStreamWaitEvent(x->stream, prev, 0));
+                    rc = run_layer(x, l, nl, 1, 2);
+                    if (rc) return rc;
+                    BOA_HIP_TRY(hipEventRecord(h ? evB[l] : evA[l], x->stream));
+                    rc = run_layer(x, l, nl, 1, 4);
+                    if (rc) return rc;
+                }
+            }
+            for (int h = 0; h < 2; ++h) {
+                LaneView v(x, h, h ? la : 0, h ? x->stream2 : s);
+                const int nl = h ? lb : la;
+                const int64_t b0 = x->lane0;
+                rc = run_head(x, nl, 1, x->logits);
+                if (rc) return rc;
+                PROF(PC_DECODE, 0.0, 4.0 * nl * x->V + (double)nl,
+                     hipLaunchKernelGGL(k_decode_step, dim3(nl), dim3(64), 0, x->stream, x->logits, x->V, t,
+                                        d_lens + b0, x->dec + b0, d_payload, d_word_off + b0, d_nwords + b0,
+                                        x->tokens + b0, d_out + b0 * out_stride, out_stride));
+            }
+            x->pos += 1;
+        }
+        BOA_HIP_TRY(hipGetLastError());
+        BOA_HIP_TRY(hipEventRecord(join, x->stream2));  // the context's stream joins the second
+        BOA_HIP_TRY(hipStreamWaitEvent(s, join, 0));
         BOA_HIP_TRY(hipStreamSynchronize(s));
         return BOA_OK;
     }

@@ -205,3 +205,27 @@ def test_compressed_size_vs_oracle_config2(gpu, ora):
     assert abs(gpu_words - ref_words) <= 0.005 * ref_words
     out = codec.decompress_payload(m, payload, nw, Ls, fb)
     assert np.array_equal(out, data)
+
+
+def test_layer_decode_in_two_halves(gpu):
+    """Per-layer decode of a wave large enough (>= 512 lanes) to run as two halves of the lanes on two streams,
+    their state groups alternating: the same bytes as one stream and as the fused decode kernel."""
+    import codec
+
+    m, _ = _model(2)
+    rng = np.random.default_rng(7)
+    lens = [int(v) for v in rng.integers(1, 40, 600)]
+    chunks = [_markov(L, seed=100 + i) for i, L in enumerate(lens)]
+    payload, nw, fb, Ls = codec.compress_payload(m, chunks)
+    for fused, halves in (("0", "2"), ("0", "1"), ("1", "2")):
+        os.environ["BOA_FUSED_STEP"] = fused
+        os.environ["BOA_DECODE_HALVES"] = halves
+        try:
+            m.release_engines()
+            out = codec.decompress_payload(m, payload, nw, Ls, fb)
+        finally:
+            del os.environ["BOA_FUSED_STEP"]
+            del os.environ["BOA_DECODE_HALVES"]
+        for i, c in enumerate(chunks):
+            assert (out[i, :lens[i]] == c).all(), (fused, halves, i)
+    m.release_engines()
