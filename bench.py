@@ -414,8 +414,9 @@ def main():
     ap.add_argument("--tile-len", type=int, default=int(os.environ.get("BOA_TILE_LEN", "64")))
     ap.add_argument("--cpu-steps", type=int, default=300, help="coded positions per chunk in the CPU sample")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--workload", choices=["codec", "coder"], default="codec",
-                    help="codec: configs[2]+[3] (the metric); coder: configs[1], the range coder alone")
+    ap.add_argument("--workload", choices=["codec", "coder", "config4"], default="codec",
+                    help="codec: configs[2]+[3] (the metric); coder: configs[1], the range coder alone; config4: "
+                         "configs[4] alone (the bounded run the default line carries as its config4 extra)")
     ap.add_argument("--coder-streams", type=int, default=16384)
     ap.add_argument("--coder-len", type=int, default=4096)
     ap.add_argument("--coder-cpu-streams", type=int, default=64)
@@ -450,6 +451,10 @@ def main():
         return
     if args.workload == "coder":
         print(json.dumps(coder_bench(args, args.steps, args.warmup, args.coder_cpu_streams)))
+        return
+    if args.workload == "config4":
+        print(json.dumps({"metric": "configs[4] input MB/s compress, decompress, d512x16L bf16 weights, 1 GPU",
+                          **config4_extra(N.lib(), args.c4_lanes, args.c4_len)}))
         return
     lib = N.lib()
     dev = torch.device("cuda")
