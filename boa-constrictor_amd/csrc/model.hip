@@ -916,11 +916,18 @@ __device__ __forceinline__ int a_off(int r, int k) { return r * D + (((k >> 3) ^
 __device__ __forceinline__ int h_off(int r, int k) { return r * HC + (((k >> 3) ^ (r >> 1)) & 7) * 8 + (k & 7); }
 }  // namespace ffn5
 
-template <int NT>
+// OUTP: the out_proj GEMM runs first, inside this kernel (decode step and compress tiles at d_model 512): mm =
+// y . W_out^T + b_out from the scan's split output y [rows][1024] (hi, lo), read in two K chunks of 512 staged
+// through the LDS operand buffer, each output accumulating its 32 K steps in ascending order through
+// mfma_split_step (as the out_proj GEMM does); mm then stays on chip (fp32 in the operand buffer) for LN2.
+// Wave w owns out_proj outputs 64 w .. + 63 of all 64 rows; its W_out blocks stream through an 8-slot ring.
+template <int NT, bool OUTP>
 __global__ void __launch_bounds__(512, 2) k_ffn512(const float* __restrict__ mm, const float* __restrict__ ln_w,
                                                    const float* __restrict__ ln_b, const uint16_t* __restrict__ W1p,
                                                    const float* __restrict__ b1, const uint16_t* __restrict__ W2p,
-                                                   const float* __restrict__ b2, float* __restrict__ x, int64_t M) {
+                                                   const float* __restrict__ b2, float* __restrict__ x, int64_t M,
+                                                   const uint16_t* __restrict__ yh, const uint16_t* __restrict__ yl,
+                                                   const uint16_t* __restrict__ Wop, const float* __restrict__ bo) {
     using namespace ffn5;
     __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * D];
     __shared__ __attribute__((aligned(16))) uint16_t sH[2][BM * HC];
@@ -928,13 +935,110 @@ __global__ void __launch_bounds__(512, 2) k_ffn512(const float* __restrict__ mm,
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int64_t m0 = (int64_t)blockIdx.x * BM;
     const int rows = (int)((M - m0) < BM ? (M - m0) : BM);
-    {
+    const float4 w0 = ldg_f4(G(ln_w) + 4 * lane), w1 = ldg_f4(G(ln_w) + 256 + 4 * lane);
+    const float4 c0 = ldg_f4(G(ln_b) + 4 * lane), c1 = ldg_f4(G(ln_b) + 256 + 4 * lane);
+    const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    const float bv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+    // LN2 of one row held by one wave (lane j: elements 4j.. and 256 + 4j..) into the split operand
+    auto ln2_store = [&](int r, const float (&v)[8]) {
+        float mu, rs;
+        ln_stats_row<2>(v, mu, rs);
+        float y[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) y[i] = ln_apply(v[i], mu, rs, wv[i], bv[i]);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            uint2 hp, lp;
+            split4(y[4 * h], y[4 * h + 1], y[4 * h + 2], y[4 * h + 3], hp, lp);
+            const int o = a_off(r, 256 * h + 4 * lane);
+            *reinterpret_cast<uint2*>(&sA[0][o]) = hp;
+            *reinterpret_cast<uint2*>(&sA[1][o]) = lp;
+        }
+    };
+    if constexpr (OUTP) {
+        constexpr int KO = 2 * D, KC = D, NKS = KO / 32, BLKO = (NT == 3) ? 1024 : 512, RO = 8;
+        const int ar = lane & 15, kq = 8 * (lane >> 4), m_of = 4 * (lane >> 4);
+        const gptr<uint16_t> wop = G(Wop);
+        u32x4 oh[RO], ol[RO];
+        // block i (W_out fragment 4 wave + i % 4, K step i / 4) into ring slot u (= i % RO, passed as a constant)
+        auto issue_o = [&](int u, int i) {
+            const gptr<uint16_t> q = wop + ((int64_t)(4 * wave + (i & 3)) * NKS + (i >> 2)) * BLKO + lane * 8;
+            oh[u] = ldg16(q);
+            ol[u] = oh[u];
+            if constexpr (NT == 3) ol[u] = ldg16(q + 512);
+        };
+#pragma unroll
+        for (int i = 0; i < RO; ++i) issue_o(i, i);
+        floatx4 macc[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) macc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        // y rows past M read 0 (buffer range check)
+        const __amdgpu_buffer_rsrc_t ryh = buf_rsrc(yh + m0 * KO, (uint32_t)rows * KO * 2);
+        const __amdgpu_buffer_rsrc_t ryl = buf_rsrc(yl + m0 * KO, (uint32_t)rows * KO * 2);
+#pragma unroll 1
+        for (int q = 0; q < KO / KC; ++q) {
+            // stage y[:, 512 q .. + 511] (hi, lo): 8 x 16 B per array per thread
+#pragma unroll
+            for (int e = 0; e < (BM * KC / 8) / 512; ++e) {
+                const int idx = e * 512 + tid, r = idx / (KC / 8), k = (idx % (KC / 8)) * 8;
+                const uint32_t off = (uint32_t)((r * KO + KC * q + k) * 2);
+                *reinterpret_cast<u32x4*>(&sA[0][a_off(r, k)]) = buf_ld16(ryh, off);
+                *reinterpret_cast<u32x4*>(&sA[1][a_off(r, k)]) = buf_ld16(ryl, off);
+            }
+            __syncthreads();
+#pragma unroll 2
+            for (int s = 0; s < KC / 32; ++s) {
+                bf16x8 ah[4], al[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int o = a_off(16 * i + ar, 32 * s + kq);
+                    ah[i] = *reinterpret_cast<const bf16x8*>(&sA[0][o]);
+                    al[i] = *reinterpret_cast<const bf16x8*>(&sA[1][o]);
+                }
+                const int sg = (KC / 32) * q + s;  // K step over the whole K
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int bi = 4 * sg + j, u = (4 * s + j) % RO;  // 4 sg = 64 q + 4 s: same slot as bi % RO
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        macc[i][j] = mfma_split_step<NT>(macc[i][j], ah[i], al[i], __builtin_bit_cast(bf16x8, oh[u]),
+                                                         __builtin_bit_cast(bf16x8, ol[u]));
+                    if (bi + RO < 4 * NKS) issue_o(u, bi + RO);
+                    pin_loads();
+                }
+            }
+            __syncthreads();  // the next chunk (or mm) rewrites the operand buffer
+        }
+        // mm (+ bias) as fp32 rows of 512 in the operand buffer
+        float* sM = reinterpret_cast<float*>(&sA[0][0]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int col = 16 * (4 * wave + j) + ar;
+            const float bias = G(bo)[col];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sM[(16 * i + m_of + r) * D + col] = epi_value<EPI_BIAS>(macc[i][j][r], bias);
+        }
+        __syncthreads();
+        // LN2 of this wave's 8 rows: all read before any split is written over the fp32 rows
+        float v[8][8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int r = 8 * wave + q;
+            const float4 u0 = *reinterpret_cast<const float4*>(&sM[r * D + 4 * lane]);
+            const float4 u1 = *reinterpret_cast<const float4*>(&sM[r * D + 256 + 4 * lane]);
+            v[q][0] = u0.x; v[q][1] = u0.y; v[q][2] = u0.z; v[q][3] = u0.w;
+            v[q][4] = u1.x; v[q][5] = u1.y; v[q][6] = u1.z; v[q][7] = u1.w;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < 8; ++q) ln2_store(8 * wave + q, v[q]);
+    } else {
         // LN2 of 8 rows per wave; rows past M read 0 (buffer range check) and are never stored
         const __amdgpu_buffer_rsrc_t rm = buf_rsrc(mm + m0 * D, (uint32_t)rows * D * 4);
-        const float4 w0 = ldg_f4(G(ln_w) + 4 * lane), w1 = ldg_f4(G(ln_w) + 256 + 4 * lane);
-        const float4 c0 = ldg_f4(G(ln_b) + 4 * lane), c1 = ldg_f4(G(ln_b) + 256 + 4 * lane);
-        const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-        const float bv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
 #pragma unroll 2
         for (int q = 0; q < BM / 8; ++q) {
             const int r = 8 * wave + q;
@@ -942,19 +1046,7 @@ __global__ void __launch_bounds__(512, 2) k_ffn512(const float* __restrict__ mm,
             const u32x4 u1 = buf_ld16(rm, (uint32_t)((r * D + 256 + 4 * lane) * 4));
             const float v[8] = {__uint_as_float(u0.x), __uint_as_float(u0.y), __uint_as_float(u0.z), __uint_as_float(u0.w),
                                 __uint_as_float(u1.x), __uint_as_float(u1.y), __uint_as_float(u1.z), __uint_as_float(u1.w)};
-            float mu, rs;
-            ln_stats_row<2>(v, mu, rs);
-            float y[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) y[i] = ln_apply(v[i], mu, rs, wv[i], bv[i]);
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                uint2 hp, lp;
-                split4(y[4 * h], y[4 * h + 1], y[4 * h + 2], y[4 * h + 3], hp, lp);
-                const int o = a_off(r, 256 * h + 4 * lane);
-                *reinterpret_cast<uint2*>(&sA[0][o]) = hp;
-                *reinterpret_cast<uint2*>(&sA[1][o]) = lp;
-            }
+            ln2_store(r, v);
         }
     }
     __syncthreads();
@@ -1794,6 +1886,7 @@ struct boa_ctx {
     // one half's state-bound groups (conv + scan) run while the other half's GEMM groups run.  lane0 shifts
     // the per-lane state of the launches (0 outside the second half).
     int decode_halves = 2;
+    bool ffn_outp = true;  // d_model 512: out_proj inside the feed-forward kernel (BOA_FFN_OUTP=0: separate GEMM)
     hipStream_t stream2 = nullptr;
     std::vector<hipEvent_t> half_ev;   // [2][L]: state group of layer l done, per half; [2L]: stream join
     int64_t lane0 = 0;
@@ -2177,6 +2270,7 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
         return boa_fail_hip(e, "boa_ctx_create upload", __FILE__, __LINE__);
     }
     if (const char* v = getenv("BOA_DECODE_HALVES")) x->decode_halves = atoi(v) == 1 ? 1 : 2;
+    if (const char* v = getenv("BOA_FFN_OUTP")) x->ffn_outp = atoi(v) != 0;
     if (!x->fused && x->decode_halves == 2) {
         // default priority (as the context's own stream): streams of different priorities are not mixed
         e = hipStreamCreateWithFlags(&x->stream2, hipStreamNonBlocking);
@@ -2371,6 +2465,23 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc, int part = 7) {
         }
     }
     if (!(part & 4)) return BOA_OK;
+    const bool ffn512 = split && d == ffn5::D && 4 * d == ffn5::DF && w.ff1_w.p && w.ff2_w.p;
+    if (ffn512 && x->ffn_outp && w.out_w.p) {
+        // out_proj + LN2 + FF1 + GELU + FF2 + residual in one kernel, d_model 512 (mm and the hidden layer kept
+        // on chip)
+        const double flops = gemm_flops(M, d, di) + gemm_flops(M, 4 * d, d) + gemm_flops(M, d, 4 * d);
+        const double bytes = 4.0 * M * di + 4.0 * M * d * 2 + 2.0 * (w.ff1_w.l ? 2 : 1) * (2.0 * 4 * d * d + d * di);
+        const unsigned grid = (unsigned)((M + ffn5::BM - 1) / ffn5::BM);
+        if (w.ff1_w.l)
+            PROF(PC_FFN, flops, bytes,
+                 hipLaunchKernelGGL((k_ffn512<3, true>), dim3(grid), dim3(512), 0, s, nullptr, w.ln2_w, w.ln2_b,
+                                    w.ff1_w.p, w.ff1_b, w.ff2_w.p, w.ff2_b, x->x, M, x->ah, x->al, w.out_w.p, w.out_b));
+        else
+            PROF(PC_FFN, flops, bytes,
+                 hipLaunchKernelGGL((k_ffn512<2, true>), dim3(grid), dim3(512), 0, s, nullptr, w.ln2_w, w.ln2_b,
+                                    w.ff1_w.p, w.ff1_b, w.ff2_w.p, w.ff2_b, x->x, M, x->ah, x->al, w.out_w.p, w.out_b));
+        return BOA_OK;
+    }
     // out_proj -> mm [M][d]
     {
         GemmArgs g = gemm_args(x->xs, di, w.out_w, w.out_b, x->mm, d, M, d, di);
@@ -2382,19 +2493,19 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc, int part = 7) {
         }
         if (rc) return rc;
     }
-    if (split && d == ffn5::D && 4 * d == ffn5::DF && w.ff1_w.p && w.ff2_w.p) {
+    if (ffn512) {
         // LN2 + FF1 + GELU + FF2 + residual in one kernel, d_model 512 (hidden layer kept on chip)
         const double flops = gemm_flops(M, 4 * d, d) + gemm_flops(M, d, 4 * d);
         const double bytes = 4.0 * M * d * 3 + 2.0 * (w.ff1_w.l ? 2 : 1) * (2.0 * 4 * d * d);
         const unsigned grid = (unsigned)((M + ffn5::BM - 1) / ffn5::BM);
         if (w.ff1_w.l)
             PROF(PC_FFN, flops, bytes,
-                 hipLaunchKernelGGL((k_ffn512<3>), dim3(grid), dim3(512), 0, s, x->mm, w.ln2_w, w.ln2_b, w.ff1_w.p,
-                                    w.ff1_b, w.ff2_w.p, w.ff2_b, x->x, M));
+                 hipLaunchKernelGGL((k_ffn512<3, false>), dim3(grid), dim3(512), 0, s, x->mm, w.ln2_w, w.ln2_b,
+                                    w.ff1_w.p, w.ff1_b, w.ff2_w.p, w.ff2_b, x->x, M, nullptr, nullptr, nullptr, nullptr));
         else
             PROF(PC_FFN, flops, bytes,
-                 hipLaunchKernelGGL((k_ffn512<2>), dim3(grid), dim3(512), 0, s, x->mm, w.ln2_w, w.ln2_b, w.ff1_w.p,
-                                    w.ff1_b, w.ff2_w.p, w.ff2_b, x->x, M));
+                 hipLaunchKernelGGL((k_ffn512<2, false>), dim3(grid), dim3(512), 0, s, x->mm, w.ln2_w, w.ln2_b,
+                                    w.ff1_w.p, w.ff1_b, w.ff2_w.p, w.ff2_b, x->x, M, nullptr, nullptr, nullptr, nullptr));
         return BOA_OK;
     }
     if (split && d == ffn::D && 4 * d == ffn::DF && w.ff1_w.p && w.ff2_w.p) {
