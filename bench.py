@@ -54,6 +54,8 @@ KERNEL_NAMES = {
     ("compress", "gemm_x_proj"): "k_xproj<3, 3>",
     ("compress", "scan"): "k_scan<16, 16, true>",
     ("compress", "conv"): "k_conv_silu",
+    ("compress", "head_xq"): "k_head_xq<3, 256>",
+    ("compress", "encode"): "k_encode_lf",
     ("decompress", "fused_step"): "k_fused_step<3, 512>",
 }
 

@@ -1750,6 +1750,215 @@ __global__ void __launch_bounds__(64) k_encode_tile(const float* __restrict__ lo
     if (lane == 0) states[b] = st;
 }
 
+// ================================================================================================
+// Head + quantiser of a compress tile, fused: for the Tc = 64 positions of one chunk lane,
+//   logits = W2 . ReLU(W1 . x + b1) + b2            (model.py:95,101: Linear -> ReLU -> Linear)
+// then the fused quantiser (XQ) of each position's logits row and the coder interval [lo, lo + width) of the
+// byte that position predicts (codec.py:56-76: step(byte t-1) -> probabilities of byte t), written as one
+// (lo, width) pair per position for k_encode_lf, which runs the sequential range coder.  The reference does
+// head, quantised table and encode per time step from logits in HBM (range_coder_kernels.cu:612-748,
+// ker_rc_encode_chunk_parallel_warp); here the logits never leave the chip.
+// The arithmetic of every value is that of the tiled head GEMMs and of the fused decode kernel: x split by
+// split4; head1 outputs accumulate their D/32 K steps in ascending order (mfma_split_step_t: the same value as
+// mfma_split_step), then epi_value<RELU>, split; head2 outputs accumulate all D/32 K steps in ascending order
+// (64-unit chunks of the hidden layer, in order), then epi_value<BIAS>.  The logits, and so the tables, equal
+// the decoder's bit for bit.
+// 512 threads (8 waves).  Per 64-unit chunk c of the hidden layer: head1 wave tile 32 rows x 16 units (the W1
+// block as the A operand, a lane's 4 outputs are consecutive units: one 8-byte store per part), then head2
+// accumulates the chunk: wave w owns logits 32 w .. + 31 (2 fragments) of all 64 rows.  A wave's weight blocks
+// (D/32 of W1, then 4 of W2 per chunk) stream through one 4-slot register ring in use order, as in k_ffn.
+// LDS: x operand [64][D] (hi, lo) + hidden chunk [64][64] (hi, lo); the logits [64][260] fp32 reuse it.
+// D = 256: 80 KB, two workgroups per CU; D = 512: 144 KB, one.
+namespace headq {
+constexpr int BM = 64, V = 256, HC = 64, LLOG = V + 4;
+constexpr uint32_t SKIP = 0xFFFFFFFFu;  // no symbol at this position (past the chunk's end, or byte >= V)
+// 16-byte chunks XOR-swizzled by row (low 4 bits of the chunk index), so 16-row fragment reads spread over banks
+template <int D> __device__ __forceinline__ int a_off(int r, int k) { return r * D + (((k >> 3) ^ (r & 15)) << 3) + (k & 7); }
+__device__ __forceinline__ int h_off(int r, int k) { return r * HC + (((k >> 3) ^ (r >> 1)) & 7) * 8 + (k & 7); }
+template <int D> constexpr int lds_bytes() {
+    return (2 * BM * D * 2 + 2 * BM * HC * 2) > BM * LLOG * 4 ? (2 * BM * D * 2 + 2 * BM * HC * 2) : BM * LLOG * 4;
+}
+}  // namespace headq
+
+template <int NT, int D>
+__global__ void __launch_bounds__(512, (D == 256) ? 4 : 2) k_head_xq(const float* __restrict__ xin,
+                                                                   const uint16_t* __restrict__ W1p,
+                                                                   const float* __restrict__ b1,
+                                                                   const uint16_t* __restrict__ W2p,
+                                                                   const float* __restrict__ b2, int t0,
+                                                                   const uint8_t* __restrict__ bytes, int64_t stride,
+                                                                   const int32_t* __restrict__ lens,
+                                                                   uint2* __restrict__ lf) {
+    using namespace headq;
+    __shared__ __attribute__((aligned(16))) unsigned char lds[lds_bytes<D>()];
+    uint16_t* sAh = reinterpret_cast<uint16_t*>(lds);
+    uint16_t* sAl = sAh + BM * D;
+    uint16_t* sHh = sAl + BM * D;
+    uint16_t* sHl = sHh + BM * HC;
+    float* sLog = reinterpret_cast<float*>(lds);  // after the last chunk
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t b = blockIdx.x;
+    {
+        const gptr<float> xr = G(xin) + b * BM * D;
+#pragma unroll 4
+        for (int q = 0; q < BM / 8; ++q) {
+            const int r = 8 * wave + q;
+#pragma unroll
+            for (int h = 0; h < D / 256; ++h) {
+                const float4 v = ldg_f4(xr + r * D + 256 * h + 4 * lane);
+                uint2 hp, lp;
+                split4(v.x, v.y, v.z, v.w, hp, lp);
+                const int o = a_off<D>(r, 256 * h + 4 * lane);
+                *reinterpret_cast<uint2*>(sAh + o) = hp;
+                *reinterpret_cast<uint2*>(sAl + o) = lp;
+            }
+        }
+    }
+    const int ar = lane & 15, m_of = 4 * (lane >> 4);
+    __syncthreads();
+    constexpr int BLK = (NT == 3) ? 1024 : 512;
+    const gptr<uint16_t> w1p = G(W1p), w2p = G(W2p);
+    const int rh = wave & 1, cf = wave >> 1;
+    constexpr int KS = D / 32, NBC = KS + 4, R = 4, NC = D / HC;
+    static_assert(NBC % R == 0 && KS % R == 0, "ring slots divide the blocks of a chunk");
+    u32x4 rhh[R], rll[R];
+    auto issue = [&](int c, int i) {
+        const int64_t blk = i < KS ? (int64_t)(4 * c + cf) * KS + i
+                                   : (int64_t)(2 * wave + ((i - KS) & 1)) * KS + 2 * c + ((i - KS) >> 1);
+        const gptr<uint16_t> q = (i < KS ? w1p : w2p) + blk * BLK + lane * 8;
+        rhh[i % R] = ldg16(q);
+        rll[i % R] = rhh[i % R];
+        if constexpr (NT == 3) rll[i % R] = ldg16(q + 512);
+    };
+    auto refill = [&](int c, int cn, int i) {
+        if (i + R < NBC) issue(c, i + R);
+        else issue(cn, i + R - NBC);
+    };
+    floatx4 out[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) out[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < R; ++i) issue(0, i);
+#pragma unroll 1
+    for (int c = 0; c < NC; ++c) {
+        const int cn = c + 1 < NC ? c + 1 : c;
+        const float4 bias = ldg_f4(G(b1) + HC * c + 16 * cf + m_of);
+        floatx4 hacc[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) hacc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+        // LDS addresses are formed per chunk from an opaque copy of the lane index: hoisted out of the chunk
+        // loop they would hold a dozen registers, which spill (and every reload waits behind the weight ring)
+        int lq = lane;
+        __asm__ volatile("" : "+v"(lq));
+        const int arq = lq & 15, kqq = 8 * (lq >> 4);
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            bf16x8 ah[2], al[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int o = a_off<D>(32 * rh + 16 * i + arq, 32 * s + kqq);
+                ah[i] = *reinterpret_cast<const bf16x8*>(sAh + o);
+                al[i] = *reinterpret_cast<const bf16x8*>(sAl + o);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                hacc[i] = mfma_split_step_t<NT>(hacc[i], ah[i], al[i], __builtin_bit_cast(bf16x8, rhh[s % R]),
+                                                __builtin_bit_cast(bf16x8, rll[s % R]));
+            refill(c, cn, s);
+            pin_loads();
+        }
+        {
+            const float bv[4] = {bias.x, bias.y, bias.z, bias.w};
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                float g[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) g[r] = epi_value<EPI_RELU>(hacc[i][r], bv[r]);
+                uint2 hp, lp;
+                split4(g[0], g[1], g[2], g[3], hp, lp);
+                const int o = h_off(32 * rh + 16 * i + ar, 16 * cf + m_of);
+                *reinterpret_cast<uint2*>(sHh + o) = hp;
+                *reinterpret_cast<uint2*>(sHl + o) = lp;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            bf16x8 ah[4], al[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int o = h_off(16 * i + arq, 32 * t + kqq);
+                ah[i] = *reinterpret_cast<const bf16x8*>(sHh + o);
+                al[i] = *reinterpret_cast<const bf16x8*>(sHl + o);
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int bi = KS + 2 * t + j;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    out[i][j] = mfma_split_step<NT>(out[i][j], ah[i], al[i], __builtin_bit_cast(bf16x8, rhh[bi % R]),
+                                                    __builtin_bit_cast(bf16x8, rll[bi % R]));
+                refill(c, cn, bi);
+                pin_loads();
+            }
+        }
+        __syncthreads();
+    }
+    // the operand and hidden buffers are dead (the last chunk ended with a barrier): logits in their place
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int col = 16 * (2 * wave + j) + ar;
+        const float bias = G(b2)[col];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sLog[(16 * i + m_of + r) * LLOG + col] = epi_value<EPI_BIAS>(out[i][j][r], bias);
+    }
+    __syncthreads();
+    // quantiser and coder interval per position: wave w takes positions 8 w .. 8 w + 7 (uniform per wave)
+    const int L = lens[b];
+    const uint8_t* src = bytes + b * stride;
+#pragma unroll 1
+    for (int q = 0; q < BM / 8; ++q) {
+        const int t = 8 * wave + q;
+        const int p = t0 + t;
+        uint2 v = make_uint2(SKIP, 0u);
+        if (p + 1 < L) {
+            const int s = src[p + 1];
+            if (s < V) {
+                XQ xq;
+                xq_build(xq, logits_row4(sLog + t * LLOG, V, lane), lane, V, CODER_P);
+                uint32_t c_s, f_s;
+                xq_sym(xq, s, c_s, f_s);
+                const uint32_t lo = xq_cdf_at(xq, c_s, s);
+                const uint32_t hi = (s + 1 < V) ? xq_cdf_at(xq, c_s + f_s, s + 1) : (1u << CODER_P);
+                v = make_uint2(lo, hi - lo);
+            }
+        }
+        if (lane == 0) lf[b * BM + t] = v;
+    }
+}
+
+// The sequential coder over one tile's (lo, width) pairs (k_head_xq), one thread per chunk lane.
+__global__ void __launch_bounds__(256) k_encode_lf(const uint2* __restrict__ lf, int Tc, int n,
+                                                  EncState* __restrict__ states, uint32_t* __restrict__ words,
+                                                  int64_t pitch) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= n) return;
+    EncState st = states[b];
+    const WordSink sink{words + b * pitch, pitch, true};
+    const uint2* q = lf + b * Tc;
+    for (int t = 0; t < Tc; ++t) {
+        const uint2 v = q[t];
+        if (v.x == headq::SKIP) continue;
+        enc_push(st, CODER_P, v.x, v.y, sink);
+    }
+    states[b] = st;
+}
+
 __global__ void k_enc_finish(EncState* states, uint32_t* words, int64_t pitch, int32_t* nwords, int32_t* overflow,
                              int n) {
     const int b = blockIdx.x * blockDim.x + threadIdx.x;
@@ -1839,12 +2048,12 @@ static GemmArgs gemm_args(const float* A, int64_t lda, const MatW& W, const floa
 // Per-kernel-class event timing (boa_profile / boa_profile_read).
 enum ProfClass {
     PC_EMBED, PC_IN, PC_CONV, PC_XPROJ, PC_SCAN, PC_OUT, PC_FF1, PC_FF2, PC_HEAD1, PC_HEAD2, PC_ENCODE, PC_DECODE,
-    PC_LN, PC_FUSED, PC_FFN, PC_MIXIN, PC_COUNT
+    PC_LN, PC_FUSED, PC_FFN, PC_MIXIN, PC_HEADXQ, PC_COUNT
 };
 static const char* kProfNames[PC_COUNT] = {"embed",    "gemm_in_proj", "conv",     "gemm_x_proj",
                                            "scan",     "gemm_out_proj", "gemm_ff1", "gemm_ff2",
                                            "gemm_head1", "gemm_head2", "encode",   "decode",
-                                           "ln_stats", "fused_step", "ffn", "mixin"};
+                                           "ln_stats", "fused_step", "ffn", "mixin", "head_xq"};
 struct ProfClassState {
     int64_t launches = 0;
     int64_t used = 0;
@@ -1887,6 +2096,7 @@ struct boa_ctx {
     // the per-lane state of the launches (0 outside the second half).
     int decode_halves = 2;
     bool ffn_outp = true;  // d_model 512: out_proj inside the feed-forward kernel (BOA_FFN_OUTP=0: separate GEMM)
+    bool head_xq = true;   // compress tiles: head + quantiser in one kernel (BOA_HEAD_XQ=0: head GEMMs + k_encode_tile)
     hipStream_t stream2 = nullptr;
     std::vector<hipEvent_t> half_ev;   // [2][L]: state group of layer l done, per half; [2L]: stream join
     int64_t lane0 = 0;
@@ -2271,6 +2481,7 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
     }
     if (const char* v = getenv("BOA_DECODE_HALVES")) x->decode_halves = atoi(v) == 1 ? 1 : 2;
     if (const char* v = getenv("BOA_FFN_OUTP")) x->ffn_outp = atoi(v) != 0;
+    if (const char* v = getenv("BOA_HEAD_XQ")) x->head_xq = atoi(v) != 0;
     if (!x->fused && x->decode_halves == 2) {
         // default priority (as the context's own stream): streams of different priorities are not mixed
         e = hipStreamCreateWithFlags(&x->stream2, hipStreamNonBlocking);
@@ -2706,6 +2917,35 @@ extern "C" int boa_model_forward(boa_ctx* x, const int32_t* d_tokens, int64_t to
     return BOA_OK;
 }
 
+// The fused head + quantiser kernel covers full tiles of 64 positions, vocab 256, d_model 256 or 512, in the
+// split modes (fragment-packed head weights); other tiles take the head GEMMs and k_encode_tile (same values).
+static bool head_xq_ok(const boa_ctx* x, int Tc) {
+    return x->head_xq && x->prec != BOA_PREC_F32 && Tc == headq::BM && x->V == headq::V && (x->d == 256 || x->d == 512) &&
+           x->h1_w.p && x->h2_w.p;
+}
+
+static int launch_head_xq(boa_ctx* x, int lanes, int t0, const uint8_t* bytes, int64_t stride, const int32_t* lens,
+                          uint2* lf) {
+    const int d = x->d, V = x->V;
+    const int64_t M = (int64_t)lanes * headq::BM;
+    const double flops = gemm_flops(M, d, d) + gemm_flops(M, V, d);
+    const double bytes_ = 4.0 * M * d + 8.0 * M + (double)M + 2.0 * (x->h1_w.l ? 2 : 1) * (double)(x->h1_w.n + x->h2_w.n);
+    const bool three = x->h1_w.l != nullptr;
+    hipStream_t s = x->stream;
+#define HXQ(NT, D)                                                                                                  \
+    PROF(PC_HEADXQ, flops, bytes_,                                                                                  \
+         hipLaunchKernelGGL((k_head_xq<NT, D>), dim3((unsigned)lanes), dim3(512), 0, s, x->x, x->h1_w.p, x->h1_b,    \
+                            x->h2_w.p, x->h2_b, t0, bytes, stride, lens, lf))
+    if (d == 256) {
+        if (three) HXQ(3, 256); else HXQ(2, 256);
+    } else {
+        if (three) HXQ(3, 512); else HXQ(2, 512);
+    }
+#undef HXQ
+    BOA_HIP_TRY(hipGetLastError());
+    return BOA_OK;
+}
+
 extern "C" int boa_compress(boa_ctx* x, const uint8_t* d_bytes, int64_t byte_stride, const int32_t* d_lens,
                             int32_t lanes, int32_t max_len, uint32_t* d_words, int64_t pitch_words, int32_t* d_nwords) {
     if (!x || !d_bytes || !d_lens || !d_words || !d_nwords || lanes < 1 || lanes > x->max_lanes || max_len < 1 ||
@@ -2723,6 +2963,19 @@ extern "C" int boa_compress(boa_ctx* x, const uint8_t* d_bytes, int64_t byte_str
         PROF(PC_EMBED, 0.0, 4.0 * rows * x->d,
              hipLaunchKernelGGL(k_embed_bytes, dim3(row_blocks(rows)), dim3(256), 0, s, d_bytes, byte_stride, d_lens,
                                 t0, Tc, rows, x->emb, x->d, x->V, x->x));
+        if (head_xq_ok(x, Tc)) {
+            // layers, then head + quantiser in one kernel (logits on chip) and the sequential coder
+            for (int l = 0; l < x->L && !rc; ++l) rc = run_layer(x, l, lanes, Tc);
+            x->pos += Tc;
+            if (rc) return rc;
+            uint2* lf = reinterpret_cast<uint2*>(x->logits);  // (lo, width) per position: 8 of the row's V * 4 bytes
+            rc = launch_head_xq(x, lanes, t0, d_bytes, byte_stride, d_lens, lf);
+            if (rc) return rc;
+            PROF(PC_ENCODE, 0.0, 8.0 * rows + 32.0 * lanes,
+                 hipLaunchKernelGGL(k_encode_lf, dim3((lanes + 255) / 256), dim3(256), 0, s, lf, Tc, lanes, x->enc,
+                                    d_words, pitch_words));
+            continue;
+        }
         rc = run_model(x, lanes, Tc, x->logits);
         x->pos += Tc;
         if (rc) return rc;

@@ -229,3 +229,34 @@ def test_layer_decode_in_two_halves(gpu):
         for i, c in enumerate(chunks):
             assert (out[i, :lens[i]] == c).all(), (fused, halves, i)
     m.release_engines()
+
+
+@pytest.mark.parametrize("d_model,precision", [(256, "bf16x3"), (256, "bf16w"), (512, "bf16w")])
+def test_head_quantiser_kernel_matches_head_gemms(gpu, d_model, precision):
+    """Compress tiles through the fused head + quantiser kernel (logits on chip, (lo, width) pairs, sequential
+    coder) and through the head GEMMs + per-lane encode kernel: identical words for every chunk, including
+    chunks that end inside a tile, length-1 chunks and the partial last tile; and the stream decodes."""
+    import codec
+    from boa_amd import weights as W
+
+    import model as M
+
+    m = M.BoaConstrictor(d_model, 2, 256).load_blob(W.seeded_blob(W.Cfg(d_model=d_model, n_layers=2), 5))
+    m.precision = precision
+    lens = [1, 2, 63, 64, 65, 66, 129, 200, 191, 130]
+    chunks = [_markov(L, seed=40 + i) for i, L in enumerate(lens)]
+    res = []
+    for flag in ("1", "0"):
+        os.environ["BOA_HEAD_XQ"] = flag
+        try:
+            m.release_engines()
+            res.append(codec.compress_payload(m, chunks))
+        finally:
+            del os.environ["BOA_HEAD_XQ"]
+    m.release_engines()
+    (p1, n1, f1, L1), (p0, n0, f0, L0) = res
+    assert np.array_equal(n1, n0) and f1 == f0 and L1 == L0
+    assert np.array_equal(np.asarray(p1), np.asarray(p0))
+    out = codec.decompress_payload(m, p1, n1, L1, f1)
+    for i, c in enumerate(chunks):
+        assert (out[i, :lens[i]] == c).all(), i
