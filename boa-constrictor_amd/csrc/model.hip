@@ -759,11 +759,18 @@ __device__ __forceinline__ int h_off(int r, int k) { return r * HC + (((k >> 3) 
 // i % R and is reloaded with block i + R right after its use, running on into the next chunk, so R blocks
 // are always in flight; pin_loads keeps each reload where it is issued.  (4 waves per SIMD instead of 2:
 // 6% faster than the 4-wave form with 64 x 16 FF1 tiles, which reads each W1 block once.)
-template <int NT>
+// OUTP: the out_proj GEMM runs first, inside this kernel: mm = y . W_out^T + b_out from the scan's split output
+// y [rows][512] (hi, lo), read in two K chunks of 256 staged through the LDS operand buffer, each output
+// accumulating its 16 K steps in ascending order through mfma_split_step (as the out_proj GEMM does); mm then
+// stays on chip (fp32 in the operand buffer) for LN2, instead of a round trip through HBM.  Wave w owns
+// out_proj outputs 32 w .. + 31 of all 64 rows; its 32 W_out blocks stream through a 4-slot ring.
+template <int NT, bool OUTP>
 __global__ void __launch_bounds__(512, 4) k_ffn(const float* __restrict__ mm, const float* __restrict__ ln_w,
                                                 const float* __restrict__ ln_b, const uint16_t* __restrict__ W1p,
                                                 const float* __restrict__ b1, const uint16_t* __restrict__ W2p,
-                                                const float* __restrict__ b2, float* __restrict__ x, int64_t M) {
+                                                const float* __restrict__ b2, float* __restrict__ x, int64_t M,
+                                                const uint16_t* __restrict__ yh, const uint16_t* __restrict__ yl,
+                                                const uint16_t* __restrict__ Wop, const float* __restrict__ bo) {
     using namespace ffn;
     __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * D];
     __shared__ __attribute__((aligned(16))) uint16_t sH[2][BM * HC];
@@ -771,7 +778,100 @@ __global__ void __launch_bounds__(512, 4) k_ffn(const float* __restrict__ mm, co
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int64_t m0 = (int64_t)blockIdx.x * BM;
     const int rows = (int)((M - m0) < BM ? (M - m0) : BM);
-    {
+    // LN2 of one row held by one wave (lane j: elements 4j .. 4j + 3) into the split operand
+    auto ln2_store = [&](int r, const float (&v)[4], float4 wv, float4 bv) {
+        float mu, rs;
+        ln_stats_row<1>(v, mu, rs);
+        const float y[4] = {ln_apply(v[0], mu, rs, wv.x, bv.x), ln_apply(v[1], mu, rs, wv.y, bv.y),
+                            ln_apply(v[2], mu, rs, wv.z, bv.z), ln_apply(v[3], mu, rs, wv.w, bv.w)};
+        uint2 hp, lp;
+        split4(y[0], y[1], y[2], y[3], hp, lp);
+        const int o = a_off(r, 4 * lane);
+        *reinterpret_cast<uint2*>(&sA[0][o]) = hp;
+        *reinterpret_cast<uint2*>(&sA[1][o]) = lp;
+    };
+    if constexpr (OUTP) {
+        constexpr int KO = 2 * D, KC = D, NKS = KO / 32, BLKO = (NT == 3) ? 1024 : 512, RO = 4;
+        const gptr<uint16_t> wop = G(Wop);
+        u32x4 oh[RO], ol[RO];
+        // block i (W_out fragment 2 wave + i % 2, K step i / 2) into ring slot i % RO
+        auto issue_o = [&](int i) {
+            const gptr<uint16_t> q = wop + ((int64_t)(2 * wave + (i & 1)) * NKS + (i >> 1)) * BLKO + lane * 8;
+            oh[i % RO] = ldg16(q);
+            ol[i % RO] = oh[i % RO];
+            if constexpr (NT == 3) ol[i % RO] = ldg16(q + 512);
+        };
+#pragma unroll
+        for (int i = 0; i < RO; ++i) issue_o(i);
+        floatx4 macc[4][2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) macc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        // y rows past M read 0 (buffer range check)
+        const __amdgpu_buffer_rsrc_t ryh = buf_rsrc(yh + m0 * KO, (uint32_t)rows * KO * 2);
+        const __amdgpu_buffer_rsrc_t ryl = buf_rsrc(yl + m0 * KO, (uint32_t)rows * KO * 2);
+#pragma unroll 1
+        for (int q = 0; q < KO / KC; ++q) {
+            // stage y[:, 256 q .. + 255] (hi, lo): 4 x 16 B per array per thread
+#pragma unroll
+            for (int e = 0; e < (BM * KC / 8) / 512; ++e) {
+                const int idx = e * 512 + tid, r = idx / (KC / 8), k = (idx % (KC / 8)) * 8;
+                const uint32_t off = (uint32_t)((r * KO + KC * q + k) * 2);
+                *reinterpret_cast<u32x4*>(&sA[0][a_off(r, k)]) = buf_ld16(ryh, off);
+                *reinterpret_cast<u32x4*>(&sA[1][a_off(r, k)]) = buf_ld16(ryl, off);
+            }
+            __syncthreads();
+            int lq = lane;  // LDS addresses formed per chunk (see k_head_xq)
+            __asm__ volatile("" : "+v"(lq));
+            const int arq = lq & 15, kqq = 8 * (lq >> 4);
+#pragma unroll
+            for (int s = 0; s < KC / 32; ++s) {
+                bf16x8 ah[4], al[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int o = a_off(16 * i + arq, 32 * s + kqq);
+                    ah[i] = *reinterpret_cast<const bf16x8*>(&sA[0][o]);
+                    al[i] = *reinterpret_cast<const bf16x8*>(&sA[1][o]);
+                }
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int bi = 2 * ((KC / 32) * q + s) + j;  // block index over the whole K
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        macc[i][j] = mfma_split_step<NT>(macc[i][j], ah[i], al[i], __builtin_bit_cast(bf16x8, oh[bi % RO]),
+                                                         __builtin_bit_cast(bf16x8, ol[bi % RO]));
+                    if (bi + RO < 2 * NKS) issue_o(bi + RO);
+                    pin_loads();
+                }
+            }
+            __syncthreads();  // the next chunk (or mm) rewrites the operand buffer
+        }
+        // mm (+ bias) as fp32 rows of 256 in the operand buffer
+        float* sM = reinterpret_cast<float*>(&sA[0][0]);
+        const int ar = lane & 15, m_of = 4 * (lane >> 4);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int col = 16 * (2 * wave + j) + ar;
+            const float bias = G(bo)[col];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sM[(16 * i + m_of + r) * D + col] = epi_value<EPI_BIAS>(macc[i][j][r], bias);
+        }
+        __syncthreads();
+        // LN2 of this wave's 8 rows: all read before any split is written over the fp32 rows
+        float v[8][4];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const float4 u = *reinterpret_cast<const float4*>(&sM[(8 * wave + q) * D + 4 * lane]);
+            v[q][0] = u.x; v[q][1] = u.y; v[q][2] = u.z; v[q][3] = u.w;
+        }
+        const float4 wv = ldg_f4(G(ln_w) + 4 * lane), bv = ldg_f4(G(ln_b) + 4 * lane);
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < 8; ++q) ln2_store(8 * wave + q, v[q], wv, bv);
+    } else {
         const __amdgpu_buffer_rsrc_t rm = buf_rsrc(mm + m0 * D, (uint32_t)rows * D * 4);
         const float4 wv = ldg_f4(G(ln_w) + 4 * lane), bv = ldg_f4(G(ln_b) + 4 * lane);
 #pragma unroll 4
@@ -779,15 +879,7 @@ __global__ void __launch_bounds__(512, 4) k_ffn(const float* __restrict__ mm, co
             const int r = 8 * wave + q;
             const u32x4 u = buf_ld16(rm, (uint32_t)((r * D + 4 * lane) * 4));
             const float v[4] = {__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w)};
-            float mu, rs;
-            ln_stats_row<1>(v, mu, rs);
-            const float y[4] = {ln_apply(v[0], mu, rs, wv.x, bv.x), ln_apply(v[1], mu, rs, wv.y, bv.y),
-                                ln_apply(v[2], mu, rs, wv.z, bv.z), ln_apply(v[3], mu, rs, wv.w, bv.w)};
-            uint2 hp, lp;
-            split4(y[0], y[1], y[2], y[3], hp, lp);
-            const int o = a_off(r, 4 * lane);
-            *reinterpret_cast<uint2*>(&sA[0][o]) = hp;
-            *reinterpret_cast<uint2*>(&sA[1][o]) = lp;
+            ln2_store(r, v, wv, bv);
         }
     }
     __syncthreads();
@@ -2095,7 +2187,7 @@ struct boa_ctx {
     // one half's state-bound groups (conv + scan) run while the other half's GEMM groups run.  lane0 shifts
     // the per-lane state of the launches (0 outside the second half).
     int decode_halves = 2;
-    bool ffn_outp = true;  // d_model 512: out_proj inside the feed-forward kernel (BOA_FFN_OUTP=0: separate GEMM)
+    bool ffn_outp = true;  // out_proj inside the feed-forward kernel (BOA_FFN_OUTP=0: separate GEMM)
     bool head_xq = true;   // compress tiles: head + quantiser in one kernel (BOA_HEAD_XQ=0: head GEMMs + k_encode_tile)
     hipStream_t stream2 = nullptr;
     std::vector<hipEvent_t> half_ev;   // [2][L]: state group of layer l done, per half; [2L]: stream join
@@ -2693,6 +2785,22 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc, int part = 7) {
                                     w.ff1_w.p, w.ff1_b, w.ff2_w.p, w.ff2_b, x->x, M, x->ah, x->al, w.out_w.p, w.out_b));
         return BOA_OK;
     }
+    const bool ffn256 = split && d == ffn::D && 4 * d == ffn::DF && di == 2 * d && w.ff1_w.p && w.ff2_w.p;
+    if (ffn256 && x->ffn_outp && w.out_w.p) {
+        // out_proj + LN2 + FF1 + GELU + FF2 + residual in one kernel (mm and the hidden layer kept on chip)
+        const double flops = gemm_flops(M, d, di) + gemm_flops(M, 4 * d, d) + gemm_flops(M, d, 4 * d);
+        const double bytes = 4.0 * M * di + 4.0 * M * d * 2 + 2.0 * (w.ff1_w.l ? 2 : 1) * (2.0 * 4 * d * d + d * di);
+        const unsigned grid = (unsigned)((M + ffn::BM - 1) / ffn::BM);
+        if (w.ff1_w.l)
+            PROF(PC_FFN, flops, bytes,
+                 hipLaunchKernelGGL((k_ffn<3, true>), dim3(grid), dim3(512), 0, s, nullptr, w.ln2_w, w.ln2_b, w.ff1_w.p,
+                                    w.ff1_b, w.ff2_w.p, w.ff2_b, x->x, M, x->ah, x->al, w.out_w.p, w.out_b));
+        else
+            PROF(PC_FFN, flops, bytes,
+                 hipLaunchKernelGGL((k_ffn<2, true>), dim3(grid), dim3(512), 0, s, nullptr, w.ln2_w, w.ln2_b, w.ff1_w.p,
+                                    w.ff1_b, w.ff2_w.p, w.ff2_b, x->x, M, x->ah, x->al, w.out_w.p, w.out_b));
+        return BOA_OK;
+    }
     // out_proj -> mm [M][d]
     {
         GemmArgs g = gemm_args(x->xs, di, w.out_w, w.out_b, x->mm, d, M, d, di);
@@ -2726,12 +2834,12 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc, int part = 7) {
         const unsigned grid = (unsigned)((M + ffn::BM - 1) / ffn::BM);
         if (w.ff1_w.l)
             PROF(PC_FFN, flops, bytes,
-                 hipLaunchKernelGGL((k_ffn<3>), dim3(grid), dim3(512), 0, s, x->mm, w.ln2_w, w.ln2_b, w.ff1_w.p,
-                                    w.ff1_b, w.ff2_w.p, w.ff2_b, x->x, M));
+                 hipLaunchKernelGGL((k_ffn<3, false>), dim3(grid), dim3(512), 0, s, x->mm, w.ln2_w, w.ln2_b, w.ff1_w.p,
+                                    w.ff1_b, w.ff2_w.p, w.ff2_b, x->x, M, nullptr, nullptr, nullptr, nullptr));
         else
             PROF(PC_FFN, flops, bytes,
-                 hipLaunchKernelGGL((k_ffn<2>), dim3(grid), dim3(512), 0, s, x->mm, w.ln2_w, w.ln2_b, w.ff1_w.p,
-                                    w.ff1_b, w.ff2_w.p, w.ff2_b, x->x, M));
+                 hipLaunchKernelGGL((k_ffn<2, false>), dim3(grid), dim3(512), 0, s, x->mm, w.ln2_w, w.ln2_b, w.ff1_w.p,
+                                    w.ff1_b, w.ff2_w.p, w.ff2_b, x->x, M, nullptr, nullptr, nullptr, nullptr));
         return BOA_OK;
     }
     // LN2 + FF1 + GELU -> g [M][4d]

@@ -231,11 +231,13 @@ def test_layer_decode_in_two_halves(gpu):
     m.release_engines()
 
 
+@pytest.mark.parametrize("flag", ["BOA_HEAD_XQ", "BOA_FFN_OUTP"])
 @pytest.mark.parametrize("d_model,precision", [(256, "bf16x3"), (256, "bf16w"), (512, "bf16w")])
-def test_head_quantiser_kernel_matches_head_gemms(gpu, d_model, precision):
-    """Compress tiles through the fused head + quantiser kernel (logits on chip, (lo, width) pairs, sequential
-    coder) and through the head GEMMs + per-lane encode kernel: identical words for every chunk, including
-    chunks that end inside a tile, length-1 chunks and the partial last tile; and the stream decodes."""
+def test_fused_compress_kernels_match_separate_kernels(gpu, d_model, precision, flag):
+    """Compress tiles with and without one kernel fusion -- BOA_HEAD_XQ: the head + quantiser kernel (logits on
+    chip, (lo, width) pairs, sequential coder) against the head GEMMs + per-lane encode kernel; BOA_FFN_OUTP:
+    out_proj inside the feed-forward kernel against the separate out_proj GEMM: identical words for every chunk,
+    including chunks that end inside a tile, length-1 chunks and the partial last tile; and the stream decodes."""
     import codec
     from boa_amd import weights as W
 
@@ -246,13 +248,13 @@ def test_head_quantiser_kernel_matches_head_gemms(gpu, d_model, precision):
     lens = [1, 2, 63, 64, 65, 66, 129, 200, 191, 130]
     chunks = [_markov(L, seed=40 + i) for i, L in enumerate(lens)]
     res = []
-    for flag in ("1", "0"):
-        os.environ["BOA_HEAD_XQ"] = flag
+    for val in ("1", "0"):
+        os.environ[flag] = val
         try:
             m.release_engines()
             res.append(codec.compress_payload(m, chunks))
         finally:
-            del os.environ["BOA_HEAD_XQ"]
+            del os.environ[flag]
     m.release_engines()
     (p1, n1, f1, L1), (p0, n0, f0, L0) = res
     assert np.array_equal(n1, n0) and f1 == f0 and L1 == L0
