@@ -2189,6 +2189,8 @@ struct boa_ctx {
     int decode_halves = 2;
     bool ffn_outp = true;  // out_proj inside the feed-forward kernel (BOA_FFN_OUTP=0: separate GEMM)
     bool head_xq = true;   // compress tiles: head + quantiser in one kernel (BOA_HEAD_XQ=0: head GEMMs + k_encode_tile)
+    // compress in two halves of the lanes on two streams, the scans alternating (BOA_COMPRESS_HALVES=0: one stream)
+    bool compress_halves = true;
     hipStream_t stream2 = nullptr;
     std::vector<hipEvent_t> half_ev;   // [2][L]: state group of layer l done, per half; [2L]: stream join
     int64_t lane0 = 0;
@@ -2574,7 +2576,8 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
     if (const char* v = getenv("BOA_DECODE_HALVES")) x->decode_halves = atoi(v) == 1 ? 1 : 2;
     if (const char* v = getenv("BOA_FFN_OUTP")) x->ffn_outp = atoi(v) != 0;
     if (const char* v = getenv("BOA_HEAD_XQ")) x->head_xq = atoi(v) != 0;
-    if (!x->fused && x->decode_halves == 2) {
+    if (const char* v = getenv("BOA_COMPRESS_HALVES")) x->compress_halves = atoi(v) != 0;
+    if ((!x->fused && x->decode_halves == 2) || (x->compress_halves && x->prec != BOA_PREC_F32)) {
         // default priority (as the context's own stream): streams of different priorities are not mixed
         e = hipStreamCreateWithFlags(&x->stream2, hipStreamNonBlocking);
         for (int i = 0; e == hipSuccess && i < 2 * L + 1; ++i) {
@@ -2661,7 +2664,8 @@ static void launch_scan(boa_ctx* x, const LayerW& w, float* ssm, int B, int Tc) 
 //               FF1(GELU, split output into xz's memory) -> FF2(+residual) into x
 // part selects which of three consecutive groups of the layer to launch (bits, 7 = the whole layer):
 //   1: LN1 + in_proj;  2: conv + x_proj + scan (the state traffic);  4: out_proj + LN2 + feed-forward.
-// The fused compress-tile kernels (k_mixin, k_mixin512) span groups 1 and 2 and need both bits.
+// Where a fused compress-tile kernel (k_mixin, k_mixin512) covers LN1 through x_proj, bit 1 launches it and
+// bit 2 the scan alone.
 static int run_layer(boa_ctx* x, int l, int B, int Tc, int part = 7) {
     const LayerW& w = x->layers[l];
     const int d = x->d, di = x->di, NS = x->NS, R = x->R;
@@ -2673,10 +2677,9 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc, int part = 7) {
     uint16_t* gl = gh + M * 4 * d;
     int rc = 0;
     float* hist = x->conv_hist + ((int64_t)l * x->max_lanes + x->lane0) * 3 * di;
-    const bool both = (part & 3) == 3;
-    const bool mix5 = both && split && d == mixin5::D && di == mixin5::DI && R + 2 * NS == mixin5::FW && Tc == mixin5::BM &&
+    const bool mix5 = split && d == mixin5::D && di == mixin5::DI && R + 2 * NS == mixin5::FW && Tc == mixin5::BM &&
                       w.in_w.p && w.x_w.p;
-    if (mix5) {
+    if (mix5 && (part & 1)) {
         // LN1 + in_proj + conv + SiLU + x_proj in one kernel per lane tile, d_model 512
         const double flops = gemm_flops(M, 2 * di, d) + gemm_flops(M, R + 2 * NS, di) + 8.0 * M * di;
         const double bytes = 4.0 * M * (d + di + di + R + 2 * NS) + 4.0 * 6 * B * di;
@@ -2691,9 +2694,9 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc, int part = 7) {
                                     w.in_w.p, w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs, x->dbc, hist,
                                     (int)(x->pos % 3)));
     }
-    const bool mix = both && !mix5 && split && d == mixin::D && di == mixin::DI && R + 2 * NS == mixin::FW && Tc == mixin::BM &&
+    const bool mix = !mix5 && split && d == mixin::D && di == mixin::DI && R + 2 * NS == mixin::FW && Tc == mixin::BM &&
                      w.in_w.p && w.x_w.p;
-    if (mix) {
+    if (mix && (part & 1)) {
         // LN1 + in_proj + conv + SiLU + x_proj in one kernel per lane tile
         const double flops = gemm_flops(M, 2 * di, d) + gemm_flops(M, R + 2 * NS, di) + 8.0 * M * di;
         const double bytes = 4.0 * M * (d + di + di + R + 2 * NS) + 4.0 * 6 * B * di;
@@ -2705,7 +2708,7 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc, int part = 7) {
             PROF(PC_MIXIN, flops, bytes,
                  hipLaunchKernelGGL((k_mixin<2>), dim3((unsigned)B), dim3(256), 0, s, x->x, w.ln1_w, w.ln1_b, w.in_w.p,
                                     w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs, x->dbc, hist, (int)(x->pos % 3)));
-    } else if (!mix5) {
+    } else if (!mix5 && !mix) {
     // LN1 + in_proj -> xz [M][2di]
     if (part & 1) {
         GemmArgs g = gemm_args(x->x, d, w.in_w, w.in_b, x->xz, 2 * di, M, 2 * di, d);
@@ -3065,7 +3068,71 @@ extern "C" int boa_compress(boa_ctx* x, const uint8_t* d_bytes, int64_t byte_str
     hipLaunchKernelGGL(k_enc_init, dim3((lanes + 255) / 256), dim3(256), 0, s, x->enc, lanes);
     BOA_HIP_TRY(hipMemsetAsync(x->flag, 0, sizeof(int32_t), s));
     const int positions = max_len - 1;  // model inputs 0..max_len-2 predict bytes 1..max_len-1
-    for (int t0 = 0; t0 < positions; t0 += x->tile_len) {
+    const int la = lanes / 2, lb = lanes - la;
+    const bool halves = x->stream2 && x->compress_halves && lanes >= 512 && (int64_t)lb * x->tile_len <= x->max_rows / 2;
+    if (halves) {
+        // Two halves of the lanes on two streams.  Per layer and half: the mixer input kernel, the scan, the
+        // feed-forward kernel.  The scans (VALU-bound) alternate between the halves (A's layer l after B's
+        // layer l - 1, B's layer l after A's layer l), so one half's scan runs beside the other half's
+        // MFMA-bound kernels.  Each half's arithmetic is unchanged.
+        const int L = x->L;
+        hipEvent_t* evA = x->half_ev.data();
+        hipEvent_t* evB = evA + L;
+        hipEvent_t join = evA[2 * L];
+        BOA_HIP_TRY(hipEventRecord(join, s));  // the second stream starts after the coder initialisation
+        BOA_HIP_TRY(hipStreamWaitEvent(x->stream2, join, 0));
+        for (int t0 = 0; t0 < positions; t0 += x->tile_len) {
+            const int Tc = std::min(x->tile_len, positions - t0);
+            for (int h = 0; h < 2; ++h) {
+                LaneView v(x, h, h ? la : 0, h ? x->stream2 : s);
+                const int64_t b0 = x->lane0, rows = (int64_t)(h ? lb : la) * Tc;
+                PROF(PC_EMBED, 0.0, 4.0 * rows * x->d,
+                     hipLaunchKernelGGL(k_embed_bytes, dim3(row_blocks(rows)), dim3(256), 0, x->stream,
+                                        d_bytes + b0 * byte_stride, byte_stride, d_lens + b0, t0, Tc, rows, x->emb,
+                                        x->d, x->V, x->x));
+            }
+            for (int l = 0; l < L; ++l) {
+                for (int h = 0; h < 2; ++h) {
+                    LaneView v(x, h, h ? la : 0, h ? x->stream2 : s);
+                    const int nl = h ? lb : la;
+                    rc = run_layer(x, l, nl, Tc, 1);
+                    if (rc) return rc;
+                    hipEvent_t prev = h ? evA[l] : (l > 0 ? evB[l - 1] : (t0 > 0 ? evB[L - 1] : nullptr));
+                    if (prev) BOA_HIP_TRY(hipStreamWaitEvent(x->stream, prev, 0));
+                    rc = run_layer(x, l, nl, Tc, 2);
+                    if (rc) return rc;
+                    BOA_HIP_TRY(hipEventRecord(h ? evB[l] : evA[l], x->stream));
+                    rc = run_layer(x, l, nl, Tc, 4);
+                    if (rc) return rc;
+                }
+            }
+            for (int h = 0; h < 2; ++h) {
+                LaneView v(x, h, h ? la : 0, h ? x->stream2 : s);
+                const int nl = h ? lb : la;
+                const int64_t b0 = x->lane0, rows = (int64_t)nl * Tc;
+                if (head_xq_ok(x, Tc)) {
+                    uint2* lf = reinterpret_cast<uint2*>(x->logits);
+                    rc = launch_head_xq(x, nl, t0, d_bytes + b0 * byte_stride, byte_stride, d_lens + b0, lf);
+                    if (rc) return rc;
+                    PROF(PC_ENCODE, 0.0, 8.0 * rows + 32.0 * nl,
+                         hipLaunchKernelGGL(k_encode_lf, dim3((nl + 255) / 256), dim3(256), 0, x->stream, lf, Tc, nl,
+                                            x->enc + b0, d_words + b0 * pitch_words, pitch_words));
+                } else {
+                    rc = run_head(x, nl, Tc, x->logits);
+                    if (rc) return rc;
+                    PROF(PC_ENCODE, 0.0, 4.0 * rows * x->V + (double)rows,
+                         hipLaunchKernelGGL(k_encode_tile, dim3(nl), dim3(64), 0, x->stream, x->logits, x->V, Tc, t0,
+                                            d_bytes + b0 * byte_stride, byte_stride, d_lens + b0, x->enc + b0,
+                                            d_words + b0 * pitch_words, pitch_words));
+                }
+            }
+            x->pos += Tc;
+        }
+        BOA_HIP_TRY(hipGetLastError());
+        BOA_HIP_TRY(hipEventRecord(join, x->stream2));  // the context's stream joins the second
+        BOA_HIP_TRY(hipStreamWaitEvent(s, join, 0));
+    }
+    for (int t0 = 0; !halves && t0 < positions; t0 += x->tile_len) {
         const int Tc = std::min(x->tile_len, positions - t0);
         const int64_t rows = (int64_t)lanes * Tc;
         PROF(PC_EMBED, 0.0, 4.0 * rows * x->d,

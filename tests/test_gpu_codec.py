@@ -262,3 +262,31 @@ def test_fused_compress_kernels_match_separate_kernels(gpu, d_model, precision, 
     out = codec.decompress_payload(m, p1, n1, L1, f1)
     for i, c in enumerate(chunks):
         assert (out[i, :lens[i]] == c).all(), i
+
+
+@pytest.mark.parametrize("precision", ["bf16x3", "bf16w"])
+def test_compress_in_two_halves(gpu, precision):
+    """A wave large enough (>= 512 lanes) to compress as two halves of the lanes on two streams, their scans
+    alternating: the same words as one stream, for full and partial tiles, and the stream decodes."""
+    import codec
+
+    m, _ = _model(2)
+    m.precision = precision
+    rng = np.random.default_rng(8)
+    lens = [int(v) for v in rng.integers(1, 200, 601)]
+    chunks = [_markov(L, seed=300 + i) for i, L in enumerate(lens)]
+    res = []
+    for val in ("1", "0"):
+        os.environ["BOA_COMPRESS_HALVES"] = val
+        try:
+            m.release_engines()
+            res.append(codec.compress_payload(m, chunks))
+        finally:
+            del os.environ["BOA_COMPRESS_HALVES"]
+    m.release_engines()
+    (p1, n1, f1, L1), (p0, n0, f0, L0) = res
+    assert np.array_equal(n1, n0)
+    assert np.array_equal(np.asarray(p1), np.asarray(p0))
+    out = codec.decompress_payload(m, p1, n1, L1, f1)
+    for i, c in enumerate(chunks):
+        assert (out[i, :lens[i]] == c).all(), i
