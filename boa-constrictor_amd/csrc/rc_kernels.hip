@@ -16,6 +16,8 @@
 
 using namespace boa;
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
 // ================================================================================================
 // Coder on precomputed tables.  Table row = cdf[0..K-1] of one step (cdf[K] = 2^P implied).
 
@@ -68,6 +70,170 @@ __global__ void __launch_bounds__(64) k_rc_decode_tables(const TC* __restrict__ 
 #pragma unroll
         for (int j = 0; j < 4; ++j) cur[j] = nxt[j];
     }
+}
+
+// The same coder for full tables (K = 256), streams of a length divisible by 4 and 16-byte aligned tables,
+// written for throughput: four streams per wavefront, 16 lanes per stream, each lane holding 16 entries of
+// a row (a row of one stream is one coalesced 512 B (P = 16) or 1 KiB (P = 24) read by its 16 lanes).
+// Rows are prefetched D = 4 steps ahead through a register ring (independent of the coder state), and each
+// stream's next code words come from a register window: lane j of a stream holds words base + j and
+// base + 16 + j, shifted by 16 (one load per lane) once the read position passes base + 16, so no step waits
+// on a word load.  The coder arithmetic is the reference's (rc_core.h: dec_target, and dec_advance's update
+// with its words taken from the window; gpu_range_coder.py:182-210); the symbol search keeps its semantics
+// (the smallest i in [1, K] with cdf[i] > q, minus one): each lane finds its first such entry in one pass from
+// the top, carrying cdf[i] and cdf[i - 1], and the stream takes the minimum over its 16 lanes.
+template <int P, typename TC>
+__global__ void __launch_bounds__(256) k_rc_decode_tables4(const TC* __restrict__ cdf,
+                                                         const uint32_t* __restrict__ words, int64_t pitch,
+                                                         const int32_t* __restrict__ nwords, int streams, int len,
+                                                         uint8_t* __restrict__ syms) {
+    constexpr int K = 256, S = 16, E = K / S, G = 64 / S, D = 4;
+    constexpr int NV = E * (int)sizeof(TC) / 16;  // 16-byte loads per lane per row
+    const int lane = threadIdx.x & 63;
+    const int j = lane & (S - 1), gbase = lane & ~(S - 1);
+    const int64_t n = ((int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6)) * G + lane / S;
+    const bool live = n < streams;
+    const int64_t nn = live ? n : 0;  // groups past the last stream shadow stream 0 with no words, write nothing
+    const uint32_t* in = words + nn * pitch;
+    int32_t nw = live ? nwords[nn] : 0;
+    if (nw > pitch) nw = (int32_t)pitch;
+    DecState st;
+    dec_init(st, in, nw);
+    int32_t base = 0;
+    uint32_t w0 = (j < nw) ? in[j] : 0u;
+    uint32_t w1 = (S + j < nw) ? in[S + j] : 0u;
+    const TC* crow = cdf + nn * (int64_t)len * K + E * j;
+    u32x4 rows[D][NV];
+    auto load_row = [&](int t, u32x4 (&r)[NV]) {
+        const TC* p = crow + (int64_t)(t < len ? t : len - 1) * K;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) r[v] = *reinterpret_cast<const u32x4*>(p + v * (16 / (int)sizeof(TC)));
+    };
+#pragma unroll
+    for (int u = 0; u < D - 1; ++u) load_row(u, rows[u]);
+    // word i of this stream (base <= i < base + 2S) from the window
+    auto word_at = [&](int i) -> uint32_t {
+        const int o = i - base;
+        const int src = gbase + (o & (S - 1));
+        const uint32_t a = __shfl(w0, src, 64), b = __shfl(w1, src, 64);
+        return o < S ? a : b;
+    };
+    uint8_t* out = syms + nn * (int64_t)len;
+#pragma unroll 1
+    for (int t0 = 0; t0 < len; t0 += D) {
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+            const int t = t0 + u;
+            load_row(t + D - 1, rows[(u + D - 1) % D]);
+            uint32_t e[E];
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                const uint32_t d[4] = {rows[u][v].x, rows[u][v].y, rows[u][v].z, rows[u][v].w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    if constexpr (sizeof(TC) == 2) {
+                        e[8 * v + 2 * k] = d[k] & 0xFFFFu;
+                        e[8 * v + 2 * k + 1] = d[k] >> 16;
+                    } else {
+                        e[4 * v + k] = d[k];
+                    }
+                }
+            }
+            const uint32_t q = dec_target(st, P);
+            const uint32_t prev_last = __shfl_up(e[E - 1], 1, 64);  // cdf[E j - 1] (unused for j = 0)
+            int first = E;
+            uint32_t hv = 0u, lv = 0u;
+#pragma unroll
+            for (int i = E - 1; i >= 0; --i) {
+                const bool pred = e[i] > q && (i > 0 || j > 0);
+                first = pred ? i : first;
+                hv = pred ? e[i] : hv;
+                lv = pred ? (i > 0 ? e[i - 1] : prev_last) : lv;
+            }
+            int kl = first < E ? E * j + first : K;
+#pragma unroll
+            for (int o = 1; o < S; o <<= 1) kl = min(kl, __shfl_xor(kl, o, 64));
+            const int owner = gbase + (kl < K ? kl / E : S - 1);
+            const uint32_t lo_a = __shfl(lv, owner, 64), hi_a = __shfl(hv, owner, 64), last = __shfl(e[E - 1], owner, 64);
+            const uint32_t lo = kl < K ? lo_a : last;
+            const uint32_t hi = kl < K ? hi_a : (1u << P);
+            if (live && j == 0) out[t] = (uint8_t)(kl - 1);
+            // dec_advance (rc_core.h) with the words from the window
+            uint32_t prob = hi - lo;
+            if (prob == 0u) prob = 1u;
+            const uint64_t scale = st.range >> P;
+            st.lower = st.lower + scale * (uint64_t)lo;
+            st.range = scale * (uint64_t)prob;
+            const uint32_t wa = word_at(st.read_idx), wb = word_at(st.read_idx + 1);
+#pragma unroll
+            for (int it = 0; it < 2; ++it) {
+                if (st.range < (1ull << 32)) {
+                    st.lower <<= 32;
+                    st.range <<= 32;
+                    st.point = (st.point << 32) | (uint64_t)(it == 0 ? wa : wb);
+                    if (st.read_idx < nw) st.read_idx++;
+                }
+            }
+            if (st.read_idx - base >= S) {
+                base += S;
+                w0 = w1;
+                const int i = base + S + j;
+                w1 = (i < nw) ? in[i] : 0u;
+            }
+        }
+    }
+}
+
+// Encoder on full tables (K = 256), streams of a length divisible by 16: one thread per stream, the table
+// entries of 16 symbols (independent of the coder state) loaded one block ahead, the symbols two blocks ahead,
+// so enc_push (rc_core.h) runs without waiting on memory.
+template <int P, typename TC>
+__global__ void __launch_bounds__(64) k_rc_encode_tables16(const TC* __restrict__ cdf,
+                                                         const uint8_t* __restrict__ syms, int streams, int len,
+                                                         uint32_t* __restrict__ words, int64_t pitch,
+                                                         int32_t* __restrict__ nwords) {
+    constexpr int K = 256, B = 16;
+    const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const bool live = n < streams;
+    const int64_t nn = live ? n : 0;
+    EncState st;
+    enc_init(st);
+    const WordSink sink{words + nn * pitch, pitch, live};
+    const TC* c = cdf + nn * (int64_t)len * K;
+    const uint8_t* sp = syms + nn * (int64_t)len;
+    const int nb = len / B;
+    auto load_syms = [&](int b) { return *reinterpret_cast<const uint4*>(sp + (int64_t)(b < nb ? b : nb - 1) * B); };
+    auto issue = [&](int b, uint4 sv, uint32_t (&lo)[B], uint32_t (&hi)[B]) {
+        const int bb = b < nb ? b : nb - 1;
+        const uint32_t w[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            const int s = (w[u / 4] >> (8 * (u % 4))) & 0xFF;
+            const TC* r = c + ((int64_t)bb * B + u) * K;
+            lo[u] = (uint32_t)r[s];
+            hi[u] = (uint32_t)r[s + 1 < K ? s + 1 : s];
+            if (s + 1 >= K) hi[u] = 1u << P;
+        }
+    };
+    auto code = [&](const uint32_t (&lo)[B], const uint32_t (&hi)[B]) {
+#pragma unroll
+        for (int u = 0; u < B; ++u) enc_push(st, P, lo[u], hi[u] - lo[u], sink);
+    };
+    uint32_t loA[B], hiA[B], loB[B], hiB[B];
+    uint4 sv1 = load_syms(1), sv2;
+    issue(0, load_syms(0), loA, hiA);
+#pragma unroll 1
+    for (int b = 0; b < nb; b += 2) {
+        sv2 = load_syms(b + 2);
+        issue(b + 1, sv1, loB, hiB);
+        code(loA, hiA);
+        if (b + 1 >= nb) break;
+        sv1 = load_syms(b + 3);
+        issue(b + 2, sv2, loA, hiA);
+        code(loB, hiB);
+    }
+    enc_finish(st, sink);
+    if (live) nwords[n] = st.nwords;
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -300,6 +466,24 @@ extern "C" int rc_encode_tables(int32_t precision, int32_t cdf_bytes, const void
     if (streams == 0) return BOA_OK;
     const dim3 grid((streams + 255) / 256), block(256);
     hipStream_t s = as_stream(stream);
+    // full tables, whole 16-symbol blocks, 16-byte aligned symbol rows: the pipelined encoder
+    if (K == 256 && len >= 16 && len % 16 == 0 && ((uintptr_t)d_syms & 15) == 0 && (precision == 16 || cdf_bytes == 4)) {
+        const dim3 g16((streams + 63) / 64), b16(64);
+        if (cdf_bytes == 2 && precision == 16)
+            hipLaunchKernelGGL((k_rc_encode_tables16<16, uint16_t>), g16, b16, 0, s, (const uint16_t*)d_cdf, d_syms,
+                               streams, len, d_words, pitch_words, d_nwords);
+        else if (cdf_bytes == 4 && precision == 16)
+            hipLaunchKernelGGL((k_rc_encode_tables16<16, uint32_t>), g16, b16, 0, s, (const uint32_t*)d_cdf, d_syms,
+                               streams, len, d_words, pitch_words, d_nwords);
+        else if (cdf_bytes == 4 && precision == 24)
+            hipLaunchKernelGGL((k_rc_encode_tables16<24, uint32_t>), g16, b16, 0, s, (const uint32_t*)d_cdf, d_syms,
+                               streams, len, d_words, pitch_words, d_nwords);
+        else
+            return boa_fail(BOA_ERR_ARG, "rc_encode_tables: precision %d with %d-byte tables unsupported",
+                            precision, cdf_bytes);
+        BOA_HIP_TRY(hipGetLastError());
+        return BOA_OK;
+    }
     if (precision == 16 && cdf_bytes == 2)
         hipLaunchKernelGGL((k_rc_encode_tables<16, uint16_t>), grid, block, 0, s, (const uint16_t*)d_cdf, K,
                            d_syms, streams, len, d_words, pitch_words, d_nwords);
@@ -325,6 +509,24 @@ extern "C" int rc_decode_tables(int32_t precision, int32_t cdf_bytes, const void
     if (streams == 0) return BOA_OK;
     const dim3 grid(streams), block(64);
     hipStream_t s = as_stream(stream);
+    // full tables, lengths in whole groups of 4 steps, 16-byte aligned rows: four streams per wavefront
+    if (K == 256 && len >= 4 && len % 4 == 0 && ((uintptr_t)d_cdf & 15) == 0) {
+        const dim3 g4((unsigned)((streams + 15) / 16)), b4(256);
+        if (cdf_bytes == 2 && precision == 16)
+            hipLaunchKernelGGL((k_rc_decode_tables4<16, uint16_t>), g4, b4, 0, s, (const uint16_t*)d_cdf, d_words,
+                               pitch_words, d_nwords, streams, len, d_syms);
+        else if (cdf_bytes == 4 && precision == 16)
+            hipLaunchKernelGGL((k_rc_decode_tables4<16, uint32_t>), g4, b4, 0, s, (const uint32_t*)d_cdf, d_words,
+                               pitch_words, d_nwords, streams, len, d_syms);
+        else if (cdf_bytes == 4 && precision == 24)
+            hipLaunchKernelGGL((k_rc_decode_tables4<24, uint32_t>), g4, b4, 0, s, (const uint32_t*)d_cdf, d_words,
+                               pitch_words, d_nwords, streams, len, d_syms);
+        else
+            return boa_fail(BOA_ERR_ARG, "rc_decode_tables: precision %d with %d-byte tables unsupported",
+                            precision, cdf_bytes);
+        BOA_HIP_TRY(hipGetLastError());
+        return BOA_OK;
+    }
     if (precision == 16 && cdf_bytes == 2)
         hipLaunchKernelGGL((k_rc_decode_tables<16, uint16_t>), grid, block, 0, s, (const uint16_t*)d_cdf, K,
                            d_words, pitch_words, d_nwords, streams, len, d_syms);

@@ -34,12 +34,15 @@ def _encode_gpu(lib, P, cb, tables, syms, pitch):
     return d_cdf, d_words, d_n
 
 
-@pytest.mark.parametrize("P,cb,K", [(16, 2, 256), (16, 4, 256), (24, 4, 256), (16, 2, 100), (24, 4, 7)])
-def test_tables_bit_exact(gpu, ora, P, cb, K):
+# T = 256 with K = 256 takes the throughput kernels (four streams per wave decoder, block-pipelined encoder);
+# T = 257 and K < 256 the one-stream-per-wave ones.  S = 45 leaves part of the last wave without a stream.
+@pytest.mark.parametrize("P,cb,K,T", [(16, 2, 256, 257), (16, 4, 256, 257), (24, 4, 256, 257), (16, 2, 100, 257),
+                                      (24, 4, 7, 257), (16, 2, 256, 256), (16, 4, 256, 256), (24, 4, 256, 256)])
+def test_tables_bit_exact(gpu, ora, P, cb, K, T):
     from boa_amd import _native as N
 
-    rng = np.random.default_rng(P * 1000 + cb * 100 + K)
-    S, T = 48, 257
+    rng = np.random.default_rng(P * 1000 + cb * 100 + K + T)
+    S = 45
     logits = rng.normal(0, 3, (S, T, K)).astype(np.float32)
     cdf = ora.xq_cdf(logits, P)
     syms = _sample(cdf, rng, P)
@@ -56,6 +59,32 @@ def test_tables_bit_exact(gpu, ora, P, cb, K):
     N.check(gpu.rc_decode_tables(P, cb, N.ptr(d_cdf), K, N.ptr(d_words), pitch, N.ptr(d_n), S, T, N.ptr(d_out),
                                  N.stream_ptr()))
     assert (d_out.cpu().numpy() == syms).all()
+
+
+@pytest.mark.parametrize("P,cb,T", [(16, 2, 256), (24, 4, 256), (16, 2, 255)])
+def test_decode_tables_arbitrary_words(gpu, ora, P, cb, T):
+    """Decoding words that no encoder wrote (random values, random stream lengths 0 .. 2 T, including 0, 1 and
+    2 words) on valid tables: every symbol equals the oracle decoder's, which exercises the target division, the
+    symbol search at arbitrary targets and the reading of words past the end of a stream (zeros)."""
+    from boa_amd import _native as N
+
+    rng = np.random.default_rng(P + T)
+    S, K = 45, 256
+    cdf = ora.xq_cdf(rng.normal(0, 3, (S, T, K)).astype(np.float32), P)
+    pitch = 2 * T + 8
+    words = rng.integers(0, 1 << 32, (S, pitch), dtype=np.uint64).astype(np.uint32)
+    nw = rng.integers(0, 2 * T, S).astype(np.int32)
+    nw[:4] = [0, 1, 2, 3]
+    d_cdf = _dev(cdf[..., :K].astype(np.uint16 if cb == 2 else np.uint32))
+    d_words = _dev(words.view(np.int32))
+    d_n = _dev(nw)
+    d_out = torch.zeros((S, T), dtype=torch.uint8, device="cuda")
+    N.check(gpu.rc_decode_tables(P, cb, N.ptr(d_cdf), K, N.ptr(d_words), pitch, N.ptr(d_n), S, T, N.ptr(d_out),
+                                 N.stream_ptr()))
+    out = d_out.cpu().numpy()
+    for s in range(S):
+        ref = ora.decode_tables(P, cdf[s], words[s, :nw[s]])
+        assert (out[s] == ref).all(), s
 
 
 def test_tables_empty_and_skipped_symbols(gpu, ora):
