@@ -134,6 +134,34 @@ BOA_HD uint32_t dec_target(const DecState& st, int P) {
     return (uint32_t)q;
 }
 
+// The same quotient for P <= 16 from an fp32 estimate: d and scale rounded to fp32 (each within 2^-23
+// relative, as hi * 2^32 + lo with two roundings), their quotient within about 2^-21 relative (the device
+// reciprocal adds 1 ulp), i.e. below 2^-5 in absolute terms for q <= 2^16; then dec_target's clamp and one-step
+// integer correction, which make it exact.  Branch-free (scale = 0 gives 0, as dec_target).
+BOA_HD float u64_to_f32(uint64_t v) {
+    uint32_t hi = (uint32_t)(v >> 32), lo = (uint32_t)v;
+#ifdef __HIP_DEVICE_COMPILE__
+    __asm__("" : "+v"(hi));  // two 32-bit conversions, not the compiler's exactly rounded 64-bit sequence
+#endif
+    return (float)hi * 4294967296.0f + (float)lo;
+}
+BOA_HD uint32_t dec_target16(const DecState& st, int P) {
+    const uint64_t scale = st.range >> P;
+    const uint64_t sc = scale ? scale : 1ull;
+    const uint64_t d = st.point - st.lower;
+    const uint32_t cap = 1u << P;
+#ifdef __HIP_DEVICE_COMPILE__
+    const float qf = u64_to_f32(d) * __builtin_amdgcn_rcpf(u64_to_f32(sc));
+#else
+    const float qf = u64_to_f32(d) / u64_to_f32(sc);
+#endif
+    uint32_t q = qf >= (float)cap ? cap : (uint32_t)qf;
+    const uint64_t prod = (uint64_t)q * sc;
+    q = prod > d ? q - 1u : ((d - prod >= sc && q < cap) ? q + 1u : q);
+    q = q >= cap ? cap - 1u : q;
+    return scale ? q : 0u;
+}
+
 // gpu_range_coder.py:200-209
 BOA_HD void dec_advance(DecState& st, int P, uint32_t left, uint32_t prob,
                                             const uint32_t* in, int32_t n) {

@@ -7,6 +7,7 @@
 #include "boa_common.h"
 
 #include <stdarg.h>
+#include <stdlib.h>
 #include <stdio.h>
 #include <string.h>
 #include <string>
@@ -82,12 +83,12 @@ __global__ void __launch_bounds__(64) k_rc_decode_tables(const TC* __restrict__ 
 // with its words taken from the window; gpu_range_coder.py:182-210); the symbol search keeps its semantics
 // (the smallest i in [1, K] with cdf[i] > q, minus one): each lane finds its first such entry in one pass from
 // the top, carrying cdf[i] and cdf[i - 1], and the stream takes the minimum over its 16 lanes.
-template <int P, typename TC>
+template <int P, typename TC, int S = 16, int D = 4>
 __global__ void __launch_bounds__(256) k_rc_decode_tables4(const TC* __restrict__ cdf,
                                                          const uint32_t* __restrict__ words, int64_t pitch,
                                                          const int32_t* __restrict__ nwords, int streams, int len,
                                                          uint8_t* __restrict__ syms) {
-    constexpr int K = 256, S = 16, E = K / S, G = 64 / S, D = 4;
+    constexpr int K = 256, E = K / S, G = 64 / S;
     constexpr int NV = E * (int)sizeof(TC) / 16;  // 16-byte loads per lane per row
     const int lane = threadIdx.x & 63;
     const int j = lane & (S - 1), gbase = lane & ~(S - 1);
@@ -139,7 +140,7 @@ __global__ void __launch_bounds__(256) k_rc_decode_tables4(const TC* __restrict_
                     }
                 }
             }
-            const uint32_t q = dec_target(st, P);
+            const uint32_t q = P <= 16 ? dec_target16(st, P) : dec_target(st, P);
             const uint32_t prev_last = __shfl_up(e[E - 1], 1, 64);  // cdf[E j - 1] (unused for j = 0)
             int first = E;
             uint32_t hv = 0u, lv = 0u;
@@ -164,16 +165,14 @@ __global__ void __launch_bounds__(256) k_rc_decode_tables4(const TC* __restrict_
             const uint64_t scale = st.range >> P;
             st.lower = st.lower + scale * (uint64_t)lo;
             st.range = scale * (uint64_t)prob;
-            const uint32_t wa = word_at(st.read_idx), wb = word_at(st.read_idx + 1);
-#pragma unroll
-            for (int it = 0; it < 2; ++it) {
-                if (st.range < (1ull << 32)) {
-                    st.lower <<= 32;
-                    st.range <<= 32;
-                    st.point = (st.point << 32) | (uint64_t)(it == 0 ? wa : wb);
-                    if (st.read_idx < nw) st.read_idx++;
-                }
-            }
+            // one renormalisation at most: the range is >= 2^32 before every step, so range' = (range >> P) * prob
+            // >= 2^(32 - P) and one 32-bit shift restores range >= 2^32 (dec_advance's second round never runs)
+            const uint32_t wa = word_at(st.read_idx);
+            const bool sh = st.range < (1ull << 32);
+            st.lower = sh ? st.lower << 32 : st.lower;
+            st.range = sh ? st.range << 32 : st.range;
+            st.point = sh ? (st.point << 32) | (uint64_t)wa : st.point;
+            st.read_idx += (sh && st.read_idx < nw) ? 1 : 0;
             if (st.read_idx - base >= S) {
                 base += S;
                 w0 = w1;

@@ -1,6 +1,7 @@
 // CPU check of the product range-coder core (boa-constrictor_amd/csrc/rc_core.h, the exact code the kernels
 // run), built with g++ under AddressSanitizer and UndefinedBehaviorSanitizer by tests/test_coder_host.py.
-//   1. dec_target (fp64 quotient estimate + one integer correction) equals the exact u64 quotient
+//   1. dec_target (fp64 quotient estimate + one integer correction), and at P = 16 dec_target16 (fp32
+//      estimate + the same correction), equal the exact u64 quotient
 //      min((point - lower) / (range >> P), 2^P - 1) of gpu_range_coder.py:191-194 on random decoder states,
 //      on corrupt-stream states (point - lower anywhere in [0, 2^64)), and on boundary states (scale 2^8,
 //      d at and next to multiples of scale, d near 2^P * scale, the largest d and range);
@@ -47,6 +48,13 @@ void check_target(uint64_t lower, uint64_t range, uint64_t point, int P) {
         std::printf("dec_target mismatch P=%d lower=%llu range=%llu point=%llu: got %u want %llu\n", P,
                     (unsigned long long)lower, (unsigned long long)range, (unsigned long long)point, got,
                     (unsigned long long)q);
+    if (P <= 16) {
+        const uint32_t g16 = boa::dec_target16(st, P);
+        if (g16 != (uint32_t)q && fails++ < 5)
+            std::printf("dec_target16 mismatch P=%d lower=%llu range=%llu point=%llu: got %u want %llu\n", P,
+                        (unsigned long long)lower, (unsigned long long)range, (unsigned long long)point, g16,
+                        (unsigned long long)q);
+    }
 }
 
 void targets() {
