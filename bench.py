@@ -45,10 +45,10 @@ TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_fused_step_d256x8L_4096la
 
 # rocprof names of the kernel instances each profiled class launches at the benchmark's shapes, default
 # precision bf16x3 (k_gemm_bf<BM, BN, BK, EPI, NT, A split, C split>: EPI 0 none, 1 bias, 2 GELU, 4 residual;
-# k_ffn: LN2 + FF1 + GELU + FF2 + residual in one kernel)
+# k_ffn<NT, true>: out_proj + LN2 + FF1 + GELU + FF2 + residual in one kernel; k_head_xq: head + quantiser)
 KERNEL_NAMES = {
     ("compress", "gemm_in_proj"): "k_gemm_bf<128, 128, 32, 1, 3, true, false>",
-    ("compress", "ffn"): "k_ffn<3>",
+    ("compress", "ffn"): "k_ffn<3, true>",
     ("compress", "mixin"): "k_mixin<3>",
     ("compress", "gemm_out_proj"): "k_gemm_bf<128, 128, 32, 1, 3, true, false>",
     ("compress", "gemm_x_proj"): "k_xproj<3, 3>",
@@ -169,7 +169,7 @@ def coder_bench(args, steps: int, warmup: int, cpu_streams: int) -> dict:
     # decode reads each step's full table row (K entries, 2 B) + writes 1 B; encode reads 2 entries + 1 B
     dec_bytes = nsym * (2.0 * K + 1) + code_bytes
     enc_bytes = nsym * (2.0 * 2 + 1) + code_bytes
-    roofline = {"bound": "hbm", "kernel": "k_rc_decode_tables", "achieved": dec_bytes / t_d / 1e9,
+    roofline = {"bound": "hbm", "kernel": "k_rc_decode_tables4<16, unsigned short, 16, 4>", "achieved": dec_bytes / t_d / 1e9,
                 "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": dec_bytes / t_d / 1e9 / PEAK_HBM_GBPS, "traffic": None,
                 "avg_launch_ms": t_d * 1e3, "algorithmic_per_launch": dec_bytes}
     cpu = None
