@@ -2306,7 +2306,9 @@ extern "C" int64_t boa_ctx_device_bytes(const boa_ctx* ctx) { return ctx ? ctx->
 // Whether a context of this shape and precision decodes through k_fused_step (BOA_FUSED_STEP=0 turns it off).
 static bool want_fused(const boa_model_cfg& c, int R, int precision) {
     const char* fenv = getenv("BOA_FUSED_STEP");
-    return precision != BOA_PREC_F32 && fused_step_supported(c.d_model, c.d_state, R, c.d_conv, c.vocab) &&
+    return precision != BOA_PREC_F32 &&
+           (fused_step_supported(c.d_model, c.d_state, R, c.d_conv, c.vocab) ||
+            fused_step512_supported(c.d_model, c.d_state, R, c.d_conv, c.vocab)) &&
            !(fenv && fenv[0] == '0');
 }
 
@@ -2966,8 +2968,14 @@ static FusedArgs fused_args(boa_ctx* x, int32_t lanes, const int32_t* tokens_in)
     a.max_lanes = x->max_lanes;
     a.emb = x->emb; a.h1_b = x->h1_b; a.h2_b = x->h2_b; a.h1_p = x->h1_w.p; a.h2_p = x->h2_w.p;
     a.ssm = x->ssm; a.hist = x->conv_hist; a.tokens_in = tokens_in;
+    a.resid = x->x; a.scr = x->xz;  // per-lane scratch rows of the d_model 512 kernel (row = lane)
     a.nsteps = 1;
     return a;
+}
+
+static hipError_t launch_fused(const boa_ctx* x, const FusedArgs& a, hipStream_t s) {
+    const int nt = x->prec == BOA_PREC_BF16X3 ? 3 : 2;
+    return x->d == 512 ? launch_fused_step512(a, nt, s) : launch_fused_step(a, nt, s);
 }
 
 // Compulsory HBM bytes of one fused step: SSM state read + write, conv history (3 reads, 1 write), input
@@ -2999,7 +3007,7 @@ extern "C" int boa_model_step(boa_ctx* x, const int32_t* d_tokens, int32_t lanes
         a.logits = d_logits;
         hipError_t e = hipSuccess;
         PROF(PC_FUSED, fused_flops(x, lanes), fused_bytes(x, lanes),
-             e = launch_fused_step(a, x->prec == BOA_PREC_BF16X3 ? 3 : 2, x->stream));
+             e = launch_fused(x, a, x->stream));
         if (e != hipSuccess) return boa_fail_hip(e, "k_fused_step", __FILE__, __LINE__);
         x->pos += 1;
         return BOA_OK;
@@ -3189,7 +3197,7 @@ extern "C" int boa_decompress(boa_ctx* x, const uint32_t* d_payload, const int64
             a.nwords = d_nwords; a.tokens_out = x->tokens; a.out = d_out; a.out_stride = out_stride;
             hipError_t e = hipSuccess;
             PROF(PC_FUSED, a.nsteps * fused_flops(x, lanes), a.nsteps * fused_bytes(x, lanes),
-                 e = launch_fused_step(a, x->prec == BOA_PREC_BF16X3 ? 3 : 2, s));
+                 e = launch_fused(x, a, s));
             if (e != hipSuccess) return boa_fail_hip(e, "k_fused_step", __FILE__, __LINE__);
             x->pos += a.nsteps;
         }

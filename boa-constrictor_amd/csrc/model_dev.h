@@ -222,14 +222,19 @@ __device__ __forceinline__ float conv_point(const float4 w, float bias, float h0
 //   h_n <- exp(dt * A_n) * h_n + B_n * (dt * x) ;  with a[n] = A_n * log2(e) so exp(dt*A_n) = exp2(dt*a[n])
 //   y = sum_n h_n * C_n + D * x ;  y <- y * SiLU(z)
 // row = [dr (R) | B (NS) | C (NS)] of the position.
-template <int NS, int R>
-__device__ __forceinline__ float scan_position(const float* row, const float (&wr)[R], float bdt, const float (&a)[NS],
-                                               float Dc, float x, float z, float (&h)[NS]) {
+// The two halves of a position, for callers that compute dt ahead of the state update (same operations):
+// scan_dt: dt of the position (uses row[0 .. R-1]); scan_update: state update, output and gate.
+template <int R>
+__device__ __forceinline__ float scan_dt(const float* row, const float (&wr)[R], float bdt) {
     float dt = 0.0f;
 #pragma unroll
     for (int r = 0; r < R; ++r) dt = __builtin_fmaf(row[r], wr[r], dt);
     dt = dt + bdt;
-    dt = hw_softplus(dt);
+    return hw_softplus(dt);
+}
+template <int NS, int R>
+__device__ __forceinline__ float scan_update(const float* row, float dt, const float (&a)[NS], float Dc, float x, float z,
+                                             float (&h)[NS]) {
     float y = 0.0f;
     const float dtx = dt * x;
 #pragma unroll
@@ -241,6 +246,11 @@ __device__ __forceinline__ float scan_position(const float* row, const float (&w
     }
     y = __builtin_fmaf(Dc, x, y);
     return y * hw_silu(z);
+}
+template <int NS, int R>
+__device__ __forceinline__ float scan_position(const float* row, const float (&wr)[R], float bdt, const float (&a)[NS],
+                                               float Dc, float x, float z, float (&h)[NS]) {
+    return scan_update<NS, R>(row, scan_dt<R>(row, wr, bdt), a, Dc, x, z, h);
 }
 
 // Logits of one lane (a V-wide row) as held by one wavefront: lane j gets elements 4j .. 4j + 3 (0 beyond V).

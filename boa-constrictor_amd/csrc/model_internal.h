@@ -1,5 +1,5 @@
-// Host/device interface between the model context (model.hip) and the fused decompress-step kernel
-// (fused_step.hip).  Internal to libboa_hip.so.
+// Host/device interface between the model context (model.hip) and the fused decompress-step kernels
+// (fused_step.hip for d_model 256, fused_step512.hip for d_model 512).  Internal to libboa_hip.so.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -47,6 +47,10 @@ struct FusedArgs {
     int32_t* tokens_out;
     uint8_t* out;
     int64_t out_stride;
+    // d_model 512 kernel only: per-lane scratch in device memory (the context's workspace rows, row = lane):
+    // the residual stream [lanes][d_model] and the mixer's z | conv output [lanes][2 d_inner]
+    float* resid;
+    float* scr;
 };
 
 // Supported shape of the fused kernel: d_model 256, d_state 16, dt_rank 16, d_conv 4, vocab % 16 == 0.
@@ -54,5 +58,10 @@ bool fused_step_supported(int d_model, int d_state, int dt_rank, int d_conv, int
 
 // nt = 3 (bf16x3 weights, hi + lo) or 2 (bf16 weights); 512 threads per workgroup of 16 lanes
 hipError_t launch_fused_step(const FusedArgs& a, int nt, hipStream_t s);
+
+// The d_model 512 form (d_inner 1024, d_state 16, dt_rank 32, d_conv 4, vocab 256): 512 threads (8 waves) per
+// workgroup of 32 lanes, one workgroup per CU (256 VGPRs per thread, 80 KB of LDS).
+bool fused_step512_supported(int d_model, int d_state, int dt_rank, int d_conv, int vocab);
+hipError_t launch_fused_step512(const FusedArgs& a, int nt, hipStream_t s);
 
 }  // namespace boa

@@ -174,12 +174,12 @@ def _stream_logits(m, tok, fused):
     return torch.stack([m.step(tok[:, t], inf) for t in range(tok.shape[1])], dim=1)
 
 
-@pytest.mark.parametrize("precision", ["bf16x3", "bf16w"])
-def test_fused_step_matches_layer_kernels(gpu, precision):
-    """The one-launch decompress step (16 lanes per workgroup, activations in LDS) against the per-layer
-    step kernels: identical bits, including a partial last workgroup (37 lanes) and > 3 positions (the conv
-    history ring wraps)."""
-    m, ref = _model(8, precision=precision)
+@pytest.mark.parametrize("d,precision", [(256, "bf16x3"), (256, "bf16w"), (512, "bf16w"), (512, "bf16x3")])
+def test_fused_step_matches_layer_kernels(gpu, d, precision):
+    """The one-launch decompress step (d_model 256: 16 lanes per workgroup, activations in LDS; d_model 512:
+    32 lanes per workgroup, chunked, with per-lane scratch) against the per-layer step kernels: identical bits,
+    including a partial last workgroup (37 lanes) and > 3 positions (the conv history ring wraps)."""
+    m, ref = _model(8 if d == 256 else 2, seed=0 if d == 256 else 1, d=d, precision=precision)
     tok = torch.from_numpy(np.random.default_rng(11).integers(0, 256, (37, 9))).cuda()
     a = _stream_logits(m, tok, fused=True)
     b = _stream_logits(m, tok, fused=False)
@@ -191,8 +191,8 @@ def test_fused_step_matches_layer_kernels(gpu, precision):
 @pytest.mark.parametrize("precision", ["bf16w", "bf16x3"])
 def test_d512_config4_shape_vs_oracle_and_identity(gpu, precision):
     """configs[4] shape (d_model 512, d_inner 1024, dt_rank 32), bf16 weights: logits vs the oracle with the
-    same bf16-rounded weights, and the decode path (per-layer step kernels; the fused step kernel covers
-    d_model 256 only) equal to the teacher-forced tile path bit for bit."""
+    same bf16-rounded weights, and the decode path (the fused d_model 512 step kernel) equal to the
+    teacher-forced tile path bit for bit."""
     m, ref = _model(2, seed=1, d=512, precision=precision)
     rng = np.random.default_rng(21)
     B, T = 20, 70  # > one 64-position tile
