@@ -106,11 +106,15 @@ def test_boa_file_round_trip(gpu, tmp_path):
         del os.environ["BOA_GPU_STREAMS"]
 
 
-@pytest.mark.parametrize("d_model,precision", [(256, "bf16x3"), (512, "bf16w"), (512, "bf16x3")])
-def test_decompress_fused_and_layer_kernels_agree(gpu, d_model, precision):
+@pytest.mark.parametrize("d_model,precision,steps", [(256, "bf16x3", None), (512, "bf16w", None),
+                                                     (512, "bf16x3", None), (256, "bf16x3", "5"),
+                                                     (512, "bf16w", "5")])
+def test_decompress_fused_and_layer_kernels_agree(gpu, d_model, precision, steps):
     """Decompression through the fused step kernel and through the per-layer kernels gives the same bytes
     (both must reproduce the compressor's logits bit for bit to decode at all).  At d_model 512 the 70 ragged
-    lanes span three 32-lane workgroups, the last one partly filled, and lanes end at different positions."""
+    lanes span three 32-lane workgroups, the last one partly filled, and lanes end at different positions.
+    steps: decode steps per fused launch (BOA_FUSED_STEPS_PER_LAUNCH; default 128), so that the conv history
+    ring position and the fed-back bytes carry across many launch boundaries."""
     import codec
     from boa_amd import weights as W
 
@@ -129,11 +133,14 @@ def test_decompress_fused_and_layer_kernels_agree(gpu, d_model, precision):
     outs = []
     for flag in ("1", "0"):
         os.environ["BOA_FUSED_STEP"] = flag
+        if steps:
+            os.environ["BOA_FUSED_STEPS_PER_LAUNCH"] = steps
         try:
             m.release_engines()
             outs.append(codec.decompress_payload(m, payload, nw, Ls, fb))
         finally:
             del os.environ["BOA_FUSED_STEP"]
+            os.environ.pop("BOA_FUSED_STEPS_PER_LAUNCH", None)
     m.release_engines()
     for out in outs:
         for i, c in enumerate(chunks):
