@@ -18,6 +18,10 @@
 // split-precision GEMM does, and every elementwise phase calls the same device function as the tiled
 // path (model_dev.h).  The logits of a lane are therefore bit-identical to those the compress path
 // computes for the same position, which the decoder depends on.
+// NT = 1 is the fp32 precision mode: the GEMM operands are fp32 in LDS (the same regions, rows 4 elements
+// shorter) and every output accumulates 16-wide K groups of four v_mfma_f32_16x16x4_f32 in ascending order,
+// lane l supplying k = 16 g + 4 (l / 16) + j to the j-th, exactly as the tiled fp32 GEMM (k_gemm) does; x_proj
+// is one ascending accumulation over all 512 channels (no K-block fold), as that GEMM computes it.
 #include "model_dev.h"
 #include "model_internal.h"
 
@@ -37,6 +41,9 @@ constexpr int LA = FDI + 8;         // split operand rows, K <= 512 (bf16 elemen
 constexpr int LXZ = 2 * FDI + 4;    // in_proj output rows (fp32)
 constexpr int LH = 4 * FD + 8;      // FF hidden split rows, K = 1024 (bf16 elements)
 constexpr int LH1 = FD + 8;         // head hidden split rows, K = 256
+// fp32 operand rows (NT = 1) in the same regions: 4 elements shorter, 4 mod 64 words, so that 16-row float4
+// reads are free of bank conflicts
+constexpr int ld32(int LD) { return LD - 4; }
 
 constexpr int SZ_RES = ROWS * LRES * 4;
 constexpr int SZ_A = 2 * ROWS * LA * 2;
@@ -64,10 +71,63 @@ __device__ __forceinline__ int frag_of(int f0, int wave, int j, int nfrag, int r
     return f >= nfrag ? f - nfrag : f;
 }
 
+// The fp32 form (NT = 1): A fp32 in LDS (row stride lda), W from fp32 fragment-packed blocks (block (f, g): lane
+// l holds W[16 f + l % 16][16 g + 4 (l / 16) + j], j < 4, one 16-byte load).  Each output accumulates its 16-K
+// groups in ascending order, the j-th MFMA of group g taking k = 16 g + 4 (l / 16) + j from lane l, which is
+// k_gemm's order.  RD groups are in flight through a register ring; the loop runs over passes of RD groups so
+// that every ring slot is fixed per unrolled position, and the last prefetches are clamped to the last group
+// (reloads, unused) instead of sitting under a branch.
+template <int NWAVE, int FPW, int K>
+__device__ __forceinline__ void mgemm_f32(const float* A, int lda, const float* __restrict__ Wp, int f0, int nfrag,
+                                          int wave, int lane, int rot, floatx4 (&acc)[FPW]) {
+    constexpr int S = K / 16, RD = 4;
+    static_assert(S % RD == 0, "whole passes of the register ring");
+    const int kq = 4 * (lane >> 4), ar = lane & 15;
+    const int fw = f0 + wave;
+#pragma unroll
+    for (int j = 0; j < FPW; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float4 bw[RD][FPW];
+    auto load = [&](int g, int slot) {
+#pragma unroll
+        for (int j = 0; j < FPW; ++j) {
+            if (fw + NWAVE * j < nfrag) {
+                const int f = frag_of<NWAVE>(f0, wave, j, nfrag, rot);
+                bw[slot][j] = ldg_f4(G(Wp) + ((int64_t)f * S + g) * 256 + lane * 4);
+            }
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < RD - 1; ++i) load(i, i);
+#pragma unroll 1
+    for (int g0 = 0; g0 < S; g0 += RD) {
+#pragma unroll
+        for (int i = 0; i < RD; ++i) {
+            const int gn = g0 + i + RD - 1;
+            load(gn < S ? gn : S - 1, (i + RD - 1) % RD);
+            const float4 a = *reinterpret_cast<const float4*>(A + ar * lda + 16 * (g0 + i) + kq);
+#pragma unroll
+            for (int j = 0; j < FPW; ++j) {
+                if (fw + NWAVE * j < nfrag) {
+                    const float4 b = bw[i][j];
+                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, acc[j], 0, 0, 0);
+                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, acc[j], 0, 0, 0);
+                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, acc[j], 0, 0, 0);
+                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, acc[j], 0, 0, 0);
+                }
+            }
+        }
+    }
+}
+
 template <int NT, int NWAVE, int FPW, int K, int D>
 __device__ __forceinline__ void mgemm(const uint16_t* sAh, const uint16_t* sAl, int lda,
                                       const uint16_t* __restrict__ Wp, int f0, int nfrag, int wave, int lane,
                                       int rot, floatx4 (&acc)[FPW]) {
+    if constexpr (NT == 1) {
+        mgemm_f32<NWAVE, FPW, K>(reinterpret_cast<const float*>(sAh), ld32(lda), reinterpret_cast<const float*>(Wp),
+                                 f0, nfrag, wave, lane, rot, acc);
+        return;
+    }
     constexpr int BLK = (NT == 3) ? 1024 : 512;
     constexpr int S = K / 32;
     const int kq = 8 * (lane >> 4), ar = lane & 15;
@@ -115,10 +175,18 @@ __device__ __forceinline__ void put_split(uint16_t* h, uint16_t* l, int idx, flo
     l[idx] = (uint16_t)lo;
 }
 
+// GEMM operand regions: split bf16 rows of LD elements (hi array, then lo array at h + ROWS * LD), or with
+// NT = 1 fp32 rows of ld32(LD) elements over the same bytes.
+template <int NT, int LD>
+__device__ __forceinline__ void store_op(uint16_t* h, int r, int c, float v) {
+    if constexpr (NT == 1) reinterpret_cast<float*>(h)[r * ld32(LD) + c] = v;
+    else put_split(h, h + ROWS * LD, r * LD + c, v);
+}
+
 // LayerNorm of rows RPW*wave .. RPW*wave + RPW-1 of src (fp32, stride LRES) into the split operand (stride LA).
 // wv, bv: this lane's 4 weights and biases, loaded by the caller ahead of the barrier before the LN phase, so
 // their L2 round trip (behind the pointer load from the layer table) overlaps the previous phase's tail.
-template <int RPW>
+template <int NT, int RPW>
 __device__ __forceinline__ void ln_rows(const float* src, float4 wv, float4 bv, uint16_t* sAh, uint16_t* sAl, int wave,
                                        int lane) {
 #pragma unroll
@@ -130,10 +198,15 @@ __device__ __forceinline__ void ln_rows(const float* src, float4 wv, float4 bv, 
         ln_stats_row<1>(v, mu, rs);
         const float y[4] = {ln_apply(v[0], mu, rs, wv.x, bv.x), ln_apply(v[1], mu, rs, wv.y, bv.y),
                             ln_apply(v[2], mu, rs, wv.z, bv.z), ln_apply(v[3], mu, rs, wv.w, bv.w)};
-        uint2 hp, lp;
-        split4(y[0], y[1], y[2], y[3], hp, lp);
-        *reinterpret_cast<uint2*>(sAh + r * LA + 4 * lane) = hp;
-        *reinterpret_cast<uint2*>(sAl + r * LA + 4 * lane) = lp;
+        if constexpr (NT == 1) {
+            *reinterpret_cast<float4*>(reinterpret_cast<float*>(sAh) + r * ld32(LA) + 4 * lane) =
+                make_float4(y[0], y[1], y[2], y[3]);
+        } else {
+            uint2 hp, lp;
+            split4(y[0], y[1], y[2], y[3], hp, lp);
+            *reinterpret_cast<uint2*>(sAh + r * LA + 4 * lane) = hp;
+            *reinterpret_cast<uint2*>(sAl + r * LA + 4 * lane) = lp;
+        }
     }
 }
 
@@ -222,7 +295,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
     for (int l = 0; l < a.L; ++l) {
         const FusedLayer& w = a.layers[l];
         // ---- LN1 -> split operand
-        ln_rows<RPW>(sRes, lnw, lnb, sAh, sAl, wave, lane);
+        ln_rows<NT, RPW>(sRes, lnw, lnb, sAh, sAl, wave, lane);
         __syncthreads();
         // ---- in_proj (+bias) -> xz fp32
 #pragma unroll 1
@@ -247,15 +320,17 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
             // x_proj weight blocks of this wave's K block, issued first (they do not depend on the step)
             constexpr int XS = FDI / 32, XF = FW / 16, XBLK = (NT == 3) ? 1024 : 512;
             uint4 xwh[XF][2], xwl[XF][2];
+            if constexpr (NT != 1) {
 #pragma unroll
-            for (int f = 0; f < XF; ++f)
+                for (int f = 0; f < XF; ++f)
 #pragma unroll
-                for (int s = 0; s < 2; ++s) {
-                    const gptr<uint16_t> p = G(w.x_p) + ((int64_t)f * XS + 2 * wave + s) * XBLK + lane * 8;
-                    xwh[f][s] = __builtin_bit_cast(uint4, ldg16(p));
-                    xwl[f][s] = xwh[f][s];
-                    if constexpr (NT == 3) xwl[f][s] = __builtin_bit_cast(uint4, ldg16(p + 512));
-                }
+                    for (int s = 0; s < 2; ++s) {
+                        const gptr<uint16_t> p = G(w.x_p) + ((int64_t)f * XS + 2 * wave + s) * XBLK + lane * 8;
+                        xwh[f][s] = __builtin_bit_cast(uint4, ldg16(p));
+                        xwl[f][s] = xwh[f][s];
+                        if constexpr (NT == 3) xwl[f][s] = __builtin_bit_cast(uint4, ldg16(p + 512));
+                    }
+            }
             const int c = tid;
             const float4 cw = ldg_f4(G(w.conv_w) + 4 * c);
             const float cb = G(w.conv_b)[c];
@@ -284,42 +359,55 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
                 const float x = sX[r * LXZ + cq];
                 const float y = conv_point(cw, cb, h0[r], h1[r], h2[r], x);
                 sX[r * LXZ + cq] = y;
-                put_split(sAh, sAl, r * LA + cq, y);
+                store_op<NT, LA>(sAh, r, cq, y);
                 buf_st1(hr3, (uint32_t)(r * 3 * FDI + p0m3 * FDI + cq) * 4, x);
             }
             // the partial reads only split values this wavefront wrote (channels 64 wave .. 64 wave + 63 of
             // every row); LDS operations of one wavefront complete in order
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            const int ar = lane & 15, kq = 8 * (lane >> 4);
-            floatx4 part[XF];
+            if constexpr (NT != 1) {
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                const int ar = lane & 15, kq = 8 * (lane >> 4);
+                floatx4 part[XF];
 #pragma unroll
-            for (int f = 0; f < XF; ++f) part[f] = floatx4{0.f, 0.f, 0.f, 0.f};
+                for (int f = 0; f < XF; ++f) part[f] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                const int k0 = XPROJ_KB * wave + 32 * s;
-                const bf16x8 ah = *reinterpret_cast<const bf16x8*>(sAh + ar * LA + k0 + kq);
-                const bf16x8 al = *reinterpret_cast<const bf16x8*>(sAl + ar * LA + k0 + kq);
+                for (int s = 0; s < 2; ++s) {
+                    const int k0 = XPROJ_KB * wave + 32 * s;
+                    const bf16x8 ah = *reinterpret_cast<const bf16x8*>(sAh + ar * LA + k0 + kq);
+                    const bf16x8 al = *reinterpret_cast<const bf16x8*>(sAl + ar * LA + k0 + kq);
+#pragma unroll
+                    for (int f = 0; f < XF; ++f)
+                        part[f] = mfma_split_step<NT>(part[f], ah, al, __builtin_bit_cast(bf16x8, xwh[f][s]),
+                                                      __builtin_bit_cast(bf16x8, xwl[f][s]));
+                }
+                float* pw = sPart + wave * (ROWS * FW);
 #pragma unroll
                 for (int f = 0; f < XF; ++f)
-                    part[f] = mfma_split_step<NT>(part[f], ah, al, __builtin_bit_cast(bf16x8, xwh[f][s]),
-                                                  __builtin_bit_cast(bf16x8, xwl[f][s]));
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) pw[(m_of + r) * FW + 16 * f + n_of] = part[f][r];
             }
-            float* pw = sPart + wave * (ROWS * FW);
-#pragma unroll
-            for (int f = 0; f < XF; ++f)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) pw[(m_of + r) * FW + 16 * f + n_of] = part[f][r];
         }
         __syncthreads();
-        // ---- x_proj fold: dbc = P_0 + P_1 + ... + P_7, in place of P_0 (element i is read and written by
-        //      one thread only)
-        for (int i = tid; i < ROWS * FW; i += NTHR) {
-            float v = sPart[i];
+        if constexpr (NT == 1) {
+            // ---- x_proj over all 512 channels at once (fp32 mode: one ascending accumulation per output):
+            //      waves 0..2 own output fragments 0..2
+            floatx4 acc[1];
+            mgemm<NT, NWAVE, 1, FDI, 4>(sAh, sAl, LA, w.x_p, 0, FW / 16, wave, lane, 0, acc);
+            if (wave < FW / 16) {
 #pragma unroll
-            for (int q = 1; q < FDI / XPROJ_KB; ++q) v = v + sPart[q * (ROWS * FW) + i];
-            sDbc[i] = v;
+                for (int r = 0; r < 4; ++r) sDbc[(m_of + r) * FW + 16 * wave + n_of] = acc[0][r];
+            }
+        } else {
+            // ---- x_proj fold: dbc = P_0 + P_1 + ... + P_7, in place of P_0 (element i is read and written by
+            //      one thread only)
+            for (int i = tid; i < ROWS * FW; i += NTHR) {
+                float v = sPart[i];
+#pragma unroll
+                for (int q = 1; q < FDI / XPROJ_KB; ++q) v = v + sPart[q * (ROWS * FW) + i];
+                sDbc[i] = v;
+            }
         }
         __syncthreads();
         // ---- dt_proj + softplus + selective scan + D + gate (thread = channel) -> y split operand
@@ -362,7 +450,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
                 __builtin_amdgcn_sched_barrier(0);
                 const float x = sX[r * LXZ + cq], z = sX[r * LXZ + FDI + cq];
                 const float y = scan_position<FNS, FR>(sDbc + r * FW, wr, bdt, av, Dc, x, z, h);
-                put_split(sAh, sAl, r * LA + cq, y);
+                store_op<NT, LA>(sAh, r, cq, y);
 #pragma unroll
                 for (int n = 0; n < FNS; n += 4)
                     buf_st4(sr, h_off(r, n, cq), f32x4{h[n], h[n + 1], h[n + 2], h[n + 3]});
@@ -388,7 +476,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
         lnb = ldg_f4(G(w.ln2_b) + 4 * lane);
         __syncthreads();
         // ---- LN2 -> split operand
-        ln_rows<RPW>(sX, lnw, lnb, sAh, sAl, wave, lane);
+        ln_rows<NT, RPW>(sX, lnw, lnb, sAh, sAl, wave, lane);
         __syncthreads();
         // ---- FF1 (+bias, GELU) -> hidden split (xz region)
 #pragma unroll 1
@@ -403,7 +491,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
                 const int n = 16 * frag_of<NWAVE>(f0, wave, j, 4 * FD / 16, rot64) + n_of;
                 const float bias = bias_j[j];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) put_split(sHh, sHl, (m_of + r) * LH + n, epi_value<EPI_GELU>(acc[j][r], bias));
+                for (int r = 0; r < 4; ++r) store_op<NT, LH>(sHh, m_of + r, n, epi_value<EPI_GELU>(acc[j][r], bias));
             }
         }
         __syncthreads();
@@ -436,7 +524,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
     // ---- head: Linear -> ReLU -> Linear (model.py:95, 101)
     for (int i = tid; i < ROWS * FD; i += NTHR) {
         const int r = i / FD, c = i % FD;
-        put_split(sAh, sAl, r * LA + c, sRes[r * LRES + c]);
+        store_op<NT, LA>(sAh, r, c, sRes[r * LRES + c]);
     }
     __syncthreads();
     uint16_t* sGh = sHh;
@@ -449,7 +537,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
             const int n = 16 * frag_of<NWAVE>(0, wave, j, FD / 16, rot16) + n_of;
             const float bias = G(a.h1_b)[n];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) put_split(sGh, sGl, (m_of + r) * LH1 + n, epi_value<EPI_RELU>(acc[j][r], bias));
+            for (int r = 0; r < 4; ++r) store_op<NT, LH1>(sGh, m_of + r, n, epi_value<EPI_RELU>(acc[j][r], bias));
         }
     }
     __syncthreads();
@@ -505,7 +593,8 @@ bool fused_step_supported(int d_model, int d_state, int dt_rank, int d_conv, int
 hipError_t launch_fused_step(const FusedArgs& a, int nt, hipStream_t s) {
     const dim3 grid((unsigned)((a.B + ROWS - 1) / ROWS));
     if (nt == 3) hipLaunchKernelGGL((k_fused_step<3, 512>), grid, dim3(512), 0, s, a);
-    else hipLaunchKernelGGL((k_fused_step<2, 512>), grid, dim3(512), 0, s, a);
+    else if (nt == 2) hipLaunchKernelGGL((k_fused_step<2, 512>), grid, dim3(512), 0, s, a);
+    else hipLaunchKernelGGL((k_fused_step<1, 512>), grid, dim3(512), 0, s, a);
     return hipGetLastError();
 }
 

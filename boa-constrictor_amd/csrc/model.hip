@@ -2303,13 +2303,13 @@ extern "C" int64_t boa_weights_nbytes(const boa_model_cfg* cfg) {
 
 extern "C" int64_t boa_ctx_device_bytes(const boa_ctx* ctx) { return ctx ? ctx->device_bytes : 0; }
 
-// Whether a context of this shape and precision decodes through k_fused_step (BOA_FUSED_STEP=0 turns it off).
+// Whether a context of this shape and precision decodes through a fused step kernel (BOA_FUSED_STEP=0 turns it
+// off): k_fused_step at d_model 256 in every precision mode, k_fused_step512 at d_model 512 in the split modes.
 static bool want_fused(const boa_model_cfg& c, int R, int precision) {
     const char* fenv = getenv("BOA_FUSED_STEP");
-    return precision != BOA_PREC_F32 &&
-           (fused_step_supported(c.d_model, c.d_state, R, c.d_conv, c.vocab) ||
-            fused_step512_supported(c.d_model, c.d_state, R, c.d_conv, c.vocab)) &&
-           !(fenv && fenv[0] == '0');
+    const bool d256 = fused_step_supported(c.d_model, c.d_state, R, c.d_conv, c.vocab);
+    const bool d512 = fused_step512_supported(c.d_model, c.d_state, R, c.d_conv, c.vocab);
+    return (d256 || (d512 && precision != BOA_PREC_F32)) && !(fenv && fenv[0] == '0');
 }
 
 // Device bytes boa_ctx_create allocates for this shape: the same list of buffers, in the same order, each
@@ -2323,12 +2323,14 @@ static int64_t ctx_plan_bytes(const boa_model_cfg& c, int R, int precision, int6
                 f4(rows * d) + f4(rows * V) + 8 * std::max<int64_t>(rows, 1);
     if (precision != BOA_PREC_F32) b += 2 * 2 * std::max<int64_t>(rows * std::max(d, di), 1);
     b += f4(max_lanes) + (int64_t)sizeof(EncState) * max_lanes + (int64_t)sizeof(DecState) * max_lanes + 4;
+    const int64_t mats = L * (2 * di * d + (R + 2 * NS) * di + d * di + 4 * d * d + 4 * d * d) + d * d + V * d;
     if (precision != BOA_PREC_F32) {
-        int64_t mats = L * (2 * di * d + (R + 2 * NS) * di + d * di + 4 * d * d + 4 * d * d) + d * d + V * d;
         b += 2 * std::max<int64_t>(2 * mats, 1);
         b += 2 * std::max<int64_t>((precision == BOA_PREC_BF16X3 ? 2 : 1) * mats, 1);
-        if (want_fused(c, R, precision)) b += (int64_t)sizeof(FusedLayer) * L;
+    } else if (want_fused(c, R, precision)) {
+        b += 2 * std::max<int64_t>(2 * mats, 1);  // fp32 fragment-packed weights, in 16-bit units
     }
+    if (want_fused(c, R, precision)) b += (int64_t)sizeof(FusedLayer) * L;
     return b;
 }
 
@@ -2382,6 +2384,19 @@ static float host_bf16_to_f(uint16_t h) {
     float f;
     memcpy(&f, &u, 4);
     return f;
+}
+
+// The fp32 fragment order of the fused decode kernel's fp32 mode: blocks (f, g) for f < N/16, g < K/16, f-major;
+// lane l of a block holds W[16 f + l % 16][16 g + 4 (l / 16) + j], j < 4 (one 16-byte load per lane).
+static void pack_fragments_f32(const float* w, int N, int K, float* out) {
+    const int S = K / 16;
+    for (int f = 0; f < N / 16; ++f)
+        for (int g = 0; g < S; ++g) {
+            float* o = out + ((int64_t)f * S + g) * 256;
+            for (int l = 0; l < 64; ++l)
+                for (int j = 0; j < 4; ++j)
+                    o[l * 4 + j] = w[(int64_t)(16 * f + (l & 15)) * K + 16 * g + 4 * (l >> 4) + j];
+        }
 }
 
 // Fragment order for the fused kernel's B operands (layout in model_internal.h).
@@ -2494,16 +2509,24 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
         boa_ctx_destroy(x);
         return boa_fail(BOA_ERR_ARG, "internal: weight layout mismatch (%lld vs %lld)", (long long)o, (long long)nf);
     }
-    // split-precision modes: bf16 parts of every GEMM matrix, [hi | lo] per matrix
+    // GEMM weight copies for the MFMA kernels.  Split-precision modes: bf16 parts of every matrix ([hi | lo] per
+    // matrix) and their fragment-packed form, read by the fused compress kernels (k_mixin, k_ffn, k_ffn512,
+    // k_head_xq) and the fused decode kernels.  fp32 mode with the fused decode kernel: the fp32 fragment-packed
+    // form.
     std::vector<uint16_t> split_host, frag_host;
+    std::vector<float> frag32_host;
     std::vector<FusedLayer> layers_host;
+    std::vector<MatW*> mats;
+    for (auto& w : x->layers) { mats.push_back(&w.in_w); mats.push_back(&w.x_w); mats.push_back(&w.out_w);
+                                mats.push_back(&w.ff1_w); mats.push_back(&w.ff2_w); }
+    mats.push_back(&x->h1_w);
+    mats.push_back(&x->h2_w);
+    x->fused = want_fused(c, R, x->prec);
+    if (const char* v = getenv("BOA_FUSED_STEPS_PER_LAUNCH")) x->fused_steps = std::max(1, atoi(v));
+    if (const char* v = getenv("BOA_FUSED_STAGGER_US")) x->stagger_us = std::max(0, atoi(v));
+    if (const char* v = getenv("BOA_FUSED_STAGGER_CLASSES")) x->stagger_classes = std::min(8, std::max(1, atoi(v)));
     if (x->prec != BOA_PREC_F32) {
         int64_t total = 0;
-        std::vector<MatW*> mats;
-        for (auto& w : x->layers) { mats.push_back(&w.in_w); mats.push_back(&w.x_w); mats.push_back(&w.out_w);
-                                    mats.push_back(&w.ff1_w); mats.push_back(&w.ff2_w); }
-        mats.push_back(&x->h1_w);
-        mats.push_back(&x->h2_w);
         for (MatW* m : mats) total += 2 * m->n;
         if (e == hipSuccess) e = dmalloc(x, &x->wsplit, total);
         if (e != hipSuccess) {
@@ -2524,47 +2547,52 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
             m->l = (x->prec == BOA_PREC_BF16X3) ? x->wsplit + so + m->n : nullptr;
             so += 2 * m->n;
         }
-        x->fused = want_fused(c, R, x->prec);
-        if (const char* v = getenv("BOA_FUSED_STEPS_PER_LAUNCH")) x->fused_steps = std::max(1, atoi(v));
-        if (const char* v = getenv("BOA_FUSED_STAGGER_US")) x->stagger_us = std::max(0, atoi(v));
-        if (const char* v = getenv("BOA_FUSED_STAGGER_CLASSES")) x->stagger_classes = std::min(8, std::max(1, atoi(v)));
-        // fragment-packed parts of every GEMM matrix: read by the fused compress kernels (k_mixin, k_ffn,
-        // k_ffn512) and the fused decode kernel
-        {
-            const bool two = x->prec == BOA_PREC_BF16X3;
-            int64_t ftotal = 0;
-            for (MatW* m : mats) ftotal += (two ? 2 : 1) * m->n;
-            frag_host.resize((size_t)ftotal);
-            if (e == hipSuccess) e = dmalloc(x, &x->wfrag, ftotal);
-            if (e == hipSuccess && x->fused) e = dmalloc(x, &x->d_layers, (int64_t)L);
-            if (e != hipSuccess) {
-                boa_ctx_destroy(x);
-                return boa_fail_hip(e, "boa_ctx_create allocation", __FILE__, __LINE__);
-            }
-            int64_t fo = 0, hs = 0;
-            for (MatW* m : mats) {
-                const uint16_t* hi = split_host.data() + hs;
-                pack_fragments(hi, hi + m->n, m->N, m->K, two, frag_host.data() + fo);
-                m->p = x->wfrag + fo;
-                fo += (two ? 2 : 1) * m->n;
-                hs += 2 * m->n;
-            }
-            if (x->fused) layers_host.resize((size_t)L);
-            for (int l = 0; l < (x->fused ? L : 0); ++l) {
-                const LayerW& w = x->layers[l];
-                FusedLayer& f = layers_host[(size_t)l];
-                f.ln1_w = w.ln1_w; f.ln1_b = w.ln1_b; f.in_b = w.in_b; f.conv_w = w.conv_w; f.conv_b = w.conv_b;
-                f.dt_w = w.dt_w; f.dt_b = w.dt_b; f.Aneg = w.Aneg; f.D = w.D; f.out_b = w.out_b;
-                f.ln2_w = w.ln2_w; f.ln2_b = w.ln2_b; f.ff1_b = w.ff1_b; f.ff2_b = w.ff2_b;
-                f.in_p = w.in_w.p; f.x_p = w.x_w.p; f.out_p = w.out_w.p; f.ff1_p = w.ff1_w.p; f.ff2_p = w.ff2_w.p;
-            }
+        const bool two = x->prec == BOA_PREC_BF16X3;
+        int64_t ftotal = 0;
+        for (MatW* m : mats) ftotal += (two ? 2 : 1) * m->n;
+        frag_host.resize((size_t)ftotal);
+        if (e == hipSuccess) e = dmalloc(x, &x->wfrag, ftotal);
+        int64_t fo = 0, hs = 0;
+        for (MatW* m : mats) {
+            const uint16_t* hi = split_host.data() + hs;
+            pack_fragments(hi, hi + m->n, m->N, m->K, two, frag_host.data() + fo);
+            m->p = x->wfrag + fo;
+            fo += (two ? 2 : 1) * m->n;
+            hs += 2 * m->n;
         }
+    } else if (x->fused) {
+        int64_t ftotal = 0;
+        for (MatW* m : mats) ftotal += m->n;
+        frag32_host.resize((size_t)ftotal);
+        if (e == hipSuccess) e = dmalloc(x, &x->wfrag, 2 * ftotal);  // 16-bit units
+        int64_t fo = 0;
+        for (MatW* m : mats) {
+            pack_fragments_f32(hw + (m->f - x->wblob), m->N, m->K, frag32_host.data() + fo);
+            m->p = x->wfrag + 2 * fo;  // fp32 data; the kernel reads it as such
+            fo += m->n;
+        }
+    }
+    if (e == hipSuccess && x->fused) e = dmalloc(x, &x->d_layers, (int64_t)L);
+    if (e != hipSuccess) {
+        boa_ctx_destroy(x);
+        return boa_fail_hip(e, "boa_ctx_create allocation", __FILE__, __LINE__);
+    }
+    if (x->fused) layers_host.resize((size_t)L);
+    for (int l = 0; l < (x->fused ? L : 0); ++l) {
+        const LayerW& w = x->layers[l];
+        FusedLayer& f = layers_host[(size_t)l];
+        f.ln1_w = w.ln1_w; f.ln1_b = w.ln1_b; f.in_b = w.in_b; f.conv_w = w.conv_w; f.conv_b = w.conv_b;
+        f.dt_w = w.dt_w; f.dt_b = w.dt_b; f.Aneg = w.Aneg; f.D = w.D; f.out_b = w.out_b;
+        f.ln2_w = w.ln2_w; f.ln2_b = w.ln2_b; f.ff1_b = w.ff1_b; f.ff2_b = w.ff2_b;
+        f.in_p = w.in_w.p; f.x_p = w.x_w.p; f.out_p = w.out_w.p; f.ff1_p = w.ff1_w.p; f.ff2_p = w.ff2_w.p;
     }
     e = hipMemcpyAsync(x->wblob, h_weights, (size_t)nbytes, hipMemcpyHostToDevice, x->stream);
     if (e == hipSuccess && !split_host.empty())
         e = hipMemcpyAsync(x->wsplit, split_host.data(), split_host.size() * 2, hipMemcpyHostToDevice, x->stream);
     if (e == hipSuccess && !frag_host.empty())
         e = hipMemcpyAsync(x->wfrag, frag_host.data(), frag_host.size() * 2, hipMemcpyHostToDevice, x->stream);
+    if (e == hipSuccess && !frag32_host.empty())
+        e = hipMemcpyAsync(x->wfrag, frag32_host.data(), frag32_host.size() * 4, hipMemcpyHostToDevice, x->stream);
     if (e == hipSuccess && !layers_host.empty())
         e = hipMemcpyAsync(x->d_layers, layers_host.data(), layers_host.size() * sizeof(FusedLayer),
                            hipMemcpyHostToDevice, x->stream);
@@ -2974,7 +3002,7 @@ static FusedArgs fused_args(boa_ctx* x, int32_t lanes, const int32_t* tokens_in)
 }
 
 static hipError_t launch_fused(const boa_ctx* x, const FusedArgs& a, hipStream_t s) {
-    const int nt = x->prec == BOA_PREC_BF16X3 ? 3 : 2;
+    const int nt = x->prec == BOA_PREC_BF16X3 ? 3 : (x->prec == BOA_PREC_BF16W ? 2 : 1);
     return x->d == 512 ? launch_fused_step512(a, nt, s) : launch_fused_step(a, nt, s);
 }
 

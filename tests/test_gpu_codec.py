@@ -106,9 +106,9 @@ def test_boa_file_round_trip(gpu, tmp_path):
         del os.environ["BOA_GPU_STREAMS"]
 
 
-@pytest.mark.parametrize("d_model,precision,steps", [(256, "bf16x3", None), (512, "bf16w", None),
-                                                     (512, "bf16x3", None), (256, "bf16x3", "5"),
-                                                     (512, "bf16w", "5")])
+@pytest.mark.parametrize("d_model,precision,steps", [(256, "bf16x3", None), (256, "f32", None),
+                                                     (512, "bf16w", None), (512, "bf16x3", None),
+                                                     (256, "bf16x3", "5"), (512, "bf16w", "5")])
 def test_decompress_fused_and_layer_kernels_agree(gpu, d_model, precision, steps):
     """Decompression through the fused step kernel and through the per-layer kernels gives the same bytes
     (both must reproduce the compressor's logits bit for bit to decode at all).  At d_model 512 the 70 ragged

@@ -174,11 +174,13 @@ def _stream_logits(m, tok, fused):
     return torch.stack([m.step(tok[:, t], inf) for t in range(tok.shape[1])], dim=1)
 
 
-@pytest.mark.parametrize("d,precision", [(256, "bf16x3"), (256, "bf16w"), (512, "bf16w"), (512, "bf16x3")])
+@pytest.mark.parametrize("d,precision", [(256, "bf16x3"), (256, "bf16w"), (256, "f32"), (512, "bf16w"),
+                                         (512, "bf16x3")])
 def test_fused_step_matches_layer_kernels(gpu, d, precision):
-    """The one-launch decompress step (d_model 256: 16 lanes per workgroup, activations in LDS; d_model 512:
-    32 lanes per workgroup, chunked, with per-lane scratch) against the per-layer step kernels: identical bits,
-    including a partial last workgroup (37 lanes) and > 3 positions (the conv history ring wraps)."""
+    """The one-launch decompress step (d_model 256: 16 lanes per workgroup, activations in LDS, in each precision
+    mode including fp32 MFMA; d_model 512: 32 lanes per workgroup, chunked, with per-lane scratch) against the
+    per-layer step kernels: identical bits, including a partial last workgroup (37 lanes) and > 3 positions
+    (the conv history ring wraps)."""
     m, ref = _model(8 if d == 256 else 2, seed=0 if d == 256 else 1, d=d, precision=precision)
     tok = torch.from_numpy(np.random.default_rng(11).integers(0, 256, (37, 9))).cuda()
     a = _stream_logits(m, tok, fused=True)
