@@ -784,14 +784,19 @@ __global__ void __launch_bounds__(512, 4) k_ffn(const float* __restrict__ mm, co
         ln_stats_row<1>(v, mu, rs);
         const float y[4] = {ln_apply(v[0], mu, rs, wv.x, bv.x), ln_apply(v[1], mu, rs, wv.y, bv.y),
                             ln_apply(v[2], mu, rs, wv.z, bv.z), ln_apply(v[3], mu, rs, wv.w, bv.w)};
-        uint2 hp, lp;
-        split4(y[0], y[1], y[2], y[3], hp, lp);
-        const int o = a_off(r, 4 * lane);
-        *reinterpret_cast<uint2*>(&sA[0][o]) = hp;
-        *reinterpret_cast<uint2*>(&sA[1][o]) = lp;
+        if constexpr (NT == 1) {
+            const int k = 4 * lane;
+            *reinterpret_cast<float4*>(&sA[f32_lo(k)][a_off(r, f32_col(k))]) = make_float4(y[0], y[1], y[2], y[3]);
+        } else {
+            uint2 hp, lp;
+            split4(y[0], y[1], y[2], y[3], hp, lp);
+            const int o = a_off(r, 4 * lane);
+            *reinterpret_cast<uint2*>(&sA[0][o]) = hp;
+            *reinterpret_cast<uint2*>(&sA[1][o]) = lp;
+        }
     };
     if constexpr (OUTP) {
-        constexpr int KO = 2 * D, KC = D, NKS = KO / 32, BLKO = (NT == 3) ? 1024 : 512, RO = 4;
+        constexpr int KO = 2 * D, KC = D, NKS = KO / 32, BLKO = two_part_blocks<NT>() ? 1024 : 512, RO = 4;
         const gptr<uint16_t> wop = G(Wop);
         u32x4 oh[RO], ol[RO];
         // block i (W_out fragment 2 wave + i % 2, K step i / 2) into ring slot i % RO
@@ -799,7 +804,7 @@ __global__ void __launch_bounds__(512, 4) k_ffn(const float* __restrict__ mm, co
             const gptr<uint16_t> q = wop + ((int64_t)(2 * wave + (i & 1)) * NKS + (i >> 1)) * BLKO + lane * 8;
             oh[i % RO] = ldg16(q);
             ol[i % RO] = oh[i % RO];
-            if constexpr (NT == 3) ol[i % RO] = ldg16(q + 512);
+            if constexpr (two_part_blocks<NT>()) ol[i % RO] = ldg16(q + 512);
         };
 #pragma unroll
         for (int i = 0; i < RO; ++i) issue_o(i);
@@ -808,18 +813,29 @@ __global__ void __launch_bounds__(512, 4) k_ffn(const float* __restrict__ mm, co
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int j = 0; j < 2; ++j) macc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-        // y rows past M read 0 (buffer range check)
-        const __amdgpu_buffer_rsrc_t ryh = buf_rsrc(yh + m0 * KO, (uint32_t)rows * KO * 2);
-        const __amdgpu_buffer_rsrc_t ryl = buf_rsrc(yl + m0 * KO, (uint32_t)rows * KO * 2);
+        // y rows past M read 0 (buffer range check).  NT = 1: y is fp32 [rows][512] at yh (yl unused).
+        const __amdgpu_buffer_rsrc_t ryh = buf_rsrc(yh + m0 * KO * (NT == 1 ? 2 : 1), (uint32_t)rows * KO * (NT == 1 ? 4 : 2));
+        const __amdgpu_buffer_rsrc_t ryl = NT == 1 ? ryh : buf_rsrc(yl + m0 * KO, (uint32_t)rows * KO * 2);
 #pragma unroll 1
         for (int q = 0; q < KO / KC; ++q) {
-            // stage y[:, 256 q .. + 255] (hi, lo): 4 x 16 B per array per thread
+            if constexpr (NT == 1) {
+                // stage y[:, 256 q .. + 255] (fp32, in the split operand's layout): 8 x 16 B per thread, 2 in
+                // flight (more spill registers: the kernel is at its 128-register limit)
+#pragma unroll 2
+                for (int e = 0; e < (BM * KC / 4) / 512; ++e) {
+                    const int idx = e * 512 + tid, r = idx / (KC / 4), k = (idx % (KC / 4)) * 4;
+                    const uint32_t off = (uint32_t)((r * KO + KC * q + k) * 4);
+                    *reinterpret_cast<u32x4*>(&sA[f32_lo(k)][a_off(r, f32_col(k))]) = buf_ld16(ryh, off);
+                }
+            } else {
+                // stage y[:, 256 q .. + 255] (hi, lo): 4 x 16 B per array per thread
 #pragma unroll
-            for (int e = 0; e < (BM * KC / 8) / 512; ++e) {
-                const int idx = e * 512 + tid, r = idx / (KC / 8), k = (idx % (KC / 8)) * 8;
-                const uint32_t off = (uint32_t)((r * KO + KC * q + k) * 2);
-                *reinterpret_cast<u32x4*>(&sA[0][a_off(r, k)]) = buf_ld16(ryh, off);
-                *reinterpret_cast<u32x4*>(&sA[1][a_off(r, k)]) = buf_ld16(ryl, off);
+                for (int e = 0; e < (BM * KC / 8) / 512; ++e) {
+                    const int idx = e * 512 + tid, r = idx / (KC / 8), k = (idx % (KC / 8)) * 8;
+                    const uint32_t off = (uint32_t)((r * KO + KC * q + k) * 2);
+                    *reinterpret_cast<u32x4*>(&sA[0][a_off(r, k)]) = buf_ld16(ryh, off);
+                    *reinterpret_cast<u32x4*>(&sA[1][a_off(r, k)]) = buf_ld16(ryl, off);
+                }
             }
             __syncthreads();
             int lq = lane;  // LDS addresses formed per chunk (see k_head_xq)
@@ -884,7 +900,7 @@ __global__ void __launch_bounds__(512, 4) k_ffn(const float* __restrict__ mm, co
     }
     __syncthreads();
     const int ar = lane & 15, kq = 8 * (lane >> 4), m_of = 4 * (lane >> 4);
-    constexpr int BLK = (NT == 3) ? 1024 : 512;
+    constexpr int BLK = two_part_blocks<NT>() ? 1024 : 512;
     const gptr<uint16_t> w1p = G(W1p), w2p = G(W2p);
     const int rh = wave & 1, cf = wave >> 1;
     constexpr int NBC = 12, R = 4;
@@ -896,7 +912,7 @@ __global__ void __launch_bounds__(512, 4) k_ffn(const float* __restrict__ mm, co
         const gptr<uint16_t> q = (i < 8 ? w1p : w2p) + blk * BLK + lane * 8;
         rhh[i % R] = ldg16(q);
         rll[i % R] = rhh[i % R];
-        if constexpr (NT == 3) rll[i % R] = ldg16(q + 512);
+        if constexpr (two_part_blocks<NT>()) rll[i % R] = ldg16(q + 512);
     };
     auto refill = [&](int c, int cn, int i) {
         if (i + R < NBC) issue(c, i + R);
@@ -939,11 +955,17 @@ __global__ void __launch_bounds__(512, 4) k_ffn(const float* __restrict__ mm, co
                 float g[4];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) g[r] = epi_value<EPI_GELU>(hacc[i][r], bv[r]);
-                uint2 hp, lp;
-                split4(g[0], g[1], g[2], g[3], hp, lp);
-                const int o = h_off(32 * rh + 16 * i + ar, 16 * cf + m_of);
-                *reinterpret_cast<uint2*>(&sH[0][o]) = hp;
-                *reinterpret_cast<uint2*>(&sH[1][o]) = lp;
+                if constexpr (NT == 1) {
+                    const int k = 16 * cf + m_of;
+                    *reinterpret_cast<float4*>(&sH[f32_lo(k)][h_off(32 * rh + 16 * i + ar, f32_col(k))]) =
+                        make_float4(g[0], g[1], g[2], g[3]);
+                } else {
+                    uint2 hp, lp;
+                    split4(g[0], g[1], g[2], g[3], hp, lp);
+                    const int o = h_off(32 * rh + 16 * i + ar, 16 * cf + m_of);
+                    *reinterpret_cast<uint2*>(&sH[0][o]) = hp;
+                    *reinterpret_cast<uint2*>(&sH[1][o]) = lp;
+                }
             }
         }
         __syncthreads();
@@ -1275,7 +1297,7 @@ __global__ void __launch_bounds__(256, 2) k_mixin(const float* __restrict__ x, c
                                                  float* __restrict__ xz, float* __restrict__ xs,
                                                  float* __restrict__ dbc, float* __restrict__ hist, int p0m3) {
     using namespace mixin;
-    constexpr int BLK = (NT == 3) ? 1024 : 512;
+    constexpr int BLK = two_part_blocks<NT>() ? 1024 : 512;
     __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * D];  // LN1 output (hi, lo)
     __shared__ __attribute__((aligned(16))) float sX[BM * CH];        // x chunk fp32; then its conv output split
     uint16_t* sXh = reinterpret_cast<uint16_t*>(sX);
@@ -1295,11 +1317,16 @@ __global__ void __launch_bounds__(256, 2) k_mixin(const float* __restrict__ x, c
             ln_stats_row<1>(v, mu, rs);
             const float y[4] = {ln_apply(v[0], mu, rs, wv.x, bv.x), ln_apply(v[1], mu, rs, wv.y, bv.y),
                                 ln_apply(v[2], mu, rs, wv.z, bv.z), ln_apply(v[3], mu, rs, wv.w, bv.w)};
-            uint2 hp, lp;
-            split4(y[0], y[1], y[2], y[3], hp, lp);
-            const int o = ffn::a_off(r, 4 * lane);
-            *reinterpret_cast<uint2*>(&sA[0][o]) = hp;
-            *reinterpret_cast<uint2*>(&sA[1][o]) = lp;
+            if constexpr (NT == 1) {
+                const int k = 4 * lane;
+                *reinterpret_cast<float4*>(&sA[f32_lo(k)][ffn::a_off(r, f32_col(k))]) = make_float4(y[0], y[1], y[2], y[3]);
+            } else {
+                uint2 hp, lp;
+                split4(y[0], y[1], y[2], y[3], hp, lp);
+                const int o = ffn::a_off(r, 4 * lane);
+                *reinterpret_cast<uint2*>(&sA[0][o]) = hp;
+                *reinterpret_cast<uint2*>(&sA[1][o]) = lp;
+            }
         }
     }
     __syncthreads();
@@ -1318,7 +1345,7 @@ __global__ void __launch_bounds__(256, 2) k_mixin(const float* __restrict__ x, c
         const gptr<uint16_t> q = wip + ((int64_t)((CH / 16) * k + wave) * (D / 32) + s) * BLK + lane * 8;
         r1h[s] = ldg16(q);
         r1l[s] = r1h[s];
-        if constexpr (NT == 3) r1l[s] = ldg16(q + 512);
+        if constexpr (two_part_blocks<NT>()) r1l[s] = ldg16(q + 512);
     };
 #pragma unroll
     for (int s = 0; s < R1; ++s) issue_w(chunk_of(0), s);
@@ -1390,7 +1417,7 @@ __global__ void __launch_bounds__(256, 2) k_mixin(const float* __restrict__ x, c
                     const gptr<uint16_t> q = wxp + ((int64_t)j * (DI / 32) + 2 * k + s) * BLK + lane * 8;
                     const u32x4 bh = ldg16(q);
                     xwh[s][j] = __builtin_bit_cast(bf16x8, bh);
-                    xwl[s][j] = NT == 3 ? __builtin_bit_cast(bf16x8, ldg16(q + 512)) : xwh[s][j];
+                    xwl[s][j] = two_part_blocks<NT>() ? __builtin_bit_cast(bf16x8, ldg16(q + 512)) : xwh[s][j];
                 }
             pin_loads();
             float xv[19];
@@ -1409,10 +1436,14 @@ __global__ void __launch_bounds__(256, 2) k_mixin(const float* __restrict__ x, c
                 const int r = 16 * g + e;
                 const float y = conv_point(cw, cb, xv[e], xv[e + 1], xv[e + 2], xv[e + 3]);
                 GM(xs)[(m0 + r) * DI + c] = y;
-                uint32_t hi, lo;
-                split2(y, hi, lo);
-                sXh[x_off(r, cl)] = (uint16_t)hi;
-                sXl[x_off(r, cl)] = (uint16_t)lo;
+                if constexpr (NT == 1) {
+                    *reinterpret_cast<float*>((f32_lo(cl) ? sXl : sXh) + x_off(r, f32_col(cl))) = y;
+                } else {
+                    uint32_t hi, lo;
+                    split2(y, hi, lo);
+                    sXh[x_off(r, cl)] = (uint16_t)hi;
+                    sXl[x_off(r, cl)] = (uint16_t)lo;
+                }
             }
             // history ring: inputs of positions p0 + 61, 62, 63 in slots (p0 + 64) mod 3, + 1, + 2 (wave 3)
             const int e0 = (p0m3 + BM) % 3, e1 = (e0 + 1) % 3, e2 = (e0 + 2) % 3;
@@ -1422,8 +1453,19 @@ __global__ void __launch_bounds__(256, 2) k_mixin(const float* __restrict__ x, c
             buf_st1(hw, (uint32_t)(e2 * DI + c) * 4, xv[18]);
         }
         __syncthreads();
-        // x_proj partial over this chunk's 64 channels (K block k): rows 16 wave .. + 15, fragments 0..2
-        {
+        // x_proj partial over this chunk's 64 channels (K block k): rows 16 wave .. + 15, fragments 0..2.  The
+        // fp32 mode accumulates straight into dbc instead (chunks in ascending channel order: one ascending K
+        // accumulation, as the tiled fp32 GEMM computes x_proj).
+        if constexpr (NT == 1) {
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                const int o = x_off(16 * wave + ar, 32 * s + kq);
+                const bf16x8 ah = *reinterpret_cast<const bf16x8*>(&sXh[o]);
+                const bf16x8 al = *reinterpret_cast<const bf16x8*>(&sXl[o]);
+#pragma unroll
+                for (int j = 0; j < 3; ++j) dacc[j] = mfma_split_step<NT>(dacc[j], ah, al, xwh[s][j], xwl[s][j]);
+            }
+        } else {
             floatx4 part[3];
 #pragma unroll
             for (int j = 0; j < 3; ++j) part[j] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -1899,17 +1941,22 @@ __global__ void __launch_bounds__(512, (D == 256) ? 4 : 2) k_head_xq(const float
 #pragma unroll
             for (int h = 0; h < D / 256; ++h) {
                 const float4 v = ldg_f4(xr + r * D + 256 * h + 4 * lane);
-                uint2 hp, lp;
-                split4(v.x, v.y, v.z, v.w, hp, lp);
-                const int o = a_off<D>(r, 256 * h + 4 * lane);
-                *reinterpret_cast<uint2*>(sAh + o) = hp;
-                *reinterpret_cast<uint2*>(sAl + o) = lp;
+                if constexpr (NT == 1) {
+                    const int k = 256 * h + 4 * lane;
+                    *reinterpret_cast<float4*>((f32_lo(k) ? sAl : sAh) + a_off<D>(r, f32_col(k))) = v;
+                } else {
+                    uint2 hp, lp;
+                    split4(v.x, v.y, v.z, v.w, hp, lp);
+                    const int o = a_off<D>(r, 256 * h + 4 * lane);
+                    *reinterpret_cast<uint2*>(sAh + o) = hp;
+                    *reinterpret_cast<uint2*>(sAl + o) = lp;
+                }
             }
         }
     }
     const int ar = lane & 15, m_of = 4 * (lane >> 4);
     __syncthreads();
-    constexpr int BLK = (NT == 3) ? 1024 : 512;
+    constexpr int BLK = two_part_blocks<NT>() ? 1024 : 512;
     const gptr<uint16_t> w1p = G(W1p), w2p = G(W2p);
     const int rh = wave & 1, cf = wave >> 1;
     constexpr int KS = D / 32, NBC = KS + 4, R = 4, NC = D / HC;
@@ -1921,7 +1968,7 @@ __global__ void __launch_bounds__(512, (D == 256) ? 4 : 2) k_head_xq(const float
         const gptr<uint16_t> q = (i < KS ? w1p : w2p) + blk * BLK + lane * 8;
         rhh[i % R] = ldg16(q);
         rll[i % R] = rhh[i % R];
-        if constexpr (NT == 3) rll[i % R] = ldg16(q + 512);
+        if constexpr (two_part_blocks<NT>()) rll[i % R] = ldg16(q + 512);
     };
     auto refill = [&](int c, int cn, int i) {
         if (i + R < NBC) issue(c, i + R);
@@ -1969,11 +2016,17 @@ __global__ void __launch_bounds__(512, (D == 256) ? 4 : 2) k_head_xq(const float
                 float g[4];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) g[r] = epi_value<EPI_RELU>(hacc[i][r], bv[r]);
-                uint2 hp, lp;
-                split4(g[0], g[1], g[2], g[3], hp, lp);
-                const int o = h_off(32 * rh + 16 * i + ar, 16 * cf + m_of);
-                *reinterpret_cast<uint2*>(sHh + o) = hp;
-                *reinterpret_cast<uint2*>(sHl + o) = lp;
+                if constexpr (NT == 1) {
+                    const int k = 16 * cf + m_of;
+                    *reinterpret_cast<float4*>((f32_lo(k) ? sHl : sHh) + h_off(32 * rh + 16 * i + ar, f32_col(k))) =
+                        make_float4(g[0], g[1], g[2], g[3]);
+                } else {
+                    uint2 hp, lp;
+                    split4(g[0], g[1], g[2], g[3], hp, lp);
+                    const int o = h_off(32 * rh + 16 * i + ar, 16 * cf + m_of);
+                    *reinterpret_cast<uint2*>(sHh + o) = hp;
+                    *reinterpret_cast<uint2*>(sHl + o) = lp;
+                }
             }
         }
         __syncthreads();
@@ -2305,6 +2358,13 @@ extern "C" int64_t boa_ctx_device_bytes(const boa_ctx* ctx) { return ctx ? ctx->
 
 // Whether a context of this shape and precision decodes through a fused step kernel (BOA_FUSED_STEP=0 turns it
 // off): k_fused_step at d_model 256 in every precision mode, k_fused_step512 at d_model 512 in the split modes.
+// Whether an fp32-mode context gets fp32 fragment-packed weights: at d_model 256 (the fused decode kernel and
+// the fused compress kernels k_mixin, k_ffn, k_head_xq read them), whether or not BOA_FUSED_STEP turns the
+// fused decode off.
+static bool f32_packed(const boa_model_cfg& c, int R, int precision) {
+    return precision == BOA_PREC_F32 && fused_step_supported(c.d_model, c.d_state, R, c.d_conv, c.vocab);
+}
+
 static bool want_fused(const boa_model_cfg& c, int R, int precision) {
     const char* fenv = getenv("BOA_FUSED_STEP");
     const bool d256 = fused_step_supported(c.d_model, c.d_state, R, c.d_conv, c.vocab);
@@ -2327,7 +2387,7 @@ static int64_t ctx_plan_bytes(const boa_model_cfg& c, int R, int precision, int6
     if (precision != BOA_PREC_F32) {
         b += 2 * std::max<int64_t>(2 * mats, 1);
         b += 2 * std::max<int64_t>((precision == BOA_PREC_BF16X3 ? 2 : 1) * mats, 1);
-    } else if (want_fused(c, R, precision)) {
+    } else if (f32_packed(c, R, precision)) {
         b += 2 * std::max<int64_t>(2 * mats, 1);  // fp32 fragment-packed weights, in 16-bit units
     }
     if (want_fused(c, R, precision)) b += (int64_t)sizeof(FusedLayer) * L;
@@ -2511,8 +2571,8 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
     }
     // GEMM weight copies for the MFMA kernels.  Split-precision modes: bf16 parts of every matrix ([hi | lo] per
     // matrix) and their fragment-packed form, read by the fused compress kernels (k_mixin, k_ffn, k_ffn512,
-    // k_head_xq) and the fused decode kernels.  fp32 mode with the fused decode kernel: the fp32 fragment-packed
-    // form.
+    // k_head_xq) and the fused decode kernels.  fp32 mode at d_model 256: the fp32 fragment-packed form, read by
+    // the same kernels' fp32 forms.
     std::vector<uint16_t> split_host, frag_host;
     std::vector<float> frag32_host;
     std::vector<FusedLayer> layers_host;
@@ -2560,7 +2620,7 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
             fo += (two ? 2 : 1) * m->n;
             hs += 2 * m->n;
         }
-    } else if (x->fused) {
+    } else if (f32_packed(c, R, x->prec)) {
         int64_t ftotal = 0;
         for (MatW* m : mats) ftotal += m->n;
         frag32_host.resize((size_t)ftotal);
@@ -2724,13 +2784,18 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc, int part = 7) {
                                     w.in_w.p, w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs, x->dbc, hist,
                                     (int)(x->pos % 3)));
     }
-    const bool mix = !mix5 && split && d == mixin::D && di == mixin::DI && R + 2 * NS == mixin::FW && Tc == mixin::BM &&
+    // (fp32 mode included: its fragment-packed weights exist at d_model 256)
+    const bool mix = !mix5 && d == mixin::D && di == mixin::DI && R + 2 * NS == mixin::FW && Tc == mixin::BM &&
                      w.in_w.p && w.x_w.p;
     if (mix && (part & 1)) {
         // LN1 + in_proj + conv + SiLU + x_proj in one kernel per lane tile
         const double flops = gemm_flops(M, 2 * di, d) + gemm_flops(M, R + 2 * NS, di) + 8.0 * M * di;
         const double bytes = 4.0 * M * (d + di + di + R + 2 * NS) + 4.0 * 6 * B * di;
-        if (w.in_w.l)
+        if (x->prec == BOA_PREC_F32)
+            PROF(PC_MIXIN, flops, bytes,
+                 hipLaunchKernelGGL((k_mixin<1>), dim3((unsigned)B), dim3(256), 0, s, x->x, w.ln1_w, w.ln1_b, w.in_w.p,
+                                    w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs, x->dbc, hist, (int)(x->pos % 3)));
+        else if (w.in_w.l)
             PROF(PC_MIXIN, flops, bytes,
                  hipLaunchKernelGGL((k_mixin<3>), dim3((unsigned)B), dim3(256), 0, s, x->x, w.ln1_w, w.ln1_b, w.in_w.p,
                                     w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs, x->dbc, hist, (int)(x->pos % 3)));
@@ -2818,13 +2883,19 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc, int part = 7) {
                                     w.ff1_w.p, w.ff1_b, w.ff2_w.p, w.ff2_b, x->x, M, x->ah, x->al, w.out_w.p, w.out_b));
         return BOA_OK;
     }
-    const bool ffn256 = split && d == ffn::D && 4 * d == ffn::DF && di == 2 * d && w.ff1_w.p && w.ff2_w.p;
+    // (fp32 mode included: its fragment-packed weights exist at d_model 256; its y is fp32 in place of xs)
+    const bool ffn256 = d == ffn::D && 4 * d == ffn::DF && di == 2 * d && w.ff1_w.p && w.ff2_w.p;
     if (ffn256 && x->ffn_outp && w.out_w.p) {
         // out_proj + LN2 + FF1 + GELU + FF2 + residual in one kernel (mm and the hidden layer kept on chip)
         const double flops = gemm_flops(M, d, di) + gemm_flops(M, 4 * d, d) + gemm_flops(M, d, 4 * d);
-        const double bytes = 4.0 * M * di + 4.0 * M * d * 2 + 2.0 * (w.ff1_w.l ? 2 : 1) * (2.0 * 4 * d * d + d * di);
+        const double bytes = 4.0 * M * di + 4.0 * M * d * 2 + 2.0 * (w.ff1_w.l || !split ? 2 : 1) * (2.0 * 4 * d * d + d * di);
         const unsigned grid = (unsigned)((M + ffn::BM - 1) / ffn::BM);
-        if (w.ff1_w.l)
+        if (!split)
+            PROF(PC_FFN, flops, bytes,
+                 hipLaunchKernelGGL((k_ffn<1, true>), dim3(grid), dim3(512), 0, s, nullptr, w.ln2_w, w.ln2_b, w.ff1_w.p,
+                                    w.ff1_b, w.ff2_w.p, w.ff2_b, x->x, M, reinterpret_cast<const uint16_t*>(x->xs),
+                                    nullptr, w.out_w.p, w.out_b));
+        else if (w.ff1_w.l)
             PROF(PC_FFN, flops, bytes,
                  hipLaunchKernelGGL((k_ffn<3, true>), dim3(grid), dim3(512), 0, s, nullptr, w.ln2_w, w.ln2_b, w.ff1_w.p,
                                     w.ff1_b, w.ff2_w.p, w.ff2_b, x->x, M, x->ah, x->al, w.out_w.p, w.out_b));
@@ -2860,12 +2931,16 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc, int part = 7) {
                                     w.ff1_w.p, w.ff1_b, w.ff2_w.p, w.ff2_b, x->x, M, nullptr, nullptr, nullptr, nullptr));
         return BOA_OK;
     }
-    if (split && d == ffn::D && 4 * d == ffn::DF && w.ff1_w.p && w.ff2_w.p) {
+    if (ffn256) {
         // LN2 + FF1 + GELU + FF2 + residual in one kernel (hidden layer kept on chip)
         const double flops = gemm_flops(M, 4 * d, d) + gemm_flops(M, d, 4 * d);
         const double bytes = 4.0 * M * d * 3 + 2.0 * 2 * (2.0 * 4 * d * d);
         const unsigned grid = (unsigned)((M + ffn::BM - 1) / ffn::BM);
-        if (w.ff1_w.l)
+        if (!split)
+            PROF(PC_FFN, flops, bytes,
+                 hipLaunchKernelGGL((k_ffn<1, false>), dim3(grid), dim3(512), 0, s, x->mm, w.ln2_w, w.ln2_b, w.ff1_w.p,
+                                    w.ff1_b, w.ff2_w.p, w.ff2_b, x->x, M, nullptr, nullptr, nullptr, nullptr));
+        else if (w.ff1_w.l)
             PROF(PC_FFN, flops, bytes,
                  hipLaunchKernelGGL((k_ffn<3, false>), dim3(grid), dim3(512), 0, s, x->mm, w.ln2_w, w.ln2_b, w.ff1_w.p,
                                     w.ff1_b, w.ff2_w.p, w.ff2_b, x->x, M, nullptr, nullptr, nullptr, nullptr));
@@ -3064,10 +3139,11 @@ extern "C" int boa_model_forward(boa_ctx* x, const int32_t* d_tokens, int64_t to
     return BOA_OK;
 }
 
-// The fused head + quantiser kernel covers full tiles of 64 positions, vocab 256, d_model 256 or 512, in the
-// split modes (fragment-packed head weights); other tiles take the head GEMMs and k_encode_tile (same values).
+// The fused head + quantiser kernel covers full tiles of 64 positions, vocab 256, d_model 256 (every precision
+// mode) or 512 (split modes), from fragment-packed head weights; other tiles take the head GEMMs and
+// k_encode_tile (same values).
 static bool head_xq_ok(const boa_ctx* x, int Tc) {
-    return x->head_xq && x->prec != BOA_PREC_F32 && Tc == headq::BM && x->V == headq::V && (x->d == 256 || x->d == 512) &&
+    return x->head_xq && Tc == headq::BM && x->V == headq::V && (x->d == 256 || (x->d == 512 && x->prec != BOA_PREC_F32)) &&
            x->h1_w.p && x->h2_w.p;
 }
 
@@ -3076,15 +3152,15 @@ static int launch_head_xq(boa_ctx* x, int lanes, int t0, const uint8_t* bytes, i
     const int d = x->d, V = x->V;
     const int64_t M = (int64_t)lanes * headq::BM;
     const double flops = gemm_flops(M, d, d) + gemm_flops(M, V, d);
-    const double bytes_ = 4.0 * M * d + 8.0 * M + (double)M + 2.0 * (x->h1_w.l ? 2 : 1) * (double)(x->h1_w.n + x->h2_w.n);
-    const bool three = x->h1_w.l != nullptr;
+    const double bytes_ = 4.0 * M * d + 8.0 * M + (double)M + 2.0 * (x->prec == BOA_PREC_BF16W ? 1 : 2) * (double)(x->h1_w.n + x->h2_w.n);
+    const bool three = x->prec == BOA_PREC_BF16X3;
     hipStream_t s = x->stream;
 #define HXQ(NT, D)                                                                                                  \
     PROF(PC_HEADXQ, flops, bytes_,                                                                                  \
          hipLaunchKernelGGL((k_head_xq<NT, D>), dim3((unsigned)lanes), dim3(512), 0, s, x->x, x->h1_w.p, x->h1_b,    \
                             x->h2_w.p, x->h2_b, t0, bytes, stride, lens, lf))
     if (d == 256) {
-        if (three) HXQ(3, 256); else HXQ(2, 256);
+        if (x->prec == BOA_PREC_F32) HXQ(1, 256); else if (three) HXQ(3, 256); else HXQ(2, 256);
     } else {
         if (three) HXQ(3, 512); else HXQ(2, 512);
     }

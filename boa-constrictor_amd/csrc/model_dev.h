@@ -139,12 +139,34 @@ __device__ __forceinline__ float ln_apply(float v, float mu, float rs, float w, 
 // One 32-wide K step of a split-precision product into acc: a = ah + al (activations), w = bh (+ bl): the
 // products lo*hi, hi*lo (NT = 3 only), hi*hi, in this order.  Every split-mode GEMM accumulates its K steps
 // through this sequence.
+//
+// NT = 1 is the fp32 mode: the 32-wide K step is two 16-K groups of v_mfma_f32_16x16x4_f32, in the order of the
+// tiled fp32 GEMM (k_gemm): group 2s, then 2s + 1, and within a group the MFMA j (j < 4) takes k = 16 g +
+// 4 (l / 16) + j from lane l.  The 16-byte operands then hold fp32 values: ah = lane l's 4 values of group 2s,
+// al = those of group 2s + 1 (fp32 activations are stored in the split operand's two arrays for that, see
+// f32_col), and the weight block likewise (bh: group 2s, bl: group 2s + 1; two 1 KB blocks, as bf16x3's hi and lo).
+__device__ __forceinline__ floatx4 mfma_f32_group(floatx4 acc, bf16x8 a, bf16x8 b) {
+    const f32x4 av = __builtin_bit_cast(f32x4, a), bv = __builtin_bit_cast(f32x4, b);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[0], bv[0], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[1], bv[1], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[2], bv[2], acc, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(av[3], bv[3], acc, 0, 0, 0);
+}
 template <int NT>
 __device__ __forceinline__ floatx4 mfma_split_step(floatx4 acc, bf16x8 ah, bf16x8 al, bf16x8 bh, bf16x8 bl) {
+    if constexpr (NT == 1) return mfma_f32_group(mfma_f32_group(acc, ah, bh), al, bl);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
     if constexpr (NT == 3) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
 }
+// Fragment-packed weight blocks come in two 1 KB halves per K step in the bf16x3 (hi, lo) and fp32 (groups 2s,
+// 2s + 1) modes, and as one 1 KB block in bf16w.
+template <int NT> constexpr bool two_part_blocks() { return NT != 2; }
+// fp32 activations in a split operand's layout (NT = 1): values k .. k + 3 of a row (k % 4 == 0) form one 16-byte
+// chunk of the "hi" array for k % 32 < 16, of the "lo" array otherwise, at the bf16 column f32_col(k), so that
+// the split kernels' 16-byte fragment reads (bf16 column 32 s + 8 (l / 16)) return a lane's group values.
+__device__ __forceinline__ int f32_col(int k) { return 32 * (k >> 5) + 2 * (k & 15); }
+__device__ __forceinline__ bool f32_lo(int k) { return (k & 16) != 0; }
 
 // The same step with the operand roles swapped: acc^T += B^T A^T, i.e. the output fragment transposed (lane l
 // holds column 4 (l / 16) + r, row l % 16).  Each output element gets the same three products (exact in fp32)
@@ -152,6 +174,7 @@ __device__ __forceinline__ floatx4 mfma_split_step(floatx4 acc, bf16x8 ah, bf16x
 // fragment-packed weight block is the A operand, which makes a lane's 4 outputs consecutive columns.
 template <int NT>
 __device__ __forceinline__ floatx4 mfma_split_step_t(floatx4 acc, bf16x8 ah, bf16x8 al, bf16x8 bh, bf16x8 bl) {
+    if constexpr (NT == 1) return mfma_f32_group(mfma_f32_group(acc, bh, ah), bl, al);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bh, al, acc, 0, 0, 0);
     if constexpr (NT == 3) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bl, ah, acc, 0, 0, 0);
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(bh, ah, acc, 0, 0, 0);
