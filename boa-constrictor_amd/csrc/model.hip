@@ -2667,7 +2667,7 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
     if (const char* v = getenv("BOA_FFN_OUTP")) x->ffn_outp = atoi(v) != 0;
     if (const char* v = getenv("BOA_HEAD_XQ")) x->head_xq = atoi(v) != 0;
     if (const char* v = getenv("BOA_COMPRESS_HALVES")) x->compress_halves = atoi(v) != 0;
-    if ((!x->fused && x->decode_halves == 2) || (x->compress_halves && x->prec != BOA_PREC_F32)) {
+    if ((!x->fused && x->decode_halves == 2) || x->compress_halves) {
         // default priority (as the context's own stream): streams of different priorities are not mixed
         e = hipStreamCreateWithFlags(&x->stream2, hipStreamNonBlocking);
         for (int i = 0; e == hipSuccess && i < 2 * L + 1; ++i) {

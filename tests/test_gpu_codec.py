@@ -282,7 +282,7 @@ def test_fused_compress_kernels_match_separate_kernels(gpu, d_model, precision, 
         assert (out[i, :lens[i]] == c).all(), i
 
 
-@pytest.mark.parametrize("precision", ["bf16x3", "bf16w"])
+@pytest.mark.parametrize("precision", ["bf16x3", "bf16w", "f32"])
 def test_compress_in_two_halves(gpu, precision):
     """A wave large enough (>= 512 lanes) to compress as two halves of the lanes on two streams, their scans
     alternating: the same words as one stream, for full and partial tiles, and the stream decodes."""
