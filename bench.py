@@ -17,9 +17,11 @@ Also reported: compress and decompress rates separately, the roofline of the dom
 event timing (boa_profile) inside the timed region, and a CPU baseline: this repo's restatement of the
 reference CPU path (codec.compress_CPU / decompress_CPU: per-step torch-CPU model + per-lane range coding in
 a thread pool) timed on a bounded sample of configs[0] on this host.  After the timed steps, untimed by the
-headline, three bounded extra measurements go into the same JSON line (--no-extras skips them):
+headline, four bounded extra measurements go into the same JSON line (--no-extras skips them):
   f32_*      the same model and data in "f32" mode (plain fp32 MFMA, the reference's precision) on a stated
              sub-size of the workload;
+  published_shape  the shape of the reference's only published throughput (d256 x 1 layer, 4096-byte
+             chunks; ~7 / ~5 MiB/s on an RTX 5090) in f32 and bf16x3, on the headline's data;
   coder      configs[1], the range coder alone: 16384 streams x 4096 symbols, P = 16;
   config4    configs[4]'s model (d512 x 16 layers, bf16 weights, seed 1) on its 16384 chunks of mixed
              int16/float32 records, each chunk cut to a stated length (steady-state rates).
@@ -351,6 +353,40 @@ def f32_extra(lib, X, lens_h, sub_len: int) -> dict:
                           "one warm-up and one timed pass"}
 
 
+def published_shape_extra(lib, X, lens_h, sub_len: int) -> dict:
+    """The shape of the reference's only published throughput: ~7 "MB/s" (MiB/s, boa.cpp:39,404) compress and
+    ~5 decompress on an NVIDIA RTX 5090 (portability_solved_cpp/README.md:66-68) for cms_experiment's model,
+    d256 x 1 layer (experiments/cms_experiment/cms_experiment.yaml:10-11), chunks of 4096 B
+    (portability_solved_cpp/README.md:45).  Here: d256 x 1 layer random init seed 0, the headline's chunks cut
+    to their first sub_len bytes, in the reference's fp32 arithmetic ("f32" mode) and in bf16x3.  The CMS data
+    and model are not shipped, so the inputs are the headline's synthetic records: an indication, not the
+    same workload, and not `vs_baseline`."""
+    import torch
+
+    from boa_amd import weights as W
+    import model as M
+
+    B = X.shape[0]
+    Xs = X[:, :sub_len].contiguous()
+    ls = [min(sub_len, v) for v in lens_h]
+    lens = torch.tensor(ls, dtype=torch.int32, device="cuda")
+    nb = sum(ls)
+    cfg = W.Cfg(n_layers=1)
+    out = {"workload": (f"d256x1L random init seed 0, {B} chunks x first {sub_len} B of the headline's records; "
+                        "one warm-up and one timed pass"),
+           "published": {"compress_MiBps": 7.0, "decompress_MiBps": 5.0, "hardware": "NVIDIA RTX 5090",
+                         "workload": "cms_experiment (CMS jets, not shipped), d256x1L, chunk 4096 B"}}
+    for prec in ("f32", "bf16x3"):
+        eng = M._Engine(W.seeded_blob(cfg, 0), cfg, B, 64, precision=prec)
+        tc, td, cb, ok = codec_pass(lib, eng, Xs, lens, ls, sub_len, reps=1, warm=1)
+        del eng
+        out[prec] = {"compress_MiBps": nb / tc / 2**20, "decompress_MiBps": nb / td / 2**20,
+                     "compress_MBps": nb / tc / 1e6, "decompress_MBps": nb / td / 1e6,
+                     "decompress_step_ms": td / (sub_len - 1) * 1e3, "round_trip_ok": ok}
+        torch.cuda.empty_cache()
+    return out
+
+
 def config4_data(n_chunks: int, chunk: int, take: int, seed: int = 1):
     """configs[4] input: int16 N(0, 300^2) clipped to +-32767 and float32 log-normal(1, 1.5) records
     interleaved 1:1 (6-byte pairs), n_chunks x chunk bytes in all; returns the first `take` bytes of every
@@ -424,6 +460,8 @@ def main():
     ap.add_argument("--coder-cpu-streams", type=int, default=64)
     ap.add_argument("--no-extras", action="store_true", help="skip the f32, coder and configs[4] extras")
     ap.add_argument("--f32-len", type=int, default=1024, help="bytes per chunk of the f32-mode extra")
+    ap.add_argument("--pub-len", type=int, default=4096,
+                    help="bytes per chunk of the published-shape extra (d256x1L; the reference's chunk size)")
     ap.add_argument("--c4-lanes", type=int, default=16384, help="chunks (= lanes) of the configs[4] extra")
     ap.add_argument("--c4-len", type=int, default=256, help="bytes per chunk of the configs[4] extra")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -602,6 +640,10 @@ def main():
             f"{extras['f32_decompress_MBps']:.3f} MB/s, round trip {extras['f32_round_trip_ok']}")
         del eng
         torch.cuda.empty_cache()
+        log(f"[bench] extra: the published shape (d256x1L, first {args.pub_len} B of each chunk)")
+        extras["published_shape"] = published_shape_extra(lib, X, lens_h, args.pub_len)
+        log(f"[bench] extra: d256x1L f32 compress {extras['published_shape']['f32']['compress_MiBps']:.2f} MiB/s, "
+            f"decompress {extras['published_shape']['f32']['decompress_MiBps']:.2f} MiB/s")
         log("[bench] extra: range coder alone (configs[1])")
         extras["coder"] = coder_bench(args, 3, 1, args.coder_cpu_streams if not args.no_cpu else 0)
         log(f"[bench] extra: coder {extras['coder']['value'] / 1e9:.2f} G symbols/s, round trip "
