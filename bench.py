@@ -171,7 +171,7 @@ def coder_bench(args, steps: int, warmup: int, cpu_streams: int) -> dict:
     # decode reads each step's full table row (K entries, 2 B) + writes 1 B; encode reads 2 entries + 1 B
     dec_bytes = nsym * (2.0 * K + 1) + code_bytes
     enc_bytes = nsym * (2.0 * 2 + 1) + code_bytes
-    roofline = {"bound": "hbm", "kernel": "k_rc_decode_tables4<16, unsigned short, 16, 4>", "achieved": dec_bytes / t_d / 1e9,
+    roofline = {"bound": "hbm", "kernel": "k_rc_decode_tables8<8>", "achieved": dec_bytes / t_d / 1e9,
                 "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": dec_bytes / t_d / 1e9 / PEAK_HBM_GBPS, "traffic": None,
                 "avg_launch_ms": t_d * 1e3, "algorithmic_per_launch": dec_bytes}
     cpu = None

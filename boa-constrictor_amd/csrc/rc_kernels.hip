@@ -11,6 +11,7 @@
 #include <stdio.h>
 #include <string.h>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "../../include/boa_hip.h"
@@ -73,59 +74,101 @@ __global__ void __launch_bounds__(64) k_rc_decode_tables(const TC* __restrict__ 
     }
 }
 
-// The same coder for full tables (K = 256), streams of a length divisible by 4 and 16-byte aligned tables,
-// written for throughput: four streams per wavefront, 16 lanes per stream, each lane holding 16 entries of
-// a row (a row of one stream is one coalesced 512 B (P = 16) or 1 KiB (P = 24) read by its 16 lanes).
-// Rows are prefetched D = 4 steps ahead through a register ring (independent of the coder state), and each
-// stream's next code words come from a register window: lane j of a stream holds words base + j and
-// base + 16 + j, shifted by 16 (one load per lane) once the read position passes base + 16, so no step waits
-// on a word load.  The coder arithmetic is the reference's (rc_core.h: dec_target, and dec_advance's update
-// with its words taken from the window; gpu_range_coder.py:182-210); the symbol search keeps its semantics
-// (the smallest i in [1, K] with cdf[i] > q, minus one): each lane finds its first such entry in one pass from
-// the top, carrying cdf[i] and cdf[i - 1], and the stream takes the minimum over its 16 lanes.
-template <int P, typename TC, int S = 16, int D = 4>
+// Keeps memory operations in program order across this point (a compiler barrier, no instruction): a register
+// ring's loads stay issued oldest row first, so the wait counts the compiler places before each row's use (the
+// loads outstanding after it, the same on loop entry as on every later pass) leave the newer rows in flight.
+__device__ __forceinline__ void pin_order() { asm volatile("" ::: "memory"); }
+// Word 3 of a raw buffer descriptor on gfx950 (32-bit data format): accesses past num_records bytes read 0 and
+// drop their stores.
+constexpr int BUF_DESC_WORD3 = 0x00020000;
+typedef uint32_t u32x2v __attribute__((vector_size(8)));
+constexpr int ROW_CPOL = 2;  // cache policy of the table row loads: NT (non-temporal)
+
+// DPP moves inside rows of 16 lanes: fixed lane permutations applied as an operand of a VALU instruction, with
+// no LDS round trip (the ds_bpermute behind __shfl is one).  A lane whose source is outside its row reads 0.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, true);
+}
+constexpr int DPP_XOR1 = 0xB1;         // quad_perm [1, 0, 3, 2]: lane i <- lane i ^ 1
+constexpr int DPP_XOR2 = 0x4E;         // quad_perm [2, 3, 0, 1]: lane i <- lane i ^ 2
+constexpr int DPP_HALF_MIRROR = 0x141; // row_half_mirror: lane i <- lane 7 - i within each 8 lanes
+constexpr int DPP_SHR1 = 0x111;        // row_shr:1: lane i <- lane i - 1 within each 16 lanes
+constexpr int DPP_MIRROR = 0x140;      // row_mirror: lane i <- lane 15 - i within each 16 lanes
+
+// The same coder for full tables (K = 256) in any table format, lengths divisible by D: four streams per
+// wavefront, 16 lanes per stream, lane j holding entries 16 j .. 16 j + 15 of each row (a row of one stream is
+// one contiguous 512 B (2-byte entries) or 1 KiB (4-byte entries) read by its 16 lanes).  The scaffolding is
+// k_rc_decode_tables8's (below): rows through a non-temporal register ring D - 1 steps ahead, code words from a
+// three-block register window moved once per pass, symbols stored once per pass, no memory access under a
+// branch.  The coder arithmetic is the reference's (rc_core.h: dec_target, and dec_advance's update with its
+// word from the window; gpu_range_coder.py:182-210); the symbol search keeps its semantics (the smallest i in
+// [1, K] with cdf[i] > q, minus one): each lane finds its first such entry in one pass from the top, carrying
+// cdf[i] and cdf[i - 1]; the stream's smallest index, then that entry's two values, are reduced over its 16
+// lanes with DPP moves (no entry > q gives index K, with cdf[K - 1] from the last lane and hi = 2^P).
+template <int P, typename TC, int D = 4>
 __global__ void __launch_bounds__(256) k_rc_decode_tables4(const TC* __restrict__ cdf,
                                                          const uint32_t* __restrict__ words, int64_t pitch,
                                                          const int32_t* __restrict__ nwords, int streams, int len,
-                                                         uint8_t* __restrict__ syms) {
-    constexpr int K = 256, E = K / S, G = 64 / S;
+                                                         uint8_t* __restrict__ syms, uint32_t words_bytes) {
+    constexpr int K = 256, S = 16, E = K / S, G = 64 / S;
     constexpr int NV = E * (int)sizeof(TC) / 16;  // 16-byte loads per lane per row
+    constexpr uint32_t ROWB = K * sizeof(TC);      // bytes per row
+    static_assert(D <= S, "at most S words are read per pass of D steps");
     const int lane = threadIdx.x & 63;
     const int j = lane & (S - 1), gbase = lane & ~(S - 1);
     const int64_t n = ((int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6)) * G + lane / S;
     const bool live = n < streams;
-    const int64_t nn = live ? n : 0;  // groups past the last stream shadow stream 0 with no words, write nothing
-    const uint32_t* in = words + nn * pitch;
+    const int64_t nn = live ? n : 0;  // streams past the last shadow stream 0 with no words and write nothing
     int32_t nw = live ? nwords[nn] : 0;
     if (nw > pitch) nw = (int32_t)pitch;
     DecState st;
-    dec_init(st, in, nw);
+    dec_init(st, words + nn * pitch, nw);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(words), (short)0,
+                                                                        (int)(words_bytes), BUF_DESC_WORD3);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(syms, (short)0, (int)((uint32_t)streams * (uint32_t)len), BUF_DESC_WORD3);
+    const uint32_t wbase = (uint32_t)(nn * pitch) * 4u;
+    auto word = [&](int i) {
+        return __builtin_amdgcn_raw_buffer_load_b32(rw, i < nw ? wbase + (uint32_t)i * 4u : 0xFFFFFFF0u, 0, 0);
+    };
+    const uint32_t sbase = (uint32_t)((live ? nn : (int64_t)streams) * len);
     int32_t base = 0;
-    uint32_t w0 = (j < nw) ? in[j] : 0u;
-    uint32_t w1 = (S + j < nw) ? in[S + j] : 0u;
-    const TC* crow = cdf + nn * (int64_t)len * K + E * j;
+    uint32_t w0 = word(j), w1 = word(S + j), w2 = word(2 * S + j);
+    const int64_t wfirst =
+        ((int64_t)blockIdx.x * (blockDim.x / 64) + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6))) * G;
+    const int nlive = (int)(streams - wfirst < 0 ? 0 : (streams - wfirst > G ? G : streams - wfirst));
+    const __amdgpu_buffer_rsrc_t rt = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<TC*>(cdf + (nlive > 0 ? wfirst : 0) * (int64_t)len * K), (short)0,
+        (int)((uint32_t)nlive * (uint32_t)len * ROWB), BUF_DESC_WORD3);
+    const uint32_t tbase = (uint32_t)(lane / S) * (uint32_t)len * ROWB + (uint32_t)(E * sizeof(TC)) * (uint32_t)j;
     u32x4 rows[D][NV];
     auto load_row = [&](int t, u32x4 (&r)[NV]) {
-        const TC* p = crow + (int64_t)(t < len ? t : len - 1) * K;
+        const uint32_t o = tbase + (uint32_t)(t < len ? t : len - 1) * ROWB;
 #pragma unroll
-        for (int v = 0; v < NV; ++v) r[v] = *reinterpret_cast<const u32x4*>(p + v * (16 / (int)sizeof(TC)));
+        for (int v = 0; v < NV; ++v)
+            r[v] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rt, o + 16u * v, 0, ROW_CPOL));
     };
 #pragma unroll
-    for (int u = 0; u < D - 1; ++u) load_row(u, rows[u]);
-    // word i of this stream (base <= i < base + 2S) from the window
-    auto word_at = [&](int i) -> uint32_t {
-        const int o = i - base;
-        const int src = gbase + (o & (S - 1));
-        const uint32_t a = __shfl(w0, src, 64), b = __shfl(w1, src, 64);
-        return o < S ? a : b;
-    };
-    uint8_t* out = syms + nn * (int64_t)len;
+    for (int u = 0; u < D - 1; ++u) {
+        load_row(u, rows[u]);
+        pin_order();
+    }
 #pragma unroll 1
     for (int t0 = 0; t0 < len; t0 += D) {
+        const bool rot = st.read_idx - base >= S;
+        w0 = rot ? w1 : w0;
+        w1 = rot ? w2 : w1;
+        base += rot ? S : 0;
+        w2 = word(base + 2 * S + j);
+        uint32_t packed = 0;
 #pragma unroll
         for (int u = 0; u < D; ++u) {
-            const int t = t0 + u;
-            load_row(t + D - 1, rows[(u + D - 1) % D]);
+            load_row(t0 + u + D - 1, rows[(u + D - 1) % D]);
+            pin_order();
+            const int o = st.read_idx - base;  // 0 <= o < 2S
+            const uint32_t wa =
+                (uint32_t)__builtin_amdgcn_ds_bpermute((gbase + (o & (S - 1))) * 4, (int)(o < S ? w0 : w1));
             uint32_t e[E];
 #pragma unroll
             for (int v = 0; v < NV; ++v) {
@@ -141,9 +184,9 @@ __global__ void __launch_bounds__(256) k_rc_decode_tables4(const TC* __restrict_
                 }
             }
             const uint32_t q = P <= 16 ? dec_target16(st, P) : dec_target(st, P);
-            const uint32_t prev_last = __shfl_up(e[E - 1], 1, 64);  // cdf[E j - 1] (unused for j = 0)
+            const uint32_t prev_last = dpp<DPP_SHR1>(e[E - 1]);  // cdf[E j - 1] (unused for j = 0)
             int first = E;
-            uint32_t hv = 0u, lv = 0u;
+            uint32_t hv = j == S - 1 ? (1u << P) : 0u, lv = j == S - 1 ? e[E - 1] : 0u;  // index K: last lane
 #pragma unroll
             for (int i = E - 1; i >= 0; --i) {
                 const bool pred = e[i] > q && (i > 0 || j > 0);
@@ -151,35 +194,181 @@ __global__ void __launch_bounds__(256) k_rc_decode_tables4(const TC* __restrict_
                 hv = pred ? e[i] : hv;
                 lv = pred ? (i > 0 ? e[i - 1] : prev_last) : lv;
             }
-            int kl = first < E ? E * j + first : K;
-#pragma unroll
-            for (int o = 1; o < S; o <<= 1) kl = min(kl, __shfl_xor(kl, o, 64));
-            const int owner = gbase + (kl < K ? kl / E : S - 1);
-            const uint32_t lo_a = __shfl(lv, owner, 64), hi_a = __shfl(hv, owner, 64), last = __shfl(e[E - 1], owner, 64);
-            const uint32_t lo = kl < K ? lo_a : last;
-            const uint32_t hi = kl < K ? hi_a : (1u << P);
-            if (live && j == 0) out[t] = (uint8_t)(kl - 1);
-            // dec_advance (rc_core.h) with the words from the window
+            const int cand = first < E ? E * j + first : (j == S - 1 ? K : K + 1);
+            int kl = cand;
+            kl = min(kl, (int)dpp<DPP_XOR1>((uint32_t)kl));
+            kl = min(kl, (int)dpp<DPP_XOR2>((uint32_t)kl));
+            kl = min(kl, (int)dpp<DPP_HALF_MIRROR>((uint32_t)kl));
+            kl = min(kl, (int)dpp<DPP_MIRROR>((uint32_t)kl));
+            const bool own = cand == kl;
+            uint32_t lo = own ? lv : 0u, hi = own ? hv : 0u;
+            lo |= dpp<DPP_XOR1>(lo);
+            hi |= dpp<DPP_XOR1>(hi);
+            lo |= dpp<DPP_XOR2>(lo);
+            hi |= dpp<DPP_XOR2>(hi);
+            lo |= dpp<DPP_HALF_MIRROR>(lo);
+            hi |= dpp<DPP_HALF_MIRROR>(hi);
+            lo |= dpp<DPP_MIRROR>(lo);
+            hi |= dpp<DPP_MIRROR>(hi);
+            packed |= (uint32_t)(uint8_t)(kl - 1) << (8 * u);
+            // dec_advance (rc_core.h), one renormalisation at most: the range is >= 2^32 before every step, so
+            // range' = (range >> P) * prob >= 2^(32 - P) and one 32-bit shift restores range >= 2^32
             uint32_t prob = hi - lo;
             if (prob == 0u) prob = 1u;
             const uint64_t scale = st.range >> P;
             st.lower = st.lower + scale * (uint64_t)lo;
             st.range = scale * (uint64_t)prob;
-            // one renormalisation at most: the range is >= 2^32 before every step, so range' = (range >> P) * prob
-            // >= 2^(32 - P) and one 32-bit shift restores range >= 2^32 (dec_advance's second round never runs)
-            const uint32_t wa = word_at(st.read_idx);
             const bool sh = st.range < (1ull << 32);
             st.lower = sh ? st.lower << 32 : st.lower;
             st.range = sh ? st.range << 32 : st.range;
             st.point = sh ? (st.point << 32) | (uint64_t)wa : st.point;
             st.read_idx += (sh && st.read_idx < nw) ? 1 : 0;
-            if (st.read_idx - base >= S) {
-                base += S;
-                w0 = w1;
-                const int i = base + S + j;
-                w1 = (i < nw) ? in[i] : 0u;
-            }
         }
+        __builtin_amdgcn_raw_buffer_store_b32(packed, rs, sbase + (uint32_t)t0, 0, 0);
+    }
+}
+
+
+// The table decoder for 2-byte tables at P = 16 (configs[1]'s coder), K = 256, lengths divisible by D: eight
+// lanes per stream, so eight streams per wavefront and half the instructions per decoded symbol of the
+// four-streams form above.  Lane j of a stream holds entries 64 v + 8 j .. + 7 (v = 0..3) of each row, so each
+// of its four 16-byte loads is, over the stream's eight lanes, one contiguous 128-byte line of the row; rows
+// are prefetched D - 1 steps ahead through a register ring.  Per step:
+//  - each entry i >= 1 is tested as a pair word (cdf[i] << 16) | cdf[i - 1] against (q << 16) | 0xFFFF, which
+//    it exceeds exactly when cdf[i] > q (cdf[i - 1] <= 0xFFFF); a lane keeps its first such entry's index and
+//    pair word (the pair word of entry 2m is one funnel shift of two table dwords, that of entry 2m + 1 a dword);
+//  - the stream's smallest index over its eight lanes, then that entry's pair word (from the one lane that
+//    holds it, the others contributing 0), are reduced with DPP moves; no entry > q gives index K, with
+//    cdf[K - 1] from the stream's last lane and hi = 2^P;
+//  - the symbol is that index minus one (the reference's linear search, gpu_range_coder.py:195-199), and the
+//    coder update is dec_advance's (rc_core.h), its renormalisation word read from the register window before
+//    the search (the window's first half always holds it: the read position stays within S words of its base).
+// The D symbols of a pass are stored as one D-byte word.
+template <int D>
+__global__ void __launch_bounds__(256) k_rc_decode_tables8(const uint16_t* __restrict__ cdf,
+                                                         const uint32_t* __restrict__ words, int64_t pitch,
+                                                         const int32_t* __restrict__ nwords, int streams, int len,
+                                                         uint8_t* __restrict__ syms, uint32_t words_bytes) {
+    constexpr int P = 16, K = 256, S = 8, NV = 4, E = 32;  // lanes per stream, 16-byte loads and entries per lane
+    static_assert(D == 4 || D == 8, "symbols of a pass are stored as one 4- or 8-byte word");
+    using SymWord = typename std::conditional<D == 8, uint64_t, uint32_t>::type;
+    const int lane = threadIdx.x & 63;
+    const int j = lane & (S - 1), gbase = lane & ~(S - 1);
+    const int64_t n = ((int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6)) * (64 / S) + lane / S;
+    const bool live = n < streams;
+    const int64_t nn = live ? n : 0;  // streams past the last shadow stream 0 with no words and write nothing
+    const uint32_t* in = words + nn * pitch;
+    int32_t nw = live ? nwords[nn] : 0;
+    if (nw > pitch) nw = (int32_t)pitch;
+    DecState st;
+    dec_init(st, in, nw);
+    // Code words and symbols through buffer descriptors over the whole word and symbol arrays (the launch
+    // checks that both fit 32-bit byte offsets); a word past the stream's nw (read as 0, as dec_advance does)
+    // and a shadow stream's symbols take an offset past the end, which reads 0 and drops the store.  So no
+    // access in the loop is under a branch, and the compiler's wait before each row's use counts exactly the
+    // loads issued after it: the rows behind it stay in flight.
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(words), (short)0,
+                                                                        (int)(words_bytes), BUF_DESC_WORD3);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(syms, (short)0, (int)((uint32_t)streams * (uint32_t)len), BUF_DESC_WORD3);
+    const uint32_t wbase = (uint32_t)(nn * pitch) * 4u;
+    auto word = [&](int i) {
+        return __builtin_amdgcn_raw_buffer_load_b32(rw, i < nw ? wbase + (uint32_t)i * 4u : 0xFFFFFFF0u, 0, 0);
+    };
+    // a shadow stream's stores start at the end of the array (the launch keeps (streams + 1) * len below 2^32)
+    const uint32_t sbase = (uint32_t)((live ? nn : (int64_t)streams) * len);
+    // window of three blocks of S words: lane j holds words base + j, base + S + j, base + 2S + j
+    int32_t base = 0;
+    uint32_t w0 = word(j), w1 = word(S + j), w2 = word(2 * S + j);
+    // Table rows through a descriptor over the tables of this wavefront's eight streams (the launch keeps 8 len
+    // rows of 512 B below 2^32 bytes): the rows of a stream past the last are past its end and read 0.  The loads
+    // are non-temporal: every row is read once, and streaming it past the caches measured 17% faster.
+    const int64_t wfirst =
+        ((int64_t)blockIdx.x * (blockDim.x / 64) + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6))) * (64 / S);
+    const int nlive = (int)(streams - wfirst < 0 ? 0 : (streams - wfirst > 64 / S ? 64 / S : streams - wfirst));
+    const __amdgpu_buffer_rsrc_t rt = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(cdf + (nlive > 0 ? wfirst : 0) * (int64_t)len * K), (short)0,
+        (int)((uint32_t)nlive * (uint32_t)len * (uint32_t)(K * 2)), BUF_DESC_WORD3);
+    const uint32_t tbase = (uint32_t)(lane / S) * (uint32_t)len * (uint32_t)(K * 2) + 16u * (uint32_t)j;
+    u32x4 rows[D][NV];
+    auto load_row = [&](int t, u32x4 (&r)[NV]) {
+        const uint32_t o = tbase + (uint32_t)(t < len ? t : len - 1) * (uint32_t)(K * 2);
+#pragma unroll
+        for (int v = 0; v < NV; ++v)
+            r[v] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rt, o + 128u * v, 0, ROW_CPOL));
+    };
+#pragma unroll
+    for (int u = 0; u < D - 1; ++u) {
+        load_row(u, rows[u]);
+        pin_order();
+    }
+#pragma unroll 1
+    for (int t0 = 0; t0 < len; t0 += D) {
+        // at most D <= S words are read per pass: once the read position has left the window's first block, the
+        // window moves by one block (its third, fetched a pass ago), and the block after it is fetched
+        const bool rot = st.read_idx - base >= S;
+        w0 = rot ? w1 : w0;
+        w1 = rot ? w2 : w1;
+        base += rot ? S : 0;
+        w2 = word(base + 2 * S + j);
+        SymWord packed = 0;
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+            load_row(t0 + u + D - 1, rows[(u + D - 1) % D]);
+            pin_order();
+            const int o = st.read_idx - base;  // 0 <= o < 2S
+            const uint32_t wa =
+                (uint32_t)__builtin_amdgcn_ds_bpermute((gbase + (o & (S - 1))) * 4, (int)(o < S ? w0 : w1));
+            const uint32_t q = dec_target16(st, P);
+            const uint32_t qk = (q << 16) | 0xFFFFu;
+            uint32_t sel = j == S - 1 ? rows[u][NV - 1].w >> 16 : 0u;  // cdf[K - 1], for index K
+            int first = E;                                             // local index 8 v + k; E: none
+#pragma unroll
+            for (int v = NV - 1; v >= 0; --v) {
+                const uint32_t dv[4] = {rows[u][v].x, rows[u][v].y, rows[u][v].z, rows[u][v].w};
+                // dword holding entry 64 v + 8 j - 1 in its high half: lane j - 1's last of this chunk, for lane 0
+                // lane 7's last of the chunk before (global entry 0 has none and is not tested)
+                const uint32_t prev_same = dpp<DPP_SHR1>(dv[3]);
+                const uint32_t prev_wrap = v > 0 ? dpp<DPP_HALF_MIRROR>(rows[u][v - 1].w) : 0u;
+                const uint32_t pv = j > 0 ? prev_same : prev_wrap;
+#pragma unroll
+                for (int k = 7; k >= 0; --k) {
+                    const int m = k >> 1;
+                    const uint32_t pw = (k & 1) ? dv[m] : __builtin_amdgcn_alignbit(dv[m], m > 0 ? dv[m - 1] : pv, 16);
+                    const bool pred = pw > qk && (v > 0 || k > 0 || j > 0);
+                    sel = pred ? pw : sel;
+                    first = pred ? 8 * v + k : first;
+                }
+            }
+            const int cand = first < E ? 64 * (first >> 3) + 8 * j + (first & 7) : (j == S - 1 ? K : K + 1);
+            int kl = cand;
+            kl = min(kl, (int)dpp<DPP_XOR1>((uint32_t)kl));
+            kl = min(kl, (int)dpp<DPP_XOR2>((uint32_t)kl));
+            kl = min(kl, (int)dpp<DPP_HALF_MIRROR>((uint32_t)kl));
+            uint32_t vv = cand == kl ? sel : 0u;
+            vv |= dpp<DPP_XOR1>(vv);
+            vv |= dpp<DPP_XOR2>(vv);
+            vv |= dpp<DPP_HALF_MIRROR>(vv);
+            const uint32_t lo = vv & 0xFFFFu;
+            const uint32_t hi = kl < K ? vv >> 16 : (1u << P);
+            packed |= (SymWord)(uint8_t)(kl - 1) << (8 * u);
+            // dec_advance (rc_core.h), one renormalisation at most (the range is >= 2^32 before every step)
+            uint32_t prob = hi - lo;
+            if (prob == 0u) prob = 1u;
+            const uint64_t scale = st.range >> P;
+            st.lower = st.lower + scale * (uint64_t)lo;
+            st.range = scale * (uint64_t)prob;
+            const bool sh = st.range < (1ull << 32);
+            st.lower = sh ? st.lower << 32 : st.lower;
+            st.range = sh ? st.range << 32 : st.range;
+            st.point = sh ? (st.point << 32) | (uint64_t)wa : st.point;
+            st.read_idx += (sh && st.read_idx < nw) ? 1 : 0;
+        }
+        // the stream's eight lanes store the same word (one write)
+        if constexpr (D == 8)
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2v, packed), rs, sbase + (uint32_t)t0, 0, 0);
+        else
+            __builtin_amdgcn_raw_buffer_store_b32(packed, rs, sbase + (uint32_t)t0, 0, 0);
     }
 }
 
@@ -508,18 +697,28 @@ extern "C" int rc_decode_tables(int32_t precision, int32_t cdf_bytes, const void
     if (streams == 0) return BOA_OK;
     const dim3 grid(streams), block(64);
     hipStream_t s = as_stream(stream);
-    // full tables, lengths in whole groups of 4 steps, 16-byte aligned rows: four streams per wavefront
-    if (K == 256 && len >= 4 && len % 4 == 0 && ((uintptr_t)d_cdf & 15) == 0) {
+    // Full tables, lengths in whole groups of 4 steps, 16-byte aligned tables and 4-byte aligned symbol rows, and
+    // sizes whose byte offsets fit the kernels' 32-bit buffer offsets: the throughput decoders (eight streams
+    // per wavefront for 2-byte tables at P = 16 and lengths in whole groups of 8 steps, four otherwise).
+    const int64_t words_bytes = (int64_t)streams * pitch_words * 4;
+    const bool fits = words_bytes < (1ll << 32) - 16 && (int64_t)(streams + 1) * len < (1ll << 32) - 16 &&
+                      (int64_t)len * K * cdf_bytes * 4 < (1ll << 31);
+    if (K == 256 && len >= 4 && len % 4 == 0 && ((uintptr_t)d_cdf & 15) == 0 && ((uintptr_t)d_syms & 3) == 0 &&
+        fits) {
         const dim3 g4((unsigned)((streams + 15) / 16)), b4(256);
-        if (cdf_bytes == 2 && precision == 16)
+        const uint32_t wb = (uint32_t)words_bytes;
+        if (cdf_bytes == 2 && precision == 16 && len % 8 == 0 && ((uintptr_t)d_syms & 7) == 0)
+            hipLaunchKernelGGL((k_rc_decode_tables8<8>), dim3((unsigned)((streams + 31) / 32)), b4, 0, s,
+                               (const uint16_t*)d_cdf, d_words, pitch_words, d_nwords, streams, len, d_syms, wb);
+        else if (cdf_bytes == 2 && precision == 16)
             hipLaunchKernelGGL((k_rc_decode_tables4<16, uint16_t>), g4, b4, 0, s, (const uint16_t*)d_cdf, d_words,
-                               pitch_words, d_nwords, streams, len, d_syms);
+                               pitch_words, d_nwords, streams, len, d_syms, wb);
         else if (cdf_bytes == 4 && precision == 16)
             hipLaunchKernelGGL((k_rc_decode_tables4<16, uint32_t>), g4, b4, 0, s, (const uint32_t*)d_cdf, d_words,
-                               pitch_words, d_nwords, streams, len, d_syms);
+                               pitch_words, d_nwords, streams, len, d_syms, wb);
         else if (cdf_bytes == 4 && precision == 24)
             hipLaunchKernelGGL((k_rc_decode_tables4<24, uint32_t>), g4, b4, 0, s, (const uint32_t*)d_cdf, d_words,
-                               pitch_words, d_nwords, streams, len, d_syms);
+                               pitch_words, d_nwords, streams, len, d_syms, wb);
         else
             return boa_fail(BOA_ERR_ARG, "rc_decode_tables: precision %d with %d-byte tables unsupported",
                             precision, cdf_bytes);

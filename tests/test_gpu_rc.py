@@ -34,10 +34,12 @@ def _encode_gpu(lib, P, cb, tables, syms, pitch):
     return d_cdf, d_words, d_n
 
 
-# T = 256 with K = 256 takes the throughput kernels (four streams per wave decoder, block-pipelined encoder);
+# T = 256 with K = 256 takes the throughput kernels (the block-pipelined encoder; the decoder with eight streams
+# per wave for 2-byte tables at P = 16 and T divisible by 8, four streams per wave otherwise, as T = 260);
 # T = 257 and K < 256 the one-stream-per-wave ones.  S = 45 leaves part of the last wave without a stream.
 @pytest.mark.parametrize("P,cb,K,T", [(16, 2, 256, 257), (16, 4, 256, 257), (24, 4, 256, 257), (16, 2, 100, 257),
-                                      (24, 4, 7, 257), (16, 2, 256, 256), (16, 4, 256, 256), (24, 4, 256, 256)])
+                                      (24, 4, 7, 257), (16, 2, 256, 256), (16, 4, 256, 256), (24, 4, 256, 256),
+                                      (16, 2, 256, 260)])
 def test_tables_bit_exact(gpu, ora, P, cb, K, T):
     from boa_amd import _native as N
 
@@ -61,16 +63,34 @@ def test_tables_bit_exact(gpu, ora, P, cb, K, T):
     assert (d_out.cpu().numpy() == syms).all()
 
 
-@pytest.mark.parametrize("P,cb,T", [(16, 2, 256), (24, 4, 256), (16, 2, 255)])
-def test_decode_tables_arbitrary_words(gpu, ora, P, cb, T):
+def _zero_runs(cdf, rng, P):
+    """The same tables with about a third of the symbols (never the last) at frequency 0, their mass moved to
+    the last symbol: runs of equal cdf entries, still below 2^P."""
+    freq = np.diff(cdf.astype(np.int64), axis=-1)
+    drop = rng.random(freq.shape) < 0.35
+    drop[..., -1] = False
+    freq[..., -1] += np.where(drop, freq, 0).sum(-1)
+    freq[drop] = 0
+    out = np.zeros_like(cdf, dtype=np.int64)
+    out[..., 1:] = np.cumsum(freq, axis=-1)
+    assert (out[..., -1] == 1 << P).all()
+    return out.astype(np.uint32)
+
+
+@pytest.mark.parametrize("P,cb,T,zero", [(16, 2, 256, False), (24, 4, 256, False), (16, 2, 255, False),
+                                         (16, 2, 256, True), (16, 2, 260, True)])
+def test_decode_tables_arbitrary_words(gpu, ora, P, cb, T, zero):
     """Decoding words that no encoder wrote (random values, random stream lengths 0 .. 2 T, including 0, 1 and
     2 words) on valid tables: every symbol equals the oracle decoder's, which exercises the target division, the
-    symbol search at arbitrary targets and the reading of words past the end of a stream (zeros)."""
+    symbol search at arbitrary targets and the reading of words past the end of a stream (zeros).  With zero,
+    the tables hold runs of zero-frequency symbols (equal entries) that the search must step over."""
     from boa_amd import _native as N
 
-    rng = np.random.default_rng(P + T)
+    rng = np.random.default_rng(P + T + zero)
     S, K = 45, 256
     cdf = ora.xq_cdf(rng.normal(0, 3, (S, T, K)).astype(np.float32), P)
+    if zero:
+        cdf = _zero_runs(cdf, rng, P)
     pitch = 2 * T + 8
     words = rng.integers(0, 1 << 32, (S, pitch), dtype=np.uint64).astype(np.uint32)
     nw = rng.integers(0, 2 * T, S).astype(np.int32)
