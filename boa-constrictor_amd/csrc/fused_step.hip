@@ -287,13 +287,13 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
         }
         *reinterpret_cast<float4*>(sRes + r * LRES + c4) = v;
     }
-    float4 lnw = ldg_f4(G(a.layers[0].ln1_w) + 4 * lane), lnb = ldg_f4(G(a.layers[0].ln1_b) + 4 * lane);
+    float4 lnw = ldg_f4(G(layer_at(a.layers, 0).ln1_w) + 4 * lane), lnb = ldg_f4(G(layer_at(a.layers, 0).ln1_b) + 4 * lane);
     __syncthreads();
 
     const int s1 = p0m3 == 2 ? 0 : p0m3 + 1, s2 = p0m3 == 0 ? 2 : p0m3 - 1;
 
     for (int l = 0; l < a.L; ++l) {
-        const FusedLayer& w = a.layers[l];
+        CFusedLayer& w = layer_at(a.layers, l);
         // ---- LN1 -> split operand
         ln_rows<NT, RPW>(sRes, lnw, lnb, sAh, sAl, wave, lane);
         __syncthreads();
@@ -514,7 +514,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
             }
         }
         {
-            const FusedLayer& wn = a.layers[l + 1 < a.L ? l + 1 : l];  // the last layer reloads its own (unused)
+            CFusedLayer& wn = layer_at(a.layers, l + 1 < a.L ? l + 1 : l);  // the last layer reloads its own (unused)
             lnw = ldg_f4(G(wn.ln1_w) + 4 * lane);
             lnb = ldg_f4(G(wn.ln1_b) + 4 * lane);
         }

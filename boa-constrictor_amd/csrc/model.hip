@@ -991,7 +991,19 @@ __global__ void __launch_bounds__(512, 4) k_ffn(const float* __restrict__ mm, co
         }
         __syncthreads();
     }
+    // residual: every value read before any is written (a read after a write to the same buffer would wait for
+    // that write, one memory round trip per value)
     const __amdgpu_buffer_rsrc_t rx = buf_rsrc(x + m0 * D, (uint32_t)rows * D * 4);
+    float res[2][4][4];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t o = (uint32_t)(((16 * i + m_of + r) * D + 16 * (2 * wave + j) + ar) * 4);
+                res[j][i][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, o, 0, 0));
+            }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int col = 16 * (2 * wave + j) + ar;
@@ -1001,9 +1013,8 @@ __global__ void __launch_bounds__(512, 4) k_ffn(const float* __restrict__ mm, co
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const uint32_t o = (uint32_t)(((16 * i + m_of + r) * D + col) * 4);
-                const float res = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, o, 0, 0));
-                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, res + epi_value<EPI_RESID>(out[i][j][r], bias)),
-                                                      rx, o, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b32(
+                    __builtin_bit_cast(uint32_t, res[j][i][r] + epi_value<EPI_RESID>(out[i][j][r], bias)), rx, o, 0, 0);
             }
     }
 }
@@ -1252,7 +1263,18 @@ __global__ void __launch_bounds__(512, 2) k_ffn512(const float* __restrict__ mm,
         }
         __syncthreads();
     }
+    // residual: every value read before any is written (as in k_ffn)
     const __amdgpu_buffer_rsrc_t rx = buf_rsrc(x + m0 * D, (uint32_t)rows * D * 4);
+    float res[4][4][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t o = (uint32_t)(((16 * i + m_of + r) * D + 16 * (4 * wave + j) + ar) * 4);
+                res[j][i][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, o, 0, 0));
+            }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int col = 16 * (4 * wave + j) + ar;
@@ -1262,9 +1284,8 @@ __global__ void __launch_bounds__(512, 2) k_ffn512(const float* __restrict__ mm,
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const uint32_t o = (uint32_t)(((16 * i + m_of + r) * D + col) * 4);
-                const float res = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, o, 0, 0));
-                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, res + epi_value<EPI_RESID>(out[i][j][r], bias)),
-                                                      rx, o, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b32(
+                    __builtin_bit_cast(uint32_t, res[j][i][r] + epi_value<EPI_RESID>(out[i][j][r], bias)), rx, o, 0, 0);
             }
     }
 }

@@ -19,6 +19,17 @@ struct FusedLayer {
     const uint16_t *in_p, *x_p, *out_p, *ff1_p, *ff2_p;
 };
 
+// The layer table as the d_model 256 fused kernel reads it: constant memory (the table does not change while the
+// kernel runs), so its pointers come through scalar loads, which wait on the scalar counter alone.  Read as global
+// memory, each pointer is a vector load, and the wait for it is also a wait for every vector load and store
+// issued before it (the counter is in order): at a phase boundary, the previous phase's state stores.  (The
+// d_model 512 kernel, short of scalar registers, measured 4.5% slower with it and reads the table as global
+// memory.)
+typedef __attribute__((address_space(4))) const FusedLayer CFusedLayer;
+__device__ __forceinline__ CFusedLayer& layer_at(const FusedLayer* table, int l) {
+    return ((CFusedLayer*)table)[l];
+}
+
 struct FusedArgs {
     const FusedLayer* layers;  // device array [L]
     int L;
