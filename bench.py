@@ -44,6 +44,7 @@ METRIC = "input MB/s compress + decompress, d256×8L Mamba, 4096 chunks, 1 GPU"
 PEAK_BF16_MFMA_TFLOPS = 2500.0  # dense; a bf16x3 GEMM issues 3 bf16 products per model multiply-add
 PEAK_HBM_GBPS = 8000.0
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_fused_step_d256x8L_4096lanes.json")
+CODER_TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_rc_coder_configs1.json")
 
 # rocprof names of the kernel instances each profiled class launches at the benchmark's shapes, default
 # precision bf16x3 (k_gemm_bf<BM, BN, BK, EPI, NT, A split, C split>: EPI 0 none, 1 bias, 2 GELU, 4 residual;
@@ -82,6 +83,19 @@ def measured_traffic(lanes: int, steps_per_launch: float):
     if t.get("lanes") != lanes:
         return None
     return t["bytes_per_step"] * steps_per_launch
+
+
+def coder_traffic(streams: int, length: int):
+    """The coder kernels' HBM bytes per launch measured with rocprofv3 --pmc (as measured_traffic), from the
+    committed profile summary when it describes this workload; otherwise None."""
+    try:
+        with open(CODER_TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if t.get("streams") != streams or t.get("symbols_per_stream") != length:
+        return None
+    return t
 
 
 def log(msg):
@@ -174,6 +188,13 @@ def coder_bench(args, steps: int, warmup: int, cpu_streams: int) -> dict:
     roofline = {"bound": "hbm", "kernel": "k_rc_decode_tables8<8>", "achieved": dec_bytes / t_d / 1e9,
                 "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": dec_bytes / t_d / 1e9 / PEAK_HBM_GBPS, "traffic": None,
                 "avg_launch_ms": t_d * 1e3, "algorithmic_per_launch": dec_bytes}
+    measured = coder_traffic(S, T)
+    encode_hbm = None
+    if measured:
+        roofline["traffic"] = measured["decode"]["bytes_per_launch"]
+        # the encoder gathers 2 entries per symbol from a different row each: its HBM traffic is whole lines
+        eb = measured["encode"]["bytes_per_launch"]
+        encode_hbm = {"traffic": eb, "achieved": eb / t_e / 1e9, "unit": "GB/s", "frac": eb / t_e / 1e9 / PEAK_HBM_GBPS}
     cpu = None
     if not args.no_cpu:
         from oracle import ora
@@ -216,6 +237,7 @@ def coder_bench(args, steps: int, warmup: int, cpu_streams: int) -> dict:
         "code_bytes": code_bytes,
         "round_trip_ok": ok,
         "roofline": roofline,
+        "encode_hbm": encode_hbm,
         "cpu_baseline": cpu,
     }
     return res
