@@ -2263,10 +2263,13 @@ struct boa_ctx {
     int decode_halves = 2;
     bool ffn_outp = true;  // out_proj inside the feed-forward kernel (BOA_FFN_OUTP=0: separate GEMM)
     bool head_xq = true;   // compress tiles: head + quantiser in one kernel (BOA_HEAD_XQ=0: head GEMMs + k_encode_tile)
-    // compress in two halves of the lanes on two streams, the scans alternating (BOA_COMPRESS_HALVES=0: one stream)
+    // compress in groups of the lanes on their own streams (BOA_COMPRESS_HALVES=0: one stream; BOA_COMPRESS_GROUPS:
+    // 2 or 3 groups, default 2)
     bool compress_halves = true;
+    int compress_groups = 2;
     hipStream_t stream2 = nullptr;
-    std::vector<hipEvent_t> half_ev;   // [2][L]: state group of layer l done, per half; [2L]: stream join
+    hipStream_t stream3 = nullptr;     // the third compress group's
+    std::vector<hipEvent_t> half_ev;   // [2][L]: state group of layer l done, per half; [2L], [2L + 1]: stream joins
     int64_t lane0 = 0;
     uint16_t* wfrag = nullptr;         // fragment-packed GEMM weights (fused)
     FusedLayer* d_layers = nullptr;    // per-layer pointer table (fused)
@@ -2441,6 +2444,7 @@ extern "C" int boa_ctx_destroy(boa_ctx* ctx) {
         for (hipEvent_t e : p.ev) (void)hipEventDestroy(e);
     for (hipEvent_t e : ctx->half_ev) (void)hipEventDestroy(e);
     if (ctx->stream2) (void)hipStreamDestroy(ctx->stream2);
+    if (ctx->stream3) (void)hipStreamDestroy(ctx->stream3);
     delete ctx;
     return BOA_OK;
 }
@@ -2688,10 +2692,13 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
     if (const char* v = getenv("BOA_FFN_OUTP")) x->ffn_outp = atoi(v) != 0;
     if (const char* v = getenv("BOA_HEAD_XQ")) x->head_xq = atoi(v) != 0;
     if (const char* v = getenv("BOA_COMPRESS_HALVES")) x->compress_halves = atoi(v) != 0;
+    if (const char* v = getenv("BOA_COMPRESS_GROUPS")) x->compress_groups = atoi(v) == 3 ? 3 : 2;
     if ((!x->fused && x->decode_halves == 2) || x->compress_halves) {
         // default priority (as the context's own stream): streams of different priorities are not mixed
         e = hipStreamCreateWithFlags(&x->stream2, hipStreamNonBlocking);
-        for (int i = 0; e == hipSuccess && i < 2 * L + 1; ++i) {
+        if (e == hipSuccess && x->compress_halves && x->compress_groups == 3)
+            e = hipStreamCreateWithFlags(&x->stream3, hipStreamNonBlocking);
+        for (int i = 0; e == hipSuccess && i < 2 * L + 2; ++i) {
             hipEvent_t ev;
             e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
             if (e == hipSuccess) x->half_ev.push_back(ev);
@@ -3039,10 +3046,10 @@ static int run_model(boa_ctx* x, int B, int Tc, float* out) {
     return run_head(x, B, Tc, out);
 }
 
-// The context as seen by the launches of one half of the lanes in the two-stream decode: the second half's
-// per-row activations live in the upper half of every workspace buffer (each holds max_rows rows at its
-// widest row length, so any row length fits), its per-lane state starts at lane0, and it runs on stream2.
-// Restores the context on destruction.
+// The context as seen by the launches of one group of the lanes on its own stream (the two-stream decode, the
+// compress groups): the group's per-row activations start row_off rows into every workspace buffer (each holds
+// max_rows rows at its widest row length, so any row length fits), its per-lane state starts at lane0, and it
+// runs on stream s.  Restores the context on destruction.
 struct LaneView {
     boa_ctx* x;
     float *px, *pxz, *pxs, *pdbc, *pmm, *plog;
@@ -3050,11 +3057,11 @@ struct LaneView {
     uint16_t *pah, *pal;
     int64_t pl0;
     hipStream_t ps;
-    LaneView(boa_ctx* c, int half, int64_t lane0, hipStream_t s)
+    LaneView(boa_ctx* c, int64_t row_off, int64_t lane0, hipStream_t s)
         : x(c), px(c->x), pxz(c->xz), pxs(c->xs), pdbc(c->dbc), pmm(c->mm), plog(c->logits), pst(c->stats),
           pah(c->ah), pal(c->al), pl0(c->lane0), ps(c->stream) {
-        if (half) {
-            const int64_t hr = x->max_rows / 2;
+        if (row_off) {
+            const int64_t hr = row_off;
             const int64_t d = x->d, di = x->di, V = x->V, W = x->R + 2 * x->NS;
             x->x += hr * d;
             x->xz += hr * std::max(2 * di, 4 * d);
@@ -3201,38 +3208,42 @@ extern "C" int boa_compress(boa_ctx* x, const uint8_t* d_bytes, int64_t byte_str
     hipLaunchKernelGGL(k_enc_init, dim3((lanes + 255) / 256), dim3(256), 0, s, x->enc, lanes);
     BOA_HIP_TRY(hipMemsetAsync(x->flag, 0, sizeof(int32_t), s));
     const int positions = max_len - 1;  // model inputs 0..max_len-2 predict bytes 1..max_len-1
-    const int la = lanes / 2, lb = lanes - la;
-    const bool halves = x->stream2 && x->compress_halves && lanes >= 512 && (int64_t)lb * x->tile_len <= x->max_rows / 2;
+    // lane groups: group g holds lanes [lo[g], lo[g + 1]), its rows lo[g] * tile_len rows into the workspace
+    const int G = x->stream3 ? 3 : 2;
+    int lo[4];
+    for (int g = 0; g <= G; ++g) lo[g] = (int)((int64_t)lanes * g / G);
+    const bool halves = x->stream2 && x->compress_halves && lanes >= 256 * G;
     if (halves) {
-        // Two halves of the lanes on two streams, each running its layers in order (per layer: the mixer input
-        // kernel, the scan, the feed-forward kernel), so that the GPU interleaves the two halves' kernels: a
-        // VALU-bound scan of one beside the MFMA-bound kernels of the other, or two of those.  Ordering the scans
-        // to alternate between the halves (A's layer l after B's layer l - 1, B's after A's) measured 1.3% slower
-        // than leaving the halves free.  Each half's arithmetic is unchanged.
+        // Groups of the lanes on their own streams, each running its layers in order (per layer: the mixer input
+        // kernel, the scan, the feed-forward kernel), so that the GPU interleaves the groups' kernels: a
+        // VALU-bound scan of one beside the MFMA-bound kernels of another, or two of those.  Ordering the scans
+        // to alternate between two halves (A's layer l after B's layer l - 1, B's after A's) measured 1.3% slower
+        // than leaving the halves free.  Each group's arithmetic is unchanged.
         const int L = x->L;
-        hipEvent_t join = x->half_ev[2 * L];
-        BOA_HIP_TRY(hipEventRecord(join, s));  // the second stream starts after the coder initialisation
-        BOA_HIP_TRY(hipStreamWaitEvent(x->stream2, join, 0));
+        hipStream_t gs[3] = {s, x->stream2, x->stream3};
+        hipEvent_t join[2] = {x->half_ev[2 * L], x->half_ev[2 * L + 1]};
+        BOA_HIP_TRY(hipEventRecord(join[0], s));  // the other streams start after the coder initialisation
+        for (int g = 1; g < G; ++g) BOA_HIP_TRY(hipStreamWaitEvent(gs[g], join[0], 0));
         for (int t0 = 0; t0 < positions; t0 += x->tile_len) {
             const int Tc = std::min(x->tile_len, positions - t0);
-            for (int h = 0; h < 2; ++h) {
-                LaneView v(x, h, h ? la : 0, h ? x->stream2 : s);
-                const int64_t b0 = x->lane0, rows = (int64_t)(h ? lb : la) * Tc;
+            for (int g = 0; g < G; ++g) {
+                LaneView v(x, (int64_t)lo[g] * x->tile_len, lo[g], gs[g]);
+                const int64_t b0 = x->lane0, rows = (int64_t)(lo[g + 1] - lo[g]) * Tc;
                 PROF(PC_EMBED, 0.0, 4.0 * rows * x->d,
                      hipLaunchKernelGGL(k_embed_bytes, dim3(row_blocks(rows)), dim3(256), 0, x->stream,
                                         d_bytes + b0 * byte_stride, byte_stride, d_lens + b0, t0, Tc, rows, x->emb,
                                         x->d, x->V, x->x));
             }
             for (int l = 0; l < L; ++l) {
-                for (int h = 0; h < 2; ++h) {
-                    LaneView v(x, h, h ? la : 0, h ? x->stream2 : s);
-                    rc = run_layer(x, l, h ? lb : la, Tc);
+                for (int g = 0; g < G; ++g) {
+                    LaneView v(x, (int64_t)lo[g] * x->tile_len, lo[g], gs[g]);
+                    rc = run_layer(x, l, lo[g + 1] - lo[g], Tc);
                     if (rc) return rc;
                 }
             }
-            for (int h = 0; h < 2; ++h) {
-                LaneView v(x, h, h ? la : 0, h ? x->stream2 : s);
-                const int nl = h ? lb : la;
+            for (int g = 0; g < G; ++g) {
+                LaneView v(x, (int64_t)lo[g] * x->tile_len, lo[g], gs[g]);
+                const int nl = lo[g + 1] - lo[g];
                 const int64_t b0 = x->lane0, rows = (int64_t)nl * Tc;
                 if (head_xq_ok(x, Tc)) {
                     uint2* lf = reinterpret_cast<uint2*>(x->logits);
@@ -3253,8 +3264,10 @@ extern "C" int boa_compress(boa_ctx* x, const uint8_t* d_bytes, int64_t byte_str
             x->pos += Tc;
         }
         BOA_HIP_TRY(hipGetLastError());
-        BOA_HIP_TRY(hipEventRecord(join, x->stream2));  // the context's stream joins the second
-        BOA_HIP_TRY(hipStreamWaitEvent(s, join, 0));
+        for (int g = 1; g < G; ++g) {  // the context's stream joins the others
+            BOA_HIP_TRY(hipEventRecord(join[g - 1], gs[g]));
+            BOA_HIP_TRY(hipStreamWaitEvent(s, join[g - 1], 0));
+        }
     }
     for (int t0 = 0; !halves && t0 < positions; t0 += x->tile_len) {
         const int Tc = std::min(x->tile_len, positions - t0);
@@ -3334,12 +3347,12 @@ extern "C" int boa_decompress(boa_ctx* x, const uint32_t* d_payload, const int64
         BOA_HIP_TRY(hipStreamWaitEvent(x->stream2, join, 0));
         for (int t = 1; t < max_len; ++t) {
             for (int h = 0; h < 2; ++h) {
-                LaneView v(x, h, h ? la : 0, h ? x->stream2 : s);
+                LaneView v(x, h ? x->max_rows / 2 : 0, h ? la : 0, h ? x->stream2 : s);
                 launch_embed_tokens(x, x->tokens + x->lane0, 1, 0, 1, h ? lb : la);
             }
             for (int l = 0; l < L; ++l) {
                 for (int h = 0; h < 2; ++h) {
-                    LaneView v(x, h, h ? la : 0, h ? x->stream2 : s);
+                    LaneView v(x, h ? x->max_rows / 2 : 0, h ? la : 0, h ? x->stream2 : s);
                     const int nl = h ? lb : la;
                     rc = run_layer(x, l, nl, 1, 1);
                     if (rc) return rc;
@@ -3353,7 +3366,7 @@ extern "C" int boa_decompress(boa_ctx* x, const uint32_t* d_payload, const int64
                 }
             }
             for (int h = 0; h < 2; ++h) {
-                LaneView v(x, h, h ? la : 0, h ? x->stream2 : s);
+                LaneView v(x, h ? x->max_rows / 2 : 0, h ? la : 0, h ? x->stream2 : s);
                 const int nl = h ? lb : la;
                 const int64_t b0 = x->lane0;
                 rc = run_head(x, nl, 1, x->logits);

@@ -284,27 +284,31 @@ def test_fused_compress_kernels_match_separate_kernels(gpu, d_model, precision, 
 
 @pytest.mark.parametrize("precision", ["bf16x3", "bf16w", "f32"])
 def test_compress_in_two_halves(gpu, precision):
-    """A wave large enough (>= 512 lanes) to compress as two halves of the lanes on two streams, their scans
-    alternating: the same words as one stream, for full and partial tiles, and the stream decodes."""
+    """A wave large enough (>= 512 lanes; 768 for three groups) to compress as groups of the lanes on their own
+    streams (two, the default, and three): the same words as one stream, for full and partial tiles, and the
+    stream decodes."""
     import codec
 
     m, _ = _model(2)
     m.precision = precision
     rng = np.random.default_rng(8)
-    lens = [int(v) for v in rng.integers(1, 200, 601)]
+    lens = [int(v) for v in rng.integers(1, 200, 801)]
     chunks = [_markov(L, seed=300 + i) for i, L in enumerate(lens)]
     res = []
-    for val in ("1", "0"):
-        os.environ["BOA_COMPRESS_HALVES"] = val
+    for halves, groups in (("1", "2"), ("1", "3"), ("0", "2")):
+        os.environ["BOA_COMPRESS_HALVES"] = halves
+        os.environ["BOA_COMPRESS_GROUPS"] = groups
         try:
             m.release_engines()
             res.append(codec.compress_payload(m, chunks))
         finally:
             del os.environ["BOA_COMPRESS_HALVES"]
+            del os.environ["BOA_COMPRESS_GROUPS"]
     m.release_engines()
-    (p1, n1, f1, L1), (p0, n0, f0, L0) = res
-    assert np.array_equal(n1, n0)
-    assert np.array_equal(np.asarray(p1), np.asarray(p0))
-    out = codec.decompress_payload(m, p1, n1, L1, f1)
+    (p0, n0, f0, L0) = res[-1]
+    for p1, n1, f1, L1 in res[:-1]:
+        assert np.array_equal(n1, n0)
+        assert np.array_equal(np.asarray(p1), np.asarray(p0))
+    out = codec.decompress_payload(m, p0, n0, L0, f0)
     for i, c in enumerate(chunks):
         assert (out[i, :lens[i]] == c).all(), i
