@@ -97,6 +97,21 @@ def _uvarints(buf: bytes, lo: int, hi: int, count: int) -> np.ndarray:
     return np.add.reduceat(parts, heads)
 
 
+def _uvarints_bytes(values) -> bytes:
+    """LEB128 of every value, concatenated (the inverse of _uvarints), built without a per-value loop: row i
+    of a [n, 10] table holds value i's 7-bit groups, each flagged 0x80 when a nonzero group follows, and the
+    first max(1, significant groups) bytes of each row are kept."""
+    v = np.asarray(values, dtype=np.uint64).reshape(-1)
+    if v.size == 0:
+        return b""
+    shifts = np.arange(10, dtype=np.uint64) * np.uint64(7)  # 10 groups cover 64 bits
+    groups = (v[:, None] >> shifts[None, :]) & np.uint64(0x7F)
+    more = np.zeros(groups.shape, dtype=bool)
+    more[:, :9] = (v[:, None] >> (shifts[None, :9] + np.uint64(7))) != 0
+    keep = np.arange(10)[None, :] < 1 + more.sum(axis=1)[:, None]
+    return (groups | np.where(more, np.uint64(0x80), np.uint64(0))).astype(np.uint8)[keep].tobytes()
+
+
 class BoaFile:
     MAGIC = b"BOA2"
     IDX = b"IDX1"
@@ -133,6 +148,15 @@ class BoaFile:
             raise ValueError("Provide either 'seq_size' or 'chunks_count'.")
         count = max(-(-int(total_size) // step), 1)
         return step, count, int(total_size) - (count - 1) * step
+
+    @classmethod
+    def _index(cls, first_bytes, lengths) -> bytes:
+        """The BOA2 index (without its CRC): b"IDX1", the first byte of every chunk, then the streams' offsets
+        in the payload as deltas from the previous offset (the first is 0, each next one the previous stream's
+        length), then the streams' lengths in bytes, all as uvarints."""
+        lengths = np.asarray(lengths, dtype=np.uint64)
+        deltas = np.concatenate([np.zeros(min(1, lengths.size), dtype=np.uint64), lengths[:-1]])
+        return cls.IDX + bytes(first_bytes) + _uvarints_bytes(deltas) + _uvarints_bytes(lengths)
 
     def _read_file(self):
         """Parses a BOA2 file into compressed_data / first_bytes / lengths / metadata (boa.py:114-157).
@@ -196,15 +220,8 @@ class BoaFile:
             print(f"[compress] gpu_streams={streams} (chunk_len={chunk_len})")
         lengths, first_bytes = [], []
         with torch.inference_mode(), open(self.filepath, "wb") as f_out:
-            f_out.write(self.MAGIC)
-            f_out.write(struct.pack("<I", self.VERSION))
-            f_out.write(struct.pack("<I", 0))
-            f_out.write(struct.pack("<Q", total_size))
-            f_out.write(struct.pack("<I", chunk_len))
-            f_out.write(struct.pack("<I", n_chunks))
-            f_out.write(struct.pack("<I", last_chunk_len))
-            f_out.write(struct.pack("<B", len(fp)))
-            f_out.write(fp)
+            f_out.write(_HEADER.pack(self.MAGIC, self.VERSION, 0, total_size, chunk_len, n_chunks, last_chunk_len,
+                                     len(fp)) + fp)
             for b0 in range(0, n_chunks, streams):
                 b1 = min(b0 + streams, n_chunks)
                 chunks = [mm[i * chunk_len:min((i + 1) * chunk_len, total_size)] for i in range(b0, b1)]
@@ -212,17 +229,8 @@ class BoaFile:
                 f_out.write(payload.astype("<u4", copy=False).tobytes())
                 lengths.extend(int(w) * 4 for w in nw)
                 first_bytes.extend(int(b) & 0xFF for b in fb)
-            idx = bytearray(self.IDX)
-            idx += bytes(first_bytes)
-            prev, off = 0, 0
-            for L in lengths:
-                idx += uvarint_encode(off - prev)
-                prev = off
-                off += L
-            for L in lengths:
-                idx += uvarint_encode(L)
-            f_out.write(idx)
-            f_out.write(struct.pack("<I", zlib.crc32(idx) & 0xFFFFFFFF))
+            idx = self._index(first_bytes, lengths)
+            f_out.write(idx + _CRC.pack(zlib.crc32(idx) & 0xFFFFFFFF))
         self.compressed_data = []
         self.first_bytes = first_bytes
         self.lengths = [chunk_len] * (n_chunks - 1) + [last_chunk_len]
