@@ -107,6 +107,34 @@ def test_decode_tables_arbitrary_words(gpu, ora, P, cb, T, zero):
         assert (out[s] == ref).all(), s
 
 
+@pytest.mark.parametrize("S,T", [(1, 8), (7, 16), (33, 8), (1, 4), (9, 12), (65, 4)])
+def test_decode_tables_short_streams(gpu, ora, S, T):
+    """The throughput decoders at their smallest shapes: one stream, fewer streams than a wavefront holds, and the
+    shortest lengths each takes (8 and 16 steps for eight streams per wave; 4 and 12 for four), on encoder
+    words and on arbitrary words (stream lengths 0 .. 2 T + 2), against the oracle decoder."""
+    from boa_amd import _native as N
+
+    rng = np.random.default_rng(S * 100 + T)
+    K, P = 256, 16
+    cdf = ora.xq_cdf(rng.normal(0, 3, (S, T, K)).astype(np.float32), P)
+    syms = _sample(cdf, rng, P)
+    tables = cdf[..., :K].astype(np.uint16)
+    pitch = 2 * T + 8
+    d_cdf, d_words, d_n = _encode_gpu(gpu, P, 2, tables, syms, pitch)
+    d_out = torch.zeros((S, T), dtype=torch.uint8, device="cuda")
+    N.check(gpu.rc_decode_tables(P, 2, N.ptr(d_cdf), K, N.ptr(d_words), pitch, N.ptr(d_n), S, T, N.ptr(d_out),
+                                 N.stream_ptr()))
+    assert (d_out.cpu().numpy() == syms).all()
+    words = rng.integers(0, 1 << 32, (S, pitch), dtype=np.uint64).astype(np.uint32)
+    nw = rng.integers(0, 2 * T + 3, S).astype(np.int32)
+    d_w, d_nw = _dev(words.view(np.int32)), _dev(nw)  # held: a freed temporary's memory is reused at once
+    N.check(gpu.rc_decode_tables(P, 2, N.ptr(d_cdf), K, N.ptr(d_w), pitch, N.ptr(d_nw), S, T, N.ptr(d_out),
+                                 N.stream_ptr()))
+    out = d_out.cpu().numpy()
+    for s in range(S):
+        assert (out[s] == ora.decode_tables(P, cdf[s], words[s, :nw[s]])).all(), s
+
+
 def test_tables_empty_and_skipped_symbols(gpu, ora):
     P, K, S, T = 16, 16, 8, 40
     rng = np.random.default_rng(3)
