@@ -2,8 +2,9 @@
 // batch coder with the reference's Q2 quantiser (drop-in for gpu.queue.RangeCoderBatch; its word export
 // goes through boa_compact, compact.hip), and the fused quantiser's table export used by the parity tests.
 //
-// One chunk lane per stream throughout.  Wave-parallel work (table search, Q2 prefix sums, quantiser
-// scans) is done by one 64-wide wavefront per lane; the coder state itself is uniform across the wave.
+// One chunk lane per stream throughout.  Wave-parallel work (table search, Q2 prefix sums, quantiser scans) is
+// done by one 64-wide wavefront per lane, or, in the throughput decoders on full tables, by 8 or 16 lanes per
+// stream (8 or 4 streams per wavefront); the coder state itself is uniform across a stream's lanes.
 #include "boa_common.h"
 
 #include <stdarg.h>
