@@ -147,6 +147,43 @@ def test_decompress_fused_and_layer_kernels_agree(gpu, d_model, precision, steps
             assert (out[i, :lens[i]] == c).all(), i
 
 
+@pytest.mark.parametrize("d_model,precision", [(256, "bf16x3"), (256, "f32"), (512, "bf16w")])
+def test_decompress_arbitrary_payload(gpu, d_model, precision):
+    """Decoding words that no encoder wrote (a random payload, random word counts including 0, chunks of 1 to
+    200 bytes): it completes, returns every chunk's first byte as given, decodes the same bytes on a second
+    run, and the fused step kernel and the per-layer kernels decode the same bytes (their logits are bit
+    identical, so they take the same path through any words)."""
+    import codec
+    from boa_amd import weights as W
+
+    import model as M
+
+    if d_model == 256:
+        m, _ = _model(2)
+    else:
+        m = M.BoaConstrictor(512, 2, 256).load_blob(W.seeded_blob(W.Cfg(d_model=512, n_layers=2), 3))
+    m.precision = precision
+    rng = np.random.default_rng(17 + d_model)
+    lens = [1, 2, 50, 130, 65, 7, 200, 33]
+    nw = rng.integers(0, 60, len(lens)).astype(np.int64)
+    nw[1] = 0
+    payload = rng.integers(0, 1 << 32, int(nw.sum()), dtype=np.uint64).astype(np.uint32)
+    fb = [int(v) for v in rng.integers(0, 256, len(lens))]
+    outs = []
+    for flag in ("1", "1", "0"):
+        os.environ["BOA_FUSED_STEP"] = flag
+        try:
+            m.release_engines()
+            outs.append(codec.decompress_payload(m, payload, nw, lens, fb))
+        finally:
+            del os.environ["BOA_FUSED_STEP"]
+    m.release_engines()
+    for i, L in enumerate(lens):
+        assert int(outs[0][i, 0]) == fb[i]
+        for out in outs[1:]:
+            assert (out[i, :L] == outs[0][i, :L]).all(), i
+
+
 def test_round_trip_d512_bf16w(gpu):
     """configs[4] model shape (d_model 512, bf16 weights), 16 layers, mixed int16 / float32 records."""
     import codec
