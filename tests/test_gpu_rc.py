@@ -135,6 +135,34 @@ def test_decode_tables_short_streams(gpu, ora, S, T):
         assert (out[s] == ora.decode_tables(P, cdf[s], words[s, :nw[s]])).all(), s
 
 
+@pytest.mark.parametrize("K,T", [(2, 8), (3, 6), (4, 5)])
+@pytest.mark.parametrize("P,cb", [(16, 2), (16, 4), (24, 4)])
+@pytest.mark.parametrize("kind", ["mixed", "top"])
+def test_tables_brute_force_tiny_alphabets(gpu, ora, K, T, P, cb, kind):
+    """Every sequence of length T over K symbols, one stream each, through the same per-step tables (the tables
+    the CPU brute-force test pins against the big-integer check and the codes' lexicographic order): the GPU
+    words equal the oracle's for every stream, and the GPU decoder returns every sequence."""
+    from boa_amd import _native as N
+    from test_oracle_rc import _all_sequences, _tiny_tables
+
+    rng = np.random.default_rng(K * 100 + T * 10 + P + (kind == "top"))
+    cdf = _tiny_tables(rng, K, T, P, kind)
+    seqs = _all_sequences(K, T)
+    S = len(seqs)
+    tables = np.ascontiguousarray(np.broadcast_to(cdf[:, :K], (S, T, K))).astype(np.uint16 if cb == 2 else np.uint32)
+    pitch = T + 8
+    d_cdf, d_words, d_n = _encode_gpu(gpu, P, cb, tables, seqs, pitch)
+    words = d_words.cpu().numpy().view(np.uint32)
+    nw = d_n.cpu().numpy()
+    for s in range(S):
+        ref = ora.encode_tables(P, cdf, seqs[s])
+        assert nw[s] == len(ref) and (words[s, :nw[s]] == ref).all(), seqs[s]
+    d_out = torch.zeros((S, T), dtype=torch.uint8, device="cuda")
+    N.check(gpu.rc_decode_tables(P, cb, N.ptr(d_cdf), K, N.ptr(d_words), pitch, N.ptr(d_n), S, T, N.ptr(d_out),
+                                 N.stream_ptr()))
+    assert (d_out.cpu().numpy() == seqs).all()
+
+
 def test_tables_empty_and_skipped_symbols(gpu, ora):
     P, K, S, T = 16, 16, 8, 40
     rng = np.random.default_rng(3)
