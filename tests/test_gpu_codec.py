@@ -106,6 +106,32 @@ def test_boa_file_round_trip(gpu, tmp_path):
         del os.environ["BOA_GPU_STREAMS"]
 
 
+@pytest.mark.parametrize("data,kw,meta", [
+    (b"\x7f", {"chunks_count": 1}, (1, 1, 1)),               # one byte: the first byte only, no coded symbols
+    (b"\x00\xff", {"seq_size": 1}, (1, 2, 1)),             # two one-byte chunks: two empty streams
+    (bytes(range(5)), {"chunks_count": 7}, (1, 5, 1)),     # more chunks asked for than bytes: 5 chunks
+    (bytes(range(9)), {"chunks_count": 4}, (3, 3, 3)),     # ceil(9/4) = 3 leaves an empty 4th chunk: dropped
+    (bytes(70), {"seq_size": 65}, (65, 2, 5)),             # a tile boundary inside the first chunk
+], ids=["1B", "2x1B", "5B-7chunks", "9B-4chunks", "70B-seq65"])
+def test_boa_file_tiny_inputs(gpu, tmp_path, data, kw, meta):
+    """BoaFile at its smallest inputs: the header's (chunk_len, n_chunks, last_chunk_len), a byte-exact
+    round trip, and the empty file refused with the reference's message (boa.py:162-164)."""
+    import boa
+
+    m, _ = _model(2)
+    src = tmp_path / "in.bin"
+    src.write_bytes(data)
+    f = boa.BOA("cuda", str(tmp_path / "x.boa"), m)
+    f.compress(str(src), progress=False, **kw)
+    got = f.get_metadata()
+    assert (got["chunk_len"], got["n_chunks"], got["last_chunk_len"]) == meta
+    assert got["uncompressed_len"] == len(data)
+    assert boa.BOA("cuda", str(tmp_path / "x.boa"), m).decompress(progress=False) == data
+    src.write_bytes(b"")
+    with pytest.raises(ValueError, match="Input file is empty"):
+        f.compress(str(src), chunks_count=1, progress=False)
+
+
 @pytest.mark.parametrize("d_model,precision,steps", [(256, "bf16x3", None), (256, "f32", None),
                                                      (512, "bf16w", None), (512, "bf16x3", None),
                                                      (256, "bf16x3", "5"), (512, "bf16w", "5")])
