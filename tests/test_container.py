@@ -175,3 +175,40 @@ def test_reader_many_streams_property(tmp_path):
     assert f.compressed_data == streams
     assert f.first_bytes == first
     assert f.lengths == [5000] * 256 + [17]
+
+
+try:
+    from hypothesis import given, settings, strategies as st
+except ImportError:  # pragma: no cover
+    given = None
+
+
+@pytest.mark.skipif(given is None, reason="needs hypothesis")
+def test_hypothesis_uvarints_and_index():
+    """Generated values over the whole u64 range: the writer's vectorised encoder equals the scalar LEB128
+    encoder, the reader's vectorised decoder returns the values from any offset, and an index built from
+    generated lengths parses back to the running offsets."""
+    import boa
+
+    @settings(max_examples=300, deadline=None, database=None)
+    @given(st.lists(st.integers(0, 2**64 - 1), max_size=40), st.binary(max_size=5))
+    def run(vals, junk):
+        enc = boa._uvarints_bytes(vals)
+        assert enc == b"".join(boa.uvarint_encode(v) for v in vals)
+        buf = junk + enc + b"\x00"
+        if vals:
+            assert [int(v) for v in boa._uvarints(buf, len(junk), len(buf), len(vals))] == vals
+
+    @settings(max_examples=200, deadline=None, database=None)
+    @given(st.lists(st.integers(0, 2**40), min_size=1, max_size=30))
+    def run_index(lengths):
+        first = [(7 * i) & 0xFF for i in range(len(lengths))]
+        idx = boa.BoaFile._index(first, lengths)
+        n = len(lengths)
+        assert idx[:4] == b"IDX1" and list(idx[4:4 + n]) == first
+        vals = [int(v) for v in boa._uvarints(idx, 4 + n, len(idx), 2 * n)]
+        offs = np.cumsum(vals[:n]).tolist()
+        assert offs == np.concatenate([[0], np.cumsum(lengths)[:-1]]).tolist() and vals[n:] == lengths
+
+    run()
+    run_index()

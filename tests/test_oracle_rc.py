@@ -203,3 +203,46 @@ def test_brute_force_tiny_alphabets(ora, K, T, P, kind):
     width = max(len(c) for c in codes)
     padded = [tuple(c + [0] * (width - len(c))) for c in codes]
     assert all(a < b for a, b in zip(padded, padded[1:]))
+
+
+try:
+    from hypothesis import HealthCheck, given, settings, strategies as st
+except ImportError:  # pragma: no cover
+    given = None
+
+
+@pytest.mark.skipif(given is None, reason="needs hypothesis")
+def test_hypothesis_round_trip(ora):
+    """Generated tables and symbols (frequencies down to 1, cut points at the ends of [1, 2^P - 1], empty and
+    one-symbol streams, one table per step): the words lie in the final interval (big-integer check), decode
+    to the symbols, and obey the two-sided length bound."""
+
+    @st.composite
+    def case(draw):
+        P = draw(st.sampled_from([16, 24]))
+        K = draw(st.integers(2, 24))
+        T = draw(st.integers(0, 24))
+        cuts = st.sets(st.integers(1, (1 << P) - 1), min_size=K - 1, max_size=K - 1)
+        shared = draw(st.booleans())
+        rows = [sorted(draw(cuts))] * T if shared and T else [sorted(draw(cuts)) for _ in range(T)]
+        syms = draw(st.lists(st.integers(0, K - 1), min_size=T, max_size=T))
+        return P, K, rows, syms
+
+    @settings(max_examples=400, deadline=None, database=None, suppress_health_check=[HealthCheck.too_slow])
+    @given(case())
+    def run(c):
+        P, K, rows, syms = c
+        T = len(syms)
+        cdf = np.array([[0] + r + [1 << P] for r in rows], dtype=np.uint32).reshape(T, K + 1)
+        s = np.array(syms, dtype=np.int32)
+        words = ora.encode_tables(P, cdf, s)
+        steps = [(int(cdf[t, v]), int(cdf[t, v + 1] - cdf[t, v])) for t, v in enumerate(syms)]
+        bigint_check.check(words, steps, P)
+        if T:
+            assert (ora.decode_tables(P, cdf, words) == s).all()
+            info = -sum(math.log2(f / (1 << P)) for _, f in steps)
+            assert math.ceil(info - 1e-9) <= 32 * len(words) < info + 64 - T * math.log2(1 - 2.0 ** (P - 32)) + 1e-9
+        else:
+            assert len(words) == 0
+
+    run()
