@@ -120,6 +120,45 @@ def test_quantiser_tables_bit_exact(gpu, ora):
         assert (got == ref).all()
 
 
+def _dev_f32(a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).cuda()
+
+
+def test_quantiser_tables_adversarial_rows(gpu, ora):
+    """The XQ quantiser on rows no model emits: infinities, NaN (some or all entries), values whose differences
+    overflow to -inf, all entries equal, one peak with every other entry far below it, differences at the
+    smallest normal scale, and subnormal logits.  Every GPU table equals the oracle's and is a valid table."""
+    from boa_amd import _native as N
+
+    K = 256
+    rng = np.random.default_rng(9)
+    base = rng.normal(0, 3, K).astype(np.float32)
+    rows = []
+    for v in (np.inf, -np.inf, np.nan):
+        r = base.copy(); r[17] = v; rows.append(r)
+    r = base.copy(); r[::3] = np.nan; rows.append(r)
+    rows.append(np.full(K, -np.inf, np.float32))
+    rows.append(np.full(K, np.inf, np.float32))
+    r = np.full(K, -3e38, np.float32); r[200] = 3e38; rows.append(r)
+    r = np.where(rng.random(K) < 0.5, 3e38, -3e38).astype(np.float32); rows.append(r)
+    rows.append(np.full(K, 7.25, np.float32))
+    r = np.full(K, -87.5, np.float32); r[0] = 0.0; rows.append(r)
+    r = np.full(K, -86.9, np.float32); r[255] = 0.0; rows.append(r)
+    rows.append((rng.integers(-4, 5, K) * np.float32(1.2e-38)).astype(np.float32))
+    rows.append((rng.integers(0, 1000, K) * np.float32(1e-45)).astype(np.float32))
+    x = np.stack(rows).astype(np.float32)
+    d_x = _dev_f32(x)
+    for P in (16, 24):
+        d_cdf = torch.empty((x.shape[0], K + 1), dtype=torch.int32, device="cuda")
+        N.check(gpu.boa_xq_cdf(N.ptr(d_x), x.shape[0], K, P, N.ptr(d_cdf), N.stream_ptr()))
+        got = d_cdf.cpu().numpy().view(np.uint32)
+        ref = ora.xq_cdf(x, P)
+        for i in range(x.shape[0]):
+            assert (got[i] == ref[i]).all(), i
+        c = got.astype(np.int64)
+        assert (c[:, 0] == 0).all() and (c[:, -1] == 1 << P).all() and (np.diff(c, axis=1) >= 1).all()
+
+
 def test_zero_weights_give_bias_only_logits(gpu):
     """Closed form: with every matrix zero, logits = head.2.bias whatever the input."""
     from boa_amd import weights as W

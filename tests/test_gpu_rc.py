@@ -248,6 +248,48 @@ def test_range_coder_batch_matches_q2_oracle(gpu, ora, K):
         assert (got[:lens[i], i] == syms[:lens[i], i]).all(), i
 
 
+def test_range_coder_batch_adversarial_probs(gpu, ora):
+    """RangeCoderBatch's Q2 on probability rows no softmax emits: all zero, NaN or +inf entries (the uniform
+    fallback), entries whose float sum overflows but whose double sum does not, subnormal entries only, one
+    nonzero entry, and zeros mixed with ordinary values.  Words equal the oracle's for every lane and decode
+    back to the symbols."""
+    import gpu_range_coder as gr
+
+    K, T = 256, 40
+    rng = np.random.default_rng(21)
+    base = _softmax(rng.normal(0, 3, K))
+    rows = [np.zeros(K, np.float32)]
+    r = base.copy(); r[5] = np.nan; rows.append(r)
+    r = base.copy(); r[9] = np.inf; rows.append(r)
+    rows.append(np.full(K, 3e38, np.float32))
+    r = np.zeros(K, np.float32); r[::7] = 3.3e38; rows.append(r)
+    rows.append((rng.integers(1, 100, K) * np.float32(1e-45)).astype(np.float32))
+    r = np.zeros(K, np.float32); r[255] = 1.0; rows.append(r)
+    r = np.zeros(K, np.float32); r[0] = 1e-45; rows.append(r)
+    r = base.copy(); r[rng.random(K) < 0.6] = 0.0; rows.append(r)
+    probs = np.stack(rows).astype(np.float32)                  # [N, K], the same rows at every step
+    N = probs.shape[0]
+    tables = np.stack([ora.q2_cdf(probs[i:i + 1], 24)[0] for i in range(N)]).astype(np.int64)
+    assert (np.diff(tables, axis=1) >= 1).all()
+    syms = rng.integers(0, K, (T, N)).astype(np.int32)
+    d_probs = _dev(probs)
+    b = gr.gpu.queue.RangeCoderBatch(N, K, T)
+    for t in range(T):
+        b.encode_step(_dev(syms[t]), d_probs)
+    b.finalize()
+    comp = b.get_compressed_list()
+    for i in range(N):
+        ref = ora.encode_probs_q2(24, np.repeat(probs[i:i + 1], T, 0), syms[:, i])
+        assert (comp[i] == ref).all(), i
+    d = gr.gpu.queue.RangeCoderBatch(N, K, T)
+    d.load_compressed_list(comp)
+    d.init_decoder()
+    out = torch.full((N,), -1, dtype=torch.int32, device="cuda")
+    for t in range(T):
+        d.decode_step(d_probs, out)
+        assert (out.cpu().numpy() == syms[t]).all(), t
+
+
 def test_range_coder_batch_errors(gpu):
     import gpu_range_coder as gr
 
