@@ -212,3 +212,18 @@ def test_hypothesis_uvarints_and_index():
 
     run()
     run_index()
+
+
+def test_wave_lanes_env_override(monkeypatch):
+    """BOA_GPU_STREAMS fixes the lanes per wave as in the reference (boa.py:207-210): an unparsable value
+    means 5000, and the result is clamped to [1, n_chunks]; the model is not consulted."""
+    import boa
+
+    class NoModel:
+        def plan_wave_lanes(self, *a):
+            raise AssertionError("model consulted despite BOA_GPU_STREAMS")
+
+    for env, n, want in [("3", 10, 3), ("abc", 9000, 5000), ("abc", 40, 40), ("0", 10, 1), ("-5", 10, 1),
+                         ("100000", 16384, 16384), (" 7 ", 10, 7)]:
+        monkeypatch.setenv("BOA_GPU_STREAMS", env)
+        assert boa._wave_lanes(NoModel(), n, 1024) == want, env
