@@ -27,9 +27,12 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 if HERE not in sys.path:
     sys.path.insert(0, HERE)
 
-# The reference's --precision choices (main.py:59) map onto this build's GEMM arithmetic: "fp32" is the
-# split-bfloat16 x3 mode (fp32-accurate); the build's own mode names are accepted as well.
-PRECISION_MAP = {"fp32": "bf16x3", "bf16x3": "bf16x3", "f32": "f32", "bf16w": "bf16w"}
+# The reference's --precision choices (main.py:59) map onto this build's GEMM arithmetic: "fp32" is plain
+# float32 arithmetic (fp32 MFMA, the "f32" mode), as the reference computes it.  The build's own mode names
+# are accepted as well: "bf16x3" (fp32 operands split into bfloat16 hi + lo, three products, fp32
+# accumulation; faster, about 16 significant bits per operand) and "bf16w" (bfloat16 weights).  The
+# reference's "fp16" / "fp8" choices select training precisions that this build does not have.
+PRECISION_MAP = {"fp32": "f32", "f32": "f32", "bf16x3": "bf16x3", "bf16w": "bf16w"}
 UNSUPPORTED_FLAGS = ("new_experiment", "train_only", "evaluate", "evaluate_only", "comparison_baseline_only")
 
 

@@ -22,7 +22,21 @@ def test_resolve_config_keys(tmp_path):
     assert r["src"] == (tmp_path / "data" / "in.bin").resolve()
     assert r["model_path"] == (tmp_path / "m.bin").resolve()
     assert (r["chunks_count"], r["num_layers"], r["verify"], r["progress"]) == (7, 2, True, False)
-    assert r["precision"] == "bf16x3"  # the reference's default "fp32"
+    assert r["precision"] == "f32"  # the reference's default "fp32" is plain float32 arithmetic
+
+
+@pytest.mark.parametrize("flag,mode", [("fp32", "f32"), ("f32", "f32"), ("bf16x3", "bf16x3"), ("bf16w", "bf16w")])
+def test_precision_flag_mapping(tmp_path, flag, mode):
+    """--precision fp32 (main.py:59, the reference's default) selects the fp32 MFMA mode; the narrower
+    split-bfloat16 modes are chosen only by their own names, from the flag or the config key."""
+    import cli
+
+    p = _cfg(tmp_path, "file_path: x.bin\n")
+    assert cli.resolve(cli.parse_args(["-c", str(p), "--precision", flag]), cli.load_config(p))["precision"] == mode
+    q = _cfg(tmp_path, f"file_path: x.bin\nprecision: {flag}\n")
+    assert cli.resolve(cli.parse_args(["-c", str(q)]), cli.load_config(q))["precision"] == mode
+    with pytest.raises(SystemExit):
+        cli.parse_args(["-c", str(p), "--precision", "fp16"])
 
 
 def test_resolve_defaults_and_rejections(tmp_path):
