@@ -17,14 +17,15 @@ Also reported: compress and decompress rates separately, the roofline of the dom
 event timing (boa_profile) inside the timed region, and a CPU baseline: this repo's restatement of the
 reference CPU path (codec.compress_CPU / decompress_CPU: per-step torch-CPU model + per-lane range coding in
 a thread pool) timed on a bounded sample of configs[0] on this host.  After the timed steps, untimed by the
-headline, four bounded extra measurements go into the same JSON line (--no-extras skips them):
-  f32_*      the same model and data in "f32" mode (plain fp32 MFMA, the reference's precision) on a stated
-             sub-size of the workload;
-  published_shape  the shape of the reference's only published throughput (d256 x 1 layer, 4096-byte
-             chunks; ~7 / ~5 MiB/s on an RTX 5090) in f32, on the headline's data;
+headline, bounded extra measurements go into the same JSON line (--no-extras skips them):
+  f32_full_* configs[2]+[3] at full size in "f32" mode (every GEMM in plain fp32 MFMA, the reference's
+             arithmetic): the same model and data, one timed compress + decompress of the whole payload,
+             with a roofline for each half;
   coder      configs[1], the range coder alone: 16384 streams x 4096 symbols, P = 16;
   config4    configs[4]'s model (d512 x 16 layers, bf16 weights, seed 1) on its 16384 chunks of mixed
-             int16/float32 records, each chunk cut to a stated length (steady-state rates).
+             int16/float32 records, each chunk cut to a stated length (steady-state rates);
+  published_shape  (only with --published-shape) the shape of the reference's only published throughput
+             (d256 x 1 layer, 4096-byte chunks; ~7 / ~5 MiB/s on an RTX 5090) in f32, on the headline's data.
 """
 from __future__ import annotations
 
@@ -43,6 +44,7 @@ for _p in (REPO, os.path.join(REPO, "boa-constrictor_amd")):
 METRIC = "input MB/s compress + decompress, d256×8L Mamba, 4096 chunks, 1 GPU"
 PEAK_BF16_MFMA_TFLOPS = 2500.0  # dense; a bf16x3 GEMM issues 3 bf16 products per model multiply-add
 PEAK_HBM_GBPS = 8000.0
+PEAK_F32_MFMA_TFLOPS = 157.3  # dense fp32 MFMA (v_mfma_f32_16x16x4_f32)
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_fused_step_d256x8L_4096lanes.json")
 CODER_TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_rc_coder_configs1.json")
 
@@ -342,8 +344,8 @@ def codec_pass(lib, eng, X, lens, lens_h, chunk: int, reps: int, warm: int):
                                 ctypes.byref(total), stream))
         torch.cuda.synchronize()
         t1 = time.perf_counter()
-        N.check(lib.boa_decompress(eng.h, N.ptr(payload), N.ptr(offs), N.ptr(nw), N.ptr(first), N.ptr(lens), B,
-                                   chunk, N.ptr(out), out.stride(0)))
+        N.check(lib.boa_decompress(eng.h, N.ptr(payload), total.value, N.ptr(offs), N.ptr(nw), N.ptr(first),
+                                   N.ptr(lens), B, chunk, N.ptr(out), out.stride(0)))
         torch.cuda.synchronize()
         t2 = time.perf_counter()
         if i >= warm:
@@ -352,27 +354,111 @@ def codec_pass(lib, eng, X, lens, lens_h, chunk: int, reps: int, warm: int):
     return float(np.mean(tcs)), float(np.mean(tds)), 4 * int(nw.sum().item()), lanes_equal(out, X, lens_h)
 
 
-def f32_extra(lib, X, lens_h, sub_len: int) -> dict:
-    """The headline's model and data in "f32" mode (fp32 MFMA GEMMs, the reference's arithmetic) on the
-    first sub_len bytes of every chunk."""
+def read_profile(lib, eng) -> dict:
+    """Per-class event timings recorded by boa_profile since the window was opened."""
+    from boa_amd import _native as N
+
+    ents = (N.ProfEntry * 32)()
+    n = ctypes.c_int32(0)
+    N.check(lib.boa_profile_read(eng.h, ents, 32, ctypes.byref(n)))
+    return {e.name.decode(): dict(launches=e.launches, sampled=e.sampled, ms=e.ms, flops=e.flops, bytes=e.bytes)
+            for e in ents[:n.value]}
+
+
+def f32_full_extra(lib, X, lens_h, chunk: int, warm_len: int) -> dict:
+    """configs[2]+[3] at full size in the reference's arithmetic: the headline's model and data in "f32" mode
+    (every GEMM in fp32 MFMA, v_mfma_f32_16x16x4_f32; the reference computes them as fp32 FMAs,
+    gemm_kernels.cu:168-280).  One untimed warm-up pass on the first warm_len bytes of every chunk, then one
+    timed compress (+ compaction) and decompress of the whole payload, with each kernel class's HIP events
+    recorded (boa_profile) for the rooflines:
+      compress    model GEMM flops (15,466,496 per coded position: every projection, dt_proj included,
+                  15,466,496 = 2 x 7,733,248 multiply-adds) / compress time, against the fp32 MFMA peak;
+      decompress  the fused decode kernel's average launch: its GEMM flops against the fp32 MFMA peak, and its
+                  compulsory bytes (SSM state read + write, conv history, embedding rows, coder state, the
+                  fp32 weights once per step) against HBM."""
+    import numpy as np
     import torch
 
+    from boa_amd import _native as N
     from boa_amd import weights as W
     import model as M
 
     B = X.shape[0]
-    Xs = X[:, :sub_len].contiguous()
-    ls = [min(sub_len, v) for v in lens_h]
-    lens = torch.tensor(ls, dtype=torch.int32, device="cuda")
     cfg = W.Cfg()
     eng = M._Engine(W.seeded_blob(cfg, 0), cfg, B, 64, precision="f32")
-    tc, td, cb, ok = codec_pass(lib, eng, Xs, lens, ls, sub_len, reps=1, warm=1)
-    nb = sum(ls)
-    del eng
-    return {"f32_compress_MBps": nb / tc / 1e6, "f32_decompress_MBps": nb / td / 1e6, "f32_round_trip_ok": ok,
-            "f32_compressed_bytes": cb, "f32_decompress_step_ms": td / (sub_len - 1) * 1e3,
-            "f32_sample": f"{B} chunks x first {sub_len} B of each (same data and model), GEMMs in fp32 MFMA, "
-                          "one warm-up and one timed pass"}
+    Xw = X[:, :warm_len].contiguous()
+    lw = [min(warm_len, v) for v in lens_h]
+    codec_pass(lib, eng, Xw, torch.tensor(lw, dtype=torch.int32, device="cuda"), lw, warm_len, reps=1, warm=0)
+    lens = torch.tensor(lens_h, dtype=torch.int32, device="cuda")
+    pitch = chunk + 8
+    words = torch.empty((B, pitch), dtype=torch.int32, device="cuda")
+    nw = torch.empty(B, dtype=torch.int32, device="cuda")
+    offs = torch.empty(B, dtype=torch.int64, device="cuda")
+    payload = torch.empty(B * pitch, dtype=torch.int32, device="cuda")
+    out = torch.empty((B, chunk), dtype=torch.uint8, device="cuda")
+    first = X[:, 0].contiguous()
+    stream = N.stream_ptr()
+    torch.cuda.synchronize()
+    N.check(lib.boa_profile(eng.h, 1))
+    t0 = time.perf_counter()
+    N.check(lib.boa_compress(eng.h, N.ptr(X), X.stride(0), N.ptr(lens), B, chunk, N.ptr(words), pitch, N.ptr(nw)))
+    total = ctypes.c_int64(0)
+    N.check(lib.boa_compact(N.ptr(words), pitch, N.ptr(nw), B, N.ptr(offs), N.ptr(payload), payload.numel(),
+                            ctypes.byref(total), stream))
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    pc = read_profile(lib, eng)
+    N.check(lib.boa_profile(eng.h, 1))
+    t1b = time.perf_counter()
+    N.check(lib.boa_decompress(eng.h, N.ptr(payload), total.value, N.ptr(offs), N.ptr(nw), N.ptr(first),
+                               N.ptr(lens), B, chunk, N.ptr(out), out.stride(0)))
+    torch.cuda.synchronize()
+    t2 = time.perf_counter()
+    pd = read_profile(lib, eng)
+    N.check(lib.boa_profile(eng.h, 0))
+    ok = lanes_equal(out, X, lens_h)
+    tc, td = t1 - t0, t2 - t1b
+    nbytes = sum(lens_h)
+    positions = sum(max(v - 1, 0) for v in lens_h)
+    fpp = 2.0 * model_macs_per_token(256, 8)
+    res = {
+        "f32_full_workload": (f"configs[2]+configs[3] in f32 mode (fp32 MFMA GEMMs, the reference's arithmetic): "
+                              f"the headline's model and data, {B} chunks x {chunk} B, one warm-up pass on the "
+                              f"first {warm_len} B of every chunk, then one timed compress + decompress of the "
+                              "whole payload"),
+        "f32_full_compress_MBps": nbytes / tc / 1e6, "f32_full_decompress_MBps": nbytes / td / 1e6,
+        "f32_full_compress_MiBps": nbytes / tc / 2**20, "f32_full_decompress_MiBps": nbytes / td / 2**20,
+        "f32_full_MBps": nbytes / (tc + td) / 1e6,
+        "f32_full_decompress_step_ms": td / (chunk - 1) * 1e3,
+        "f32_full_compressed_bytes": 4 * int(total.value), "f32_full_round_trip_ok": ok,
+        "f32_full_roofline_compress": {"bound": "mfma", "achieved": positions * fpp / tc / 1e12,
+                                       "peak": PEAK_F32_MFMA_TFLOPS, "unit": "TFLOP/s",
+                                       "frac": positions * fpp / tc / 1e12 / PEAK_F32_MFMA_TFLOPS,
+                                       "flops_per_position": fpp, "positions": positions,
+                                       "note": "whole compress pass (all kernels) against the fp32 MFMA peak"},
+        "f32_full_kernel_ms": {f"{ph}/{k}": round(e["ms"] * e["launches"] / e["sampled"], 3)
+                               for ph, pp in (("compress", pc), ("decompress", pd)) for k, e in pp.items()
+                               if e["sampled"]},
+    }
+    e = pd.get("fused_step")
+    if e and e["sampled"]:
+        avg_ms = e["ms"] / e["sampled"]
+        per_launch_bytes = e["bytes"] / e["sampled"]
+        steps = per_launch_bytes / fused_step_bytes(B)
+        per_launch_flops = steps * B * fpp
+        res["f32_full_roofline_decompress"] = {
+            "kernel": "decompress/fused_step", "rocprof_name": "k_fused_step<1, 512>", "avg_launch_ms": avg_ms,
+            "launches": e["launches"], "steps_per_launch": round(steps, 3),
+            "mfma": {"bound": "mfma", "achieved": per_launch_flops / (avg_ms * 1e-3) / 1e12,
+                     "peak": PEAK_F32_MFMA_TFLOPS, "unit": "TFLOP/s",
+                     "frac": per_launch_flops / (avg_ms * 1e-3) / 1e12 / PEAK_F32_MFMA_TFLOPS,
+                     "flops_per_launch": per_launch_flops},
+            "hbm": {"bound": "hbm", "achieved": per_launch_bytes / (avg_ms * 1e-3) / 1e9, "peak": PEAK_HBM_GBPS,
+                    "unit": "GB/s", "frac": per_launch_bytes / (avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBPS,
+                    "bytes_per_launch": per_launch_bytes}}
+    del eng, words, payload, offs, out
+    torch.cuda.empty_cache()
+    return res
 
 
 def published_shape_extra(lib, X, lens_h, sub_len: int) -> dict:
@@ -482,11 +568,17 @@ def main():
     ap.add_argument("--coder-len", type=int, default=4096)
     ap.add_argument("--coder-cpu-streams", type=int, default=64)
     ap.add_argument("--no-extras", action="store_true", help="skip the f32, coder and configs[4] extras")
-    ap.add_argument("--f32-len", type=int, default=1024, help="bytes per chunk of the f32-mode extra")
+    ap.add_argument("--f32-warm-len", type=int, default=256,
+                    help="bytes per chunk of the untimed warm-up before the full-size f32-mode pass")
+    ap.add_argument("--no-f32-full", action="store_true", help="skip the full-size f32-mode pass")
+    ap.add_argument("--published-shape", action="store_true",
+                    help="also run the published-shape extra (d256x1L in f32 mode; off by default, so that the "
+                         "f32 kernels' profile averages describe the 8-layer model alone)")
     ap.add_argument("--pub-len", type=int, default=4096,
                     help="bytes per chunk of the published-shape extra (d256x1L; the reference's chunk size)")
     ap.add_argument("--c4-lanes", type=int, default=16384, help="chunks (= lanes) of the configs[4] extra")
-    ap.add_argument("--c4-len", type=int, default=256, help="bytes per chunk of the configs[4] extra")
+    ap.add_argument("--c4-len", type=int, default=257,
+                    help="bytes per chunk of the configs[4] extra (257: 256 coded positions, four whole tiles)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy 3 times (PMC byte-counter calibration)")
     args = ap.parse_args()
@@ -553,18 +645,11 @@ def main():
                                 ctypes.byref(total), stream))
         torch.cuda.synchronize()
         t1 = time.perf_counter()
-        N.check(lib.boa_decompress(eng.h, N.ptr(payload), N.ptr(offs), N.ptr(nw), N.ptr(first), N.ptr(lens), B, chunk,
-                                   N.ptr(out), out.stride(0)))
+        N.check(lib.boa_decompress(eng.h, N.ptr(payload), total.value, N.ptr(offs), N.ptr(nw), N.ptr(first),
+                                   N.ptr(lens), B, chunk, N.ptr(out), out.stride(0)))
         torch.cuda.synchronize()
         t2 = time.perf_counter()
         return t1 - t0, t2 - t1, total.value
-
-    def read_profile():
-        ents = (N.ProfEntry * 32)()
-        n = ctypes.c_int32(0)
-        N.check(lib.boa_profile_read(eng.h, ents, 32, ctypes.byref(n)))
-        return {e.name.decode(): dict(launches=e.launches, sampled=e.sampled, ms=e.ms, flops=e.flops, bytes=e.bytes)
-                for e in ents[:n.value]}
 
     for i in range(args.warmup):
         tc, td, tw = step()
@@ -581,14 +666,14 @@ def main():
                                 ctypes.byref(total), stream))
         torch.cuda.synchronize()
         t1 = time.perf_counter()
-        pc = read_profile()
+        pc = read_profile(lib, eng)
         N.check(lib.boa_profile(eng.h, 1))
         t1b = time.perf_counter()
-        N.check(lib.boa_decompress(eng.h, N.ptr(payload), N.ptr(offs), N.ptr(nw), N.ptr(first), N.ptr(lens), B, chunk,
-                                   N.ptr(out), out.stride(0)))
+        N.check(lib.boa_decompress(eng.h, N.ptr(payload), total.value, N.ptr(offs), N.ptr(nw), N.ptr(first),
+                                   N.ptr(lens), B, chunk, N.ptr(out), out.stride(0)))
         torch.cuda.synchronize()
         t2 = time.perf_counter()
-        pd = read_profile()
+        pd = read_profile(lib, eng)
         N.check(lib.boa_profile(eng.h, 0))
         tcs.append(t1 - t0)
         tds.append(t2 - t1b)
@@ -656,17 +741,21 @@ def main():
 
     extras = {}
     if not args.no_extras:
-        del words, payload, offs
-        log(f"[bench] extra: f32 mode on the first {args.f32_len} B of each chunk")
-        extras.update(f32_extra(lib, X, lens_h, args.f32_len))
-        log(f"[bench] extra: f32 compress {extras['f32_compress_MBps']:.3f} MB/s, decompress "
-            f"{extras['f32_decompress_MBps']:.3f} MB/s, round trip {extras['f32_round_trip_ok']}")
-        del eng
+        del words, payload, offs, eng
         torch.cuda.empty_cache()
-        log(f"[bench] extra: the published shape (d256x1L, first {args.pub_len} B of each chunk)")
-        extras["published_shape"] = published_shape_extra(lib, X, lens_h, args.pub_len)
-        log(f"[bench] extra: d256x1L f32 compress {extras['published_shape']['f32']['compress_MiBps']:.2f} MiB/s, "
-            f"decompress {extras['published_shape']['f32']['decompress_MiBps']:.2f} MiB/s")
+        if not args.no_f32_full:
+            log(f"[bench] extra: f32 mode, full size ({B} chunks x {chunk} B)")
+            extras.update(f32_full_extra(lib, X, lens_h, chunk, args.f32_warm_len))
+            log(f"[bench] extra: f32 compress {extras['f32_full_compress_MBps']:.3f} MB/s, decompress "
+                f"{extras['f32_full_decompress_MBps']:.3f} MB/s "
+                f"({extras['f32_full_decompress_step_ms']:.3f} ms per step), round trip "
+                f"{extras['f32_full_round_trip_ok']}")
+        if args.published_shape:
+            log(f"[bench] extra: the published shape (d256x1L, first {args.pub_len} B of each chunk)")
+            extras["published_shape"] = published_shape_extra(lib, X, lens_h, args.pub_len)
+            log(f"[bench] extra: d256x1L f32 compress "
+                f"{extras['published_shape']['f32']['compress_MiBps']:.2f} MiB/s, decompress "
+                f"{extras['published_shape']['f32']['decompress_MiBps']:.2f} MiB/s")
         log("[bench] extra: range coder alone (configs[1])")
         extras["coder"] = coder_bench(args, 3, 1, args.coder_cpu_streams if not args.no_cpu else 0)
         log(f"[bench] extra: coder {extras['coder']['value'] / 1e9:.2f} G symbols/s, round trip "

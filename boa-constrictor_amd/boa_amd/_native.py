@@ -81,7 +81,7 @@ SIGNATURES = [
     ("boa_profile", ctypes.c_int, [_P, ctypes.c_int]),
     ("boa_profile_read", ctypes.c_int, [_P, _P, _I32, ctypes.POINTER(_I32)]),
     ("boa_compress", ctypes.c_int, [_P, _P, _I64, _P, _I32, _I32, _P, _I64, _P]),
-    ("boa_decompress", ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I32, _I32, _P, _I64]),
+    ("boa_decompress", ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _P, _I32, _I32, _P, _I64]),
     ("boa_xq_cdf", ctypes.c_int, [_P, _I64, _I32, _I32, _P, _P]),
     ("boa_compact", ctypes.c_int, [_P, _I64, _P, _I32, _P, _P, _I64, ctypes.POINTER(_I64), _P]),
     ("boa_compact_noalloc", ctypes.c_int, [_P, _I64, _P, _I32, _P, _P, _I64, ctypes.POINTER(_I64), _P]),
@@ -111,11 +111,19 @@ def _bind(lib):
     return lib
 
 
+# The C ABI these signatures describe (boa_abi_version); 2: boa_decompress takes the payload's length.
+ABI_VERSION = 2
+
+
 def load_cdll():
-    """Loads the shared library and binds every signature (no GPU needed)."""
+    """Loads the shared library, checks its ABI version and binds every signature (no GPU needed)."""
     if not os.path.exists(LIB_PATH):
         raise RuntimeError(f"libboa_hip.so not built ({LIB_PATH}); run __graft_entry__.build()")
-    return _bind(ctypes.CDLL(LIB_PATH))
+    L = _bind(ctypes.CDLL(LIB_PATH))
+    if L.boa_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"libboa_hip.so has ABI {L.boa_abi_version()}, this package needs {ABI_VERSION}: "
+                           "rebuild it (__graft_entry__.build())")
+    return L
 
 
 def lib():

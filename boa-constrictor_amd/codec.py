@@ -79,6 +79,7 @@ def decompress_payload(model, payload: np.ndarray, nwords: Sequence[int], full_l
     offs = np.concatenate([[0], np.cumsum(nw)[:-1]]).astype(np.int64)
     dev = torch.device("cuda")
     pl = np.ascontiguousarray(payload, dtype=np.uint32)
+    total = int(pl.size)
     if pl.size == 0:
         pl = np.zeros(1, dtype=np.uint32)
     d_payload = torch.from_numpy(pl.view(np.int32)).to(dev)
@@ -88,7 +89,7 @@ def decompress_payload(model, payload: np.ndarray, nwords: Sequence[int], full_l
     d_lens = torch.tensor([int(v) for v in full_lens], dtype=torch.int32).to(dev)
     out = torch.empty((N, maxL), dtype=torch.uint8, device=dev)
     eng = model.engine(N, 1)
-    _nat.check(_nat.lib().boa_decompress(eng.h, _nat.ptr(d_payload), _nat.ptr(d_off), _nat.ptr(d_nw),
+    _nat.check(_nat.lib().boa_decompress(eng.h, _nat.ptr(d_payload), total, _nat.ptr(d_off), _nat.ptr(d_nw),
                                          _nat.ptr(d_first), _nat.ptr(d_lens), N, maxL, _nat.ptr(out), out.stride(0)))
     return out.cpu().numpy()
 

@@ -570,7 +570,8 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
             const int64_t b = b0 + r;
             if (t >= a.lens[b]) continue;
             DecState st = a.dec[b];
-            const int s = decode_row(sLog + r * LRES, V, lane, st, a.payload + a.off[b], a.nwords[b]);
+            const LaneWords w = lane_words(a.payload, a.payload_words, a.off, a.nwords, b);
+            const int s = decode_row(sLog + r * LRES, V, lane, st, w.p, w.n);
             if (lane == 0) {
                 a.dec[b] = st;
                 sTok[r] = s;

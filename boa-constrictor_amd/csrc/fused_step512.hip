@@ -766,7 +766,8 @@ __global__ void __launch_bounds__(NTHR, 1) k_fused_step512(FusedArgs a0) {
             const int64_t b = b0 + r;
             if (t >= a.lens[b]) continue;
             DecState st = a.dec[b];
-            const int s = decode_row(sF + r * LLOG, VV, lane, st, a.payload + a.off[b], a.nwords[b]);
+            const LaneWords w = lane_words(a.payload, a.payload_words, a.off, a.nwords, b);
+            const int s = decode_row(sF + r * LLOG, VV, lane, st, w.p, w.n);
             tokv = lane == q ? s : tokv;
             if (lane == 0) {
                 a.dec[b] = st;

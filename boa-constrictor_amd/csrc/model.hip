@@ -47,7 +47,7 @@ int boa_fail_hip(hipError_t e, const char* what, const char* file, int line) {
 }
 
 extern "C" const char* boa_last_error(void) { return g_last_error.c_str(); }
-extern "C" int boa_abi_version(void) { return 1; }
+extern "C" int boa_abi_version(void) { return 2; }  // 2: boa_decompress takes payload_words
 
 extern "C" int boa_is_device_pointer(const void* p) {
     hipPointerAttribute_t a;
@@ -2137,13 +2137,14 @@ __global__ void k_enc_finish(EncState* states, uint32_t* words, int64_t pitch, i
     if (st.overflow) overflow[0] = 1;
 }
 
-__global__ void k_dec_init(DecState* states, const uint32_t* payload, const int64_t* off, const int32_t* nwords,
-                           const uint8_t* first, const int32_t* lens, int32_t* tokens, uint8_t* out,
-                           int64_t out_stride, int n) {
+__global__ void k_dec_init(DecState* states, const uint32_t* payload, int64_t payload_words, const int64_t* off,
+                           const int32_t* nwords, const uint8_t* first, const int32_t* lens, int32_t* tokens,
+                           uint8_t* out, int64_t out_stride, int n) {
     const int b = blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= n) return;
     DecState st;
-    dec_init(st, payload + off[b], nwords[b]);
+    const LaneWords w = lane_words(payload, payload_words, off, nwords, b);
+    dec_init(st, w.p, w.n);
     states[b] = st;
     tokens[b] = first[b];
     if (lens[b] >= 1) out[(int64_t)b * out_stride] = first[b];
@@ -2153,7 +2154,7 @@ __global__ void k_dec_init(DecState* states, const uint32_t* payload, const int6
 // coder state points into, advance the state, emit the byte and feed it back as the next token.
 __global__ void __launch_bounds__(64) k_decode_step(const float* __restrict__ logits, int V, int t,
                                                    const int32_t* __restrict__ lens, DecState* __restrict__ states,
-                                                   const uint32_t* __restrict__ payload,
+                                                   const uint32_t* __restrict__ payload, int64_t payload_words,
                                                    const int64_t* __restrict__ off, const int32_t* __restrict__ nwords,
                                                    int32_t* __restrict__ tokens, uint8_t* __restrict__ out,
                                                    int64_t out_stride) {
@@ -2161,7 +2162,8 @@ __global__ void __launch_bounds__(64) k_decode_step(const float* __restrict__ lo
     const int lane = threadIdx.x;
     if (t >= lens[b]) return;
     DecState st = states[b];
-    const int s = decode_row(logits + b * V, V, lane, st, payload + off[b], nwords[b]);
+    const LaneWords w = lane_words(payload, payload_words, off, nwords, b);
+    const int s = decode_row(logits + b * V, V, lane, st, w.p, w.n);
     if (lane == 0) {
         states[b] = st;
         tokens[b] = s;
@@ -3110,14 +3112,15 @@ static hipError_t launch_fused(const boa_ctx* x, const FusedArgs& a, hipStream_t
 }
 
 // Compulsory HBM bytes of one fused step: SSM state read + write, conv history (3 reads, 1 write), input
-// embedding rows, per-lane coder state and bytes, plus the packed weights once.
+// embedding rows, per-lane coder state and bytes, plus the packed weights once (4 B per parameter as fp32
+// or bf16 hi + lo, 2 B as bf16).
 static double fused_bytes(const boa_ctx* x, int32_t lanes) {
     const double per_lane_layer = 2.0 * x->di * x->NS * 4 + 4.0 * x->di * 4;
     double wbytes = 0.0;
     for (const auto& w : x->layers)
         wbytes += 2.0 * (double)(w.in_w.n + w.x_w.n + w.out_w.n + w.ff1_w.n + w.ff2_w.n);
     wbytes += 2.0 * (double)(x->h1_w.n + x->h2_w.n);
-    if (x->prec == BOA_PREC_BF16X3) wbytes *= 2.0;
+    if (x->prec != BOA_PREC_BF16W) wbytes *= 2.0;
     return (double)lanes * (x->L * per_lane_layer + 4.0 * x->d + 64.0) + wbytes;
 }
 
@@ -3305,25 +3308,25 @@ extern "C" int boa_compress(boa_ctx* x, const uint8_t* d_bytes, int64_t byte_str
     return BOA_OK;
 }
 
-extern "C" int boa_decompress(boa_ctx* x, const uint32_t* d_payload, const int64_t* d_word_off, const int32_t* d_nwords,
-                              const uint8_t* d_first, const int32_t* d_lens, int32_t lanes, int32_t max_len,
-                              uint8_t* d_out, int64_t out_stride) {
-    if (!x || !d_payload || !d_word_off || !d_nwords || !d_first || !d_lens || !d_out || lanes < 1 ||
-        lanes > x->max_lanes || max_len < 1 || out_stride < max_len)
+extern "C" int boa_decompress(boa_ctx* x, const uint32_t* d_payload, int64_t payload_words, const int64_t* d_word_off,
+                              const int32_t* d_nwords, const uint8_t* d_first, const int32_t* d_lens, int32_t lanes,
+                              int32_t max_len, uint8_t* d_out, int64_t out_stride) {
+    if (!x || !d_payload || payload_words < 0 || !d_word_off || !d_nwords || !d_first || !d_lens || !d_out ||
+        lanes < 1 || lanes > x->max_lanes || max_len < 1 || out_stride < max_len)
         return boa_fail(BOA_ERR_ARG, "boa_decompress: bad arguments");
     hipStream_t s = x->stream;
     int rc = boa_state_reset(x, lanes);
     if (rc) return rc;
-    hipLaunchKernelGGL(k_dec_init, dim3((lanes + 255) / 256), dim3(256), 0, s, x->dec, d_payload, d_word_off, d_nwords,
-                       d_first, d_lens, x->tokens, d_out, out_stride, lanes);
+    hipLaunchKernelGGL(k_dec_init, dim3((lanes + 255) / 256), dim3(256), 0, s, x->dec, d_payload, payload_words,
+                       d_word_off, d_nwords, d_first, d_lens, x->tokens, d_out, out_stride, lanes);
     if (x->fused) {
         // the fused kernel runs fused_steps positions per launch, feeding each decoded byte back itself
         for (int t = 1; t < max_len; t += x->fused_steps) {
             FusedArgs a = fused_args(x, lanes, x->tokens);
             a.decode = 1; a.t = t; a.nsteps = std::min(x->fused_steps, max_len - t); a.stagger_us = x->stagger_us;
             a.stagger_classes = x->stagger_classes;
-            a.lens = d_lens; a.dec = x->dec; a.payload = d_payload; a.off = d_word_off;
-            a.nwords = d_nwords; a.tokens_out = x->tokens; a.out = d_out; a.out_stride = out_stride;
+            a.lens = d_lens; a.dec = x->dec; a.payload = d_payload; a.payload_words = payload_words;
+            a.off = d_word_off; a.nwords = d_nwords; a.tokens_out = x->tokens; a.out = d_out; a.out_stride = out_stride;
             hipError_t e = hipSuccess;
             PROF(PC_FUSED, a.nsteps * fused_flops(x, lanes), a.nsteps * fused_bytes(x, lanes),
                  e = launch_fused(x, a, s));
@@ -3373,8 +3376,8 @@ extern "C" int boa_decompress(boa_ctx* x, const uint32_t* d_payload, const int64
                 if (rc) return rc;
                 PROF(PC_DECODE, 0.0, 4.0 * nl * x->V + (double)nl,
                      hipLaunchKernelGGL(k_decode_step, dim3(nl), dim3(64), 0, x->stream, x->logits, x->V, t,
-                                        d_lens + b0, x->dec + b0, d_payload, d_word_off + b0, d_nwords + b0,
-                                        x->tokens + b0, d_out + b0 * out_stride, out_stride));
+                                        d_lens + b0, x->dec + b0, d_payload, payload_words, d_word_off + b0,
+                                        d_nwords + b0, x->tokens + b0, d_out + b0 * out_stride, out_stride));
             }
             x->pos += 1;
         }
@@ -3391,7 +3394,7 @@ extern "C" int boa_decompress(boa_ctx* x, const uint32_t* d_payload, const int64
         if (rc) return rc;
         PROF(PC_DECODE, 0.0, 4.0 * lanes * x->V + (double)lanes,
              hipLaunchKernelGGL(k_decode_step, dim3(lanes), dim3(64), 0, s, x->logits, x->V, t, d_lens, x->dec,
-                                d_payload, d_word_off, d_nwords, x->tokens, d_out, out_stride));
+                                d_payload, payload_words, d_word_off, d_nwords, x->tokens, d_out, out_stride));
     }
     BOA_HIP_TRY(hipGetLastError());
     BOA_HIP_TRY(hipStreamSynchronize(s));

@@ -289,6 +289,23 @@ __device__ __forceinline__ float4 logits_row4(const float* row, int V, int lane)
     return l4;
 }
 
+// Chunk b's stream inside a payload of `total` words: words [off[b], off[b] + nwords[b]) clamped to
+// [0, total).  Offsets or counts that do not fit the payload then read zeros, as the decoder reads zeros
+// past the end of any stream, and no word outside the payload is read (the file reader's bound,
+// boa.cpp:240, enforced on the device for callers that pass arbitrary offsets).
+struct LaneWords {
+    const uint32_t* p;
+    int32_t n;
+};
+__device__ __forceinline__ LaneWords lane_words(const uint32_t* payload, int64_t total, const int64_t* off,
+                                                const int32_t* nwords, int64_t b) {
+    int64_t o = off[b];
+    o = o < 0 ? 0 : (o > total ? total : o);
+    int64_t n = nwords[b];
+    n = n < 0 ? 0 : (n > total - o ? total - o : n);
+    return {payload + o, (int32_t)n};
+}
+
 // One decode step of one lane (whole wavefront): quantise the logits (XQ), find the symbol the coder state
 // points into, advance the state.  Returns the symbol (uniform across the wave).
 __device__ __forceinline__ int decode_row(const float* row, int V, int lane, DecState& st, const uint32_t* in,

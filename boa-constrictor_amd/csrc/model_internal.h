@@ -53,6 +53,7 @@ struct FusedArgs {
     const int32_t* lens;
     DecState* dec;
     const uint32_t* payload;
+    int64_t payload_words;     // the payload's length: every lane's stream is clamped to it
     const int64_t* off;
     const int32_t* nwords;
     int32_t* tokens_out;

@@ -30,7 +30,7 @@ extern "C" {
 
 /* Library identity and last error (replaces the reference's exit(1) on CUDA errors, gemm_gpu.hpp:36-43). */
 const char* boa_last_error(void);
-int boa_abi_version(void);
+int boa_abi_version(void);  /* 2 (boa_decompress takes the payload length since version 2) */
 /* Reports whether d_ptr is device memory of the HIP runtime this library is bound to (1 yes, 0 no). */
 int boa_is_device_pointer(const void* d_ptr);
 
@@ -125,10 +125,13 @@ int boa_compress(boa_ctx* ctx, const uint8_t* d_bytes, int64_t byte_stride, cons
                  int32_t* d_nwords);
 
 /* Fused batched decompress of boa_compress output held contiguously: stream i is
- * d_payload[d_word_off[i] .. + d_nwords[i]).  d_first[i] is chunk i's raw first byte.  Writes
- * d_out[i*out_stride + t] for t < d_lens[i].  Strictly sequential per chunk: one model step per byte.
- * Replaces codec.decompress_GPU (codec.py:89-151) and decompress_v2's GPU loop (boa.cpp:535-574).      */
-int boa_decompress(boa_ctx* ctx, const uint32_t* d_payload, const int64_t* d_word_off,
+ * d_payload[d_word_off[i] .. + d_nwords[i]), clamped to the payload's payload_words words (offsets or
+ * counts past the payload read zeros, as reads past a stream's end do; nothing outside the payload is
+ * read: the bound decompress_v2 checks on the host, boa.cpp:240).  d_first[i] is chunk i's raw first
+ * byte.  Writes d_out[i*out_stride + t] for t < d_lens[i].  Strictly sequential per chunk: one model
+ * step per byte.  Replaces codec.decompress_GPU (codec.py:89-151) and decompress_v2's GPU loop
+ * (boa.cpp:535-574).                                                                                    */
+int boa_decompress(boa_ctx* ctx, const uint32_t* d_payload, int64_t payload_words, const int64_t* d_word_off,
                    const int32_t* d_nwords, const uint8_t* d_first, const int32_t* d_lens, int32_t lanes,
                    int32_t max_len, uint8_t* d_out, int64_t out_stride);
 

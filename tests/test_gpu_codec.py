@@ -210,6 +210,89 @@ def test_decompress_arbitrary_payload(gpu, d_model, precision):
             assert (out[i, :L] == outs[0][i, :L]).all(), i
 
 
+def _decode_raw(m, buf, total, offs, nws, fb, lens):
+    """boa_decompress through the C ABI over a device buffer `buf` of which the first `total` words are the
+    payload."""
+    from boa_amd import _native as nat
+
+    N = len(lens)
+    d_buf = torch.from_numpy(np.ascontiguousarray(buf, dtype=np.uint32).view(np.int32)).cuda()
+    d_off = torch.tensor(offs, dtype=torch.int64).cuda()
+    d_nw = torch.tensor(nws, dtype=torch.int32).cuda()
+    d_first = torch.tensor(fb, dtype=torch.uint8).cuda()
+    d_lens = torch.tensor(lens, dtype=torch.int32).cuda()
+    out = torch.zeros((N, max(lens)), dtype=torch.uint8, device="cuda")
+    eng = m.engine(N, 1)
+    nat.check(nat.lib().boa_decompress(eng.h, nat.ptr(d_buf), int(total), nat.ptr(d_off), nat.ptr(d_nw),
+                                       nat.ptr(d_first), nat.ptr(d_lens), N, max(lens), nat.ptr(out), out.stride(0)))
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("d_model,fused", [(256, "1"), (256, "0"), (512, "1")])
+def test_decompress_payload_bound(gpu, d_model, fused):
+    """boa_decompress clamps every stream to the payload_words it is given (the bound decompress_v2 checks,
+    boa.cpp:240).  The payload sits in a larger buffer whose words past the payload are random: a stream whose
+    offset lies past the payload decodes as an empty stream, one that runs past the end as its clamped
+    prefix, a negative offset as offset 0 and a negative count as 0 -- each equal to decoding the clamped
+    arguments, so no word past the payload was read -- and every consistent lane still round-trips."""
+    import codec
+    from boa_amd import weights as W
+
+    import model as M
+
+    if d_model == 256:
+        m, _ = _model(2)
+        m.precision = "bf16x3"
+    else:
+        m = M.BoaConstrictor(512, 2, 256).load_blob(W.seeded_blob(W.Cfg(d_model=512, n_layers=2), 3))
+        m.precision = "bf16w"
+    lens = [90, 60, 75, 80, 50, 70, 64]
+    chunks = [_markov(L, seed=40 + i) for i, L in enumerate(lens)]
+    payload, nw, fb, Ls = codec.compress_payload(m, chunks)
+    total = int(nw.sum())
+    offs = np.concatenate([[0], np.cumsum(nw)[:-1]]).astype(np.int64)
+    rng = np.random.default_rng(9)
+    buf = np.concatenate([payload, rng.integers(1, 1 << 32, 4096, dtype=np.uint64).astype(np.uint32)])
+    bad_off, bad_nw = offs.copy(), nw.astype(np.int64).copy()
+    clamp_off, clamp_nw = offs.copy(), nw.astype(np.int64).copy()
+    bad_off[1], bad_nw[1] = total + 100, 50          # past the end: empty
+    clamp_off[1], clamp_nw[1] = 0, 0
+    bad_off[3], bad_nw[3] = total - 3, 40            # runs past the end: the last 3 words
+    clamp_off[3], clamp_nw[3] = total - 3, 3
+    bad_off[4], bad_nw[4] = -5, 10                   # negative offset: from word 0
+    clamp_off[4], clamp_nw[4] = 0, 10
+    bad_nw[5] = -7                                   # negative count: empty
+    clamp_nw[5] = 0
+    os.environ["BOA_FUSED_STEP"] = fused
+    try:
+        m.release_engines()
+        good = _decode_raw(m, buf, total, offs, nw, fb, lens)
+        bad = _decode_raw(m, buf, total, bad_off, bad_nw, fb, lens)
+        exp = _decode_raw(m, np.concatenate([payload, np.zeros(4096, np.uint32)]), total, clamp_off, clamp_nw, fb,
+                          lens)
+    finally:
+        del os.environ["BOA_FUSED_STEP"]
+        m.release_engines()
+    for i, c in enumerate(chunks):
+        assert (good[i, :lens[i]] == c).all(), i
+        assert (bad[i, :lens[i]] == exp[i, :lens[i]]).all(), i
+        if i not in (1, 3, 4, 5):
+            assert (bad[i, :lens[i]] == c).all(), i
+    assert not (bad[3, :lens[3]] == chunks[3]).all()   # the clamped stream is not the whole stream
+
+
+def test_boa_decompress_rejects_negative_payload_words(gpu):
+    from boa_amd import _native as nat
+
+    m, _ = _model(1)
+    eng = m.engine(1, 1)
+    z = torch.zeros(16, dtype=torch.int64, device="cuda")
+    rc = nat.lib().boa_decompress(eng.h, nat.ptr(z), -1, nat.ptr(z), nat.ptr(z), nat.ptr(z), nat.ptr(z), 1, 4,
+                                  nat.ptr(z), 4)
+    assert rc != 0 and b"bad arguments" in nat.lib().boa_last_error()
+    m.release_engines()
+
+
 def test_round_trip_d512_bf16w(gpu):
     """configs[4] model shape (d_model 512, bf16 weights), 16 layers, mixed int16 / float32 records."""
     import codec
