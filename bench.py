@@ -8,19 +8,20 @@ Workload (BASELINE.json configs[2] + configs[3]): d_model 256 x 8 Mamba layers, 
 compaction) and decompress it again (strictly sequential, one model step per byte), inputs resident in HBM.
 value = input bytes / (compress time + decompress time), in MB/s (10^6 bytes/s).
 
-GEMM arithmetic is the build's default "bf16x3" mode: fp32 values, each GEMM product formed from two-part
-bfloat16 splits of both operands (three bf16 MFMA products, fp32 accumulation, ~16 significant bits per
-operand); everything else (LayerNorm, conv, scan, activations, quantiser) is fp32/integer.  The line's
-"dtype" says so.
+Arithmetic is the reference's: the default precision "f32" computes every GEMM in fp32 on the matrix cores
+(v_mfma_f32_16x16x4_f32, fp32 operands and accumulation; the reference uses fp32 FMAs,
+gemm_kernels.cu:168-280); LayerNorm, conv, scan, activations and the quantiser are fp32 / integer everywhere.
+Warm-up steps are the same compress + decompress over the first --warmup-len bytes of every chunk (same
+kernels, lanes and buffers; untimed), so that the driver's warm-up count does not multiply the run time.
 
 Also reported: compress and decompress rates separately, the roofline of the dominant kernel from live HIP
 event timing (boa_profile) inside the timed region, and a CPU baseline: this repo's restatement of the
 reference CPU path (codec.compress_CPU / decompress_CPU: per-step torch-CPU model + per-lane range coding in
 a thread pool) timed on a bounded sample of configs[0] on this host.  After the timed steps, untimed by the
 headline, bounded extra measurements go into the same JSON line (--no-extras skips them):
-  f32_full_* configs[2]+[3] at full size in "f32" mode (every GEMM in plain fp32 MFMA, the reference's
-             arithmetic): the same model and data, one timed compress + decompress of the whole payload,
-             with a roofline for each half;
+  bf16x3_full_*  the same model and data at full size in the "bf16x3" mode (fp32 operands split into bf16
+             hi + lo, three bf16 MFMA products per multiply-add, fp32 accumulation: ~16 significant bits per
+             operand, narrower than the reference's fp32), one timed compress + decompress, with rooflines;
   coder      configs[1], the range coder alone: 16384 streams x 4096 symbols, P = 16;
   config4    configs[4]'s model (d512 x 16 layers, bf16 weights, seed 1) on its 16384 chunks of mixed
              int16/float32 records, each chunk cut to a stated length (steady-state rates);
@@ -45,23 +46,36 @@ METRIC = "input MB/s compress + decompress, d256×8L Mamba, 4096 chunks, 1 GPU"
 PEAK_BF16_MFMA_TFLOPS = 2500.0  # dense; a bf16x3 GEMM issues 3 bf16 products per model multiply-add
 PEAK_HBM_GBPS = 8000.0
 PEAK_F32_MFMA_TFLOPS = 157.3  # dense fp32 MFMA (v_mfma_f32_16x16x4_f32)
-TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_fused_step_d256x8L_4096lanes.json")
+# measured HBM traffic of the fused decode kernel, per precision mode
+TRAFFIC_FILES = {p: os.path.join(REPO, "profiles", f"traffic_fused_step_{p}_d256x8L_4096lanes.json")
+                 for p in ("f32", "bf16x3")}
 CODER_TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_rc_coder_configs1.json")
 
-# rocprof names of the kernel instances each profiled class launches at the benchmark's shapes, default
-# precision bf16x3 (k_gemm_bf<BM, BN, BK, EPI, NT, A split, C split>: EPI 0 none, 1 bias, 2 GELU, 4 residual;
-# k_ffn<NT, true>: out_proj + LN2 + FF1 + GELU + FF2 + residual in one kernel; k_head_xq: head + quantiser)
+# rocprof names of the kernel instances each profiled class launches at the benchmark's shapes, per precision
+# (k_gemm_bf<BM, BN, BK, EPI, NT, A split, C split>: EPI 0 none, 1 bias, 2 GELU, 4 residual; k_ffn<NT, true>:
+# out_proj + LN2 + FF1 + GELU + FF2 + residual in one kernel; k_mixin<NT>: LN1 + in_proj + conv + x_proj;
+# k_head_xq: head + quantiser; NT = 1 is the fp32 form, 3 the bf16x3 form)
 KERNEL_NAMES = {
-    ("compress", "gemm_in_proj"): "k_gemm_bf<128, 128, 32, 1, 3, true, false>",
-    ("compress", "ffn"): "k_ffn<3, true>",
-    ("compress", "mixin"): "k_mixin<3>",
-    ("compress", "gemm_out_proj"): "k_gemm_bf<128, 128, 32, 1, 3, true, false>",
-    ("compress", "gemm_x_proj"): "k_xproj<3, 3>",
-    ("compress", "scan"): "k_scan<16, 16, true>",
-    ("compress", "conv"): "k_conv_silu",
-    ("compress", "head_xq"): "k_head_xq<3, 256>",
-    ("compress", "encode"): "k_encode_lf",
-    ("decompress", "fused_step"): "k_fused_step<3, 512>",
+    "f32": {
+        ("compress", "ffn"): "k_ffn<1, true>",
+        ("compress", "mixin"): "k_mixin<1>",
+        ("compress", "scan"): "k_scan<16, 16, false>",
+        ("compress", "head_xq"): "k_head_xq<1, 256>",
+        ("compress", "encode"): "k_encode_lf",
+        ("decompress", "fused_step"): "k_fused_step<1, 512>",
+    },
+    "bf16x3": {
+        ("compress", "gemm_in_proj"): "k_gemm_bf<128, 128, 32, 1, 3, true, false>",
+        ("compress", "ffn"): "k_ffn<3, true>",
+        ("compress", "mixin"): "k_mixin<3>",
+        ("compress", "gemm_out_proj"): "k_gemm_bf<128, 128, 32, 1, 3, true, false>",
+        ("compress", "gemm_x_proj"): "k_xproj<3, 3>",
+        ("compress", "scan"): "k_scan<16, 16, true>",
+        ("compress", "conv"): "k_conv_silu",
+        ("compress", "head_xq"): "k_head_xq<3, 256>",
+        ("compress", "encode"): "k_encode_lf",
+        ("decompress", "fused_step"): "k_fused_step<3, 512>",
+    },
 }
 
 
@@ -73,14 +87,14 @@ def fused_step_bytes(lanes: int, d: int = 256, L: int = 8, di: int = 512, ns: in
     return lanes * (L * (2.0 * di * ns * 4 + 4.0 * di * 4) + 4.0 * d + 64.0) + 4.0 * params
 
 
-def measured_traffic(lanes: int, steps_per_launch: float):
+def measured_traffic(lanes: int, steps_per_launch: float, precision: str):
     """HBM bytes per fused-step launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled by the
     same counters on a copy kernel of known size), from the committed profile summary when it describes this
-    launch shape; otherwise None."""
+    launch shape and precision; otherwise None."""
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(TRAFFIC_FILES[precision]) as f:
             t = json.load(f)
-    except (OSError, ValueError):
+    except (OSError, ValueError, KeyError):
         return None
     if t.get("lanes") != lanes:
         return None
@@ -365,18 +379,37 @@ def read_profile(lib, eng) -> dict:
             for e in ents[:n.value]}
 
 
-def f32_full_extra(lib, X, lens_h, chunk: int, warm_len: int) -> dict:
-    """configs[2]+[3] at full size in the reference's arithmetic: the headline's model and data in "f32" mode
-    (every GEMM in fp32 MFMA, v_mfma_f32_16x16x4_f32; the reference computes them as fp32 FMAs,
-    gemm_kernels.cu:168-280).  One untimed warm-up pass on the first warm_len bytes of every chunk, then one
-    timed compress (+ compaction) and decompress of the whole payload, with each kernel class's HIP events
-    recorded (boa_profile) for the rooflines:
+def fused_roofline(e: dict, B: int, precision: str) -> dict:
+    """Roofline of the fused decode kernel from its boa_profile entry: model GEMM flops per launch against the
+    MFMA peak of the precision's arithmetic (fp32 MFMA for f32; bf16 for bf16x3, counting its three products),
+    and compulsory bytes per launch (SSM state read + write, conv history, embedding rows, coder state, the
+    packed weights once per step) against HBM.  The binding one is the larger fraction."""
+    avg_ms = e["ms"] / e["sampled"]
+    per_launch_bytes = e["bytes"] / e["sampled"]
+    steps = per_launch_bytes / fused_step_bytes(B)
+    fpp = 2.0 * model_macs_per_token(256, 8)
+    if precision == "f32":
+        flops, peak = steps * B * fpp, PEAK_F32_MFMA_TFLOPS
+    else:
+        flops, peak = 3.0 * steps * B * fpp, PEAK_BF16_MFMA_TFLOPS
+    t = avg_ms * 1e-3
+    mfma = {"bound": "mfma", "achieved": flops / t / 1e12, "peak": peak, "unit": "TFLOP/s",
+            "frac": flops / t / 1e12 / peak, "flops_per_launch": flops}
+    hbm = {"bound": "hbm", "achieved": per_launch_bytes / t / 1e9, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+           "frac": per_launch_bytes / t / 1e9 / PEAK_HBM_GBPS, "bytes_per_launch": per_launch_bytes}
+    return {"avg_launch_ms": avg_ms, "launches": e["launches"], "steps_per_launch": round(steps, 3), "mfma": mfma,
+            "hbm": hbm}
+
+
+def full_pass_extra(lib, X, lens_h, chunk: int, warm_len: int, precision: str) -> dict:
+    """configs[2]+[3] at full size in another precision mode: the headline's model and data, one untimed warm-up
+    pass on the first warm_len bytes of every chunk, then one timed compress (+ compaction) and decompress of
+    the whole payload, with each kernel class's HIP events recorded (boa_profile) for the rooflines:
       compress    model GEMM flops (15,466,496 per coded position: every projection, dt_proj included,
-                  15,466,496 = 2 x 7,733,248 multiply-adds) / compress time, against the fp32 MFMA peak;
-      decompress  the fused decode kernel's average launch: its GEMM flops against the fp32 MFMA peak, and its
-                  compulsory bytes (SSM state read + write, conv history, embedding rows, coder state, the
-                  fp32 weights once per step) against HBM."""
-    import numpy as np
+                  = 2 x 7,733,248 multiply-adds; x3 for bf16x3's products) / compress time, against the MFMA
+                  peak of the mode's arithmetic;
+      decompress  the fused decode kernel's average launch (fused_roofline)."""
+    import numpy as np  # noqa: F401
     import torch
 
     from boa_amd import _native as N
@@ -385,7 +418,7 @@ def f32_full_extra(lib, X, lens_h, chunk: int, warm_len: int) -> dict:
 
     B = X.shape[0]
     cfg = W.Cfg()
-    eng = M._Engine(W.seeded_blob(cfg, 0), cfg, B, 64, precision="f32")
+    eng = M._Engine(W.seeded_blob(cfg, 0), cfg, B, 64, precision=precision)
     Xw = X[:, :warm_len].contiguous()
     lw = [min(warm_len, v) for v in lens_h]
     codec_pass(lib, eng, Xw, torch.tensor(lw, dtype=torch.int32, device="cuda"), lw, warm_len, reps=1, warm=0)
@@ -420,42 +453,31 @@ def f32_full_extra(lib, X, lens_h, chunk: int, warm_len: int) -> dict:
     tc, td = t1 - t0, t2 - t1b
     nbytes = sum(lens_h)
     positions = sum(max(v - 1, 0) for v in lens_h)
-    fpp = 2.0 * model_macs_per_token(256, 8)
+    products = 1.0 if precision == "f32" else 3.0
+    peak = PEAK_F32_MFMA_TFLOPS if precision == "f32" else PEAK_BF16_MFMA_TFLOPS
+    fpp = 2.0 * model_macs_per_token(256, 8) * products
+    p = f"{precision}_full_"
     res = {
-        "f32_full_workload": (f"configs[2]+configs[3] in f32 mode (fp32 MFMA GEMMs, the reference's arithmetic): "
-                              f"the headline's model and data, {B} chunks x {chunk} B, one warm-up pass on the "
-                              f"first {warm_len} B of every chunk, then one timed compress + decompress of the "
-                              "whole payload"),
-        "f32_full_compress_MBps": nbytes / tc / 1e6, "f32_full_decompress_MBps": nbytes / td / 1e6,
-        "f32_full_compress_MiBps": nbytes / tc / 2**20, "f32_full_decompress_MiBps": nbytes / td / 2**20,
-        "f32_full_MBps": nbytes / (tc + td) / 1e6,
-        "f32_full_decompress_step_ms": td / (chunk - 1) * 1e3,
-        "f32_full_compressed_bytes": 4 * int(total.value), "f32_full_round_trip_ok": ok,
-        "f32_full_roofline_compress": {"bound": "mfma", "achieved": positions * fpp / tc / 1e12,
-                                       "peak": PEAK_F32_MFMA_TFLOPS, "unit": "TFLOP/s",
-                                       "frac": positions * fpp / tc / 1e12 / PEAK_F32_MFMA_TFLOPS,
-                                       "flops_per_position": fpp, "positions": positions,
-                                       "note": "whole compress pass (all kernels) against the fp32 MFMA peak"},
-        "f32_full_kernel_ms": {f"{ph}/{k}": round(e["ms"] * e["launches"] / e["sampled"], 3)
-                               for ph, pp in (("compress", pc), ("decompress", pd)) for k, e in pp.items()
-                               if e["sampled"]},
+        p + "workload": (f"configs[2]+configs[3] in {precision} mode: the headline's model and data, {B} chunks x "
+                         f"{chunk} B, one warm-up pass on the first {warm_len} B of every chunk, then one timed "
+                         "compress + decompress of the whole payload"),
+        p + "compress_MBps": nbytes / tc / 1e6, p + "decompress_MBps": nbytes / td / 1e6,
+        p + "MBps": nbytes / (tc + td) / 1e6,
+        p + "decompress_step_ms": td / (chunk - 1) * 1e3,
+        p + "compressed_bytes": 4 * int(total.value), p + "round_trip_ok": ok,
+        p + "roofline_compress": {"bound": "mfma", "achieved": positions * fpp / tc / 1e12, "peak": peak,
+                                  "unit": "TFLOP/s", "frac": positions * fpp / tc / 1e12 / peak,
+                                  "flops_per_position": fpp, "positions": positions,
+                                  "note": "whole compress pass (all kernels) against the MFMA peak"},
+        p + "kernel_ms": {f"{ph}/{k}": round(e["ms"] * e["launches"] / e["sampled"], 3)
+                          for ph, pp in (("compress", pc), ("decompress", pd)) for k, e in pp.items()
+                          if e["sampled"]},
     }
     e = pd.get("fused_step")
     if e and e["sampled"]:
-        avg_ms = e["ms"] / e["sampled"]
-        per_launch_bytes = e["bytes"] / e["sampled"]
-        steps = per_launch_bytes / fused_step_bytes(B)
-        per_launch_flops = steps * B * fpp
-        res["f32_full_roofline_decompress"] = {
-            "kernel": "decompress/fused_step", "rocprof_name": "k_fused_step<1, 512>", "avg_launch_ms": avg_ms,
-            "launches": e["launches"], "steps_per_launch": round(steps, 3),
-            "mfma": {"bound": "mfma", "achieved": per_launch_flops / (avg_ms * 1e-3) / 1e12,
-                     "peak": PEAK_F32_MFMA_TFLOPS, "unit": "TFLOP/s",
-                     "frac": per_launch_flops / (avg_ms * 1e-3) / 1e12 / PEAK_F32_MFMA_TFLOPS,
-                     "flops_per_launch": per_launch_flops},
-            "hbm": {"bound": "hbm", "achieved": per_launch_bytes / (avg_ms * 1e-3) / 1e9, "peak": PEAK_HBM_GBPS,
-                    "unit": "GB/s", "frac": per_launch_bytes / (avg_ms * 1e-3) / 1e9 / PEAK_HBM_GBPS,
-                    "bytes_per_launch": per_launch_bytes}}
+        res[p + "roofline_decompress"] = {"kernel": "decompress/fused_step",
+                                          "rocprof_name": KERNEL_NAMES[precision][("decompress", "fused_step")],
+                                          **fused_roofline(e, B, precision)}
     del eng, words, payload, offs, out
     torch.cuda.empty_cache()
     return res
@@ -567,10 +589,14 @@ def main():
     ap.add_argument("--coder-streams", type=int, default=16384)
     ap.add_argument("--coder-len", type=int, default=4096)
     ap.add_argument("--coder-cpu-streams", type=int, default=64)
-    ap.add_argument("--no-extras", action="store_true", help="skip the f32, coder and configs[4] extras")
-    ap.add_argument("--f32-warm-len", type=int, default=256,
-                    help="bytes per chunk of the untimed warm-up before the full-size f32-mode pass")
-    ap.add_argument("--no-f32-full", action="store_true", help="skip the full-size f32-mode pass")
+    ap.add_argument("--precision", choices=["f32", "bf16x3"], default="f32",
+                    help="GEMM arithmetic of the headline: f32 (fp32 MFMA, the reference's arithmetic) or bf16x3")
+    ap.add_argument("--warmup-len", type=int, default=1024,
+                    help="bytes per chunk of each untimed warm-up step (the same kernels over a prefix)")
+    ap.add_argument("--no-extras", action="store_true", help="skip the bf16x3, coder and configs[4] extras")
+    ap.add_argument("--alt-warm-len", type=int, default=256,
+                    help="bytes per chunk of the untimed warm-up before the full-size bf16x3 pass")
+    ap.add_argument("--no-alt-full", action="store_true", help="skip the full-size bf16x3 pass")
     ap.add_argument("--published-shape", action="store_true",
                     help="also run the published-shape extra (d256x1L in f32 mode; off by default, so that the "
                          "f32 kernels' profile averages describe the 8-layer model alone)")
@@ -625,7 +651,8 @@ def main():
     lens = torch.tensor(lens_h, dtype=torch.int32, device=dev)
     first = X[:, 0].contiguous()
     cfg = W.Cfg()
-    eng = M._Engine(W.seeded_blob(cfg, 0), cfg, B, args.tile_len)
+    prec = args.precision
+    eng = M._Engine(W.seeded_blob(cfg, 0), cfg, B, args.tile_len, precision=prec)
     pitch = chunk + 8
     words = torch.empty((B, pitch), dtype=torch.int32, device=dev)
     nw = torch.empty(B, dtype=torch.int32, device=dev)
@@ -635,10 +662,14 @@ def main():
     stream = N.stream_ptr()
     log(f"[bench] context holds {eng.device_bytes / 2**30:.2f} GiB")
 
-    def step():
+    # warm-up step: the same calls over the first wl bytes of every chunk (X keeps its row stride)
+    wl = max(2, min(args.warmup_len, chunk))
+    lens_w = torch.clamp(lens, max=wl)
+
+    def warm_step():
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        N.check(lib.boa_compress(eng.h, N.ptr(X), X.stride(0), N.ptr(lens), B, chunk, N.ptr(words), pitch,
+        N.check(lib.boa_compress(eng.h, N.ptr(X), X.stride(0), N.ptr(lens_w), B, wl, N.ptr(words), pitch,
                                  N.ptr(nw)))
         total = ctypes.c_int64(0)
         N.check(lib.boa_compact(N.ptr(words), pitch, N.ptr(nw), B, N.ptr(offs), N.ptr(payload), payload.numel(),
@@ -646,14 +677,14 @@ def main():
         torch.cuda.synchronize()
         t1 = time.perf_counter()
         N.check(lib.boa_decompress(eng.h, N.ptr(payload), total.value, N.ptr(offs), N.ptr(nw), N.ptr(first),
-                                   N.ptr(lens), B, chunk, N.ptr(out), out.stride(0)))
+                                   N.ptr(lens_w), B, wl, N.ptr(out), out.stride(0)))
         torch.cuda.synchronize()
         t2 = time.perf_counter()
         return t1 - t0, t2 - t1, total.value
 
     for i in range(args.warmup):
-        tc, td, tw = step()
-        log(f"[bench] warmup {i}: compress {tc:.2f}s decompress {td:.2f}s words {tw}")
+        tc, td, tw = warm_step()
+        log(f"[bench] warmup {i} ({wl} B per chunk): compress {tc:.2f}s decompress {td:.2f}s words {tw}")
     tcs, tds = [], []
     prof = {"compress": {}, "decompress": {}}
     for i in range(args.steps):
@@ -713,7 +744,20 @@ def main():
                 best = (tot_ms, phase, name, e)
     total_ms = sum(share.values())
     roofline = None
-    if best is not None:
+    if best is not None and best[2] == "fused_step":
+        _, phase, name, e = best
+        fr = fused_roofline(e, B, prec)
+        # the binding resource: fp32 MFMA for the f32 form (its GEMM phases), HBM for the split forms
+        main = fr["mfma"] if fr["mfma"]["frac"] >= fr["hbm"]["frac"] else fr["hbm"]
+        roofline = {k: main[k] for k in ("bound", "achieved", "peak", "unit", "frac")}
+        roofline["traffic"] = measured_traffic(B, fr["steps_per_launch"], prec)
+        roofline.update({"kernel": f"{phase}/{name}", "rocprof_name": KERNEL_NAMES[prec].get((phase, name), name),
+                         "avg_launch_ms": fr["avg_launch_ms"], "launches": fr["launches"],
+                         "steps_per_launch": fr["steps_per_launch"],
+                         "algorithmic_per_launch": main.get("flops_per_launch", main.get("bytes_per_launch")),
+                         "time_share": best[0] / total_ms if total_ms else None,
+                         "other_bound": fr["hbm"] if main is fr["mfma"] else fr["mfma"]})
+    elif best is not None:
         _, phase, name, e = best
         avg_ms = e["ms"] / e["sampled"]
         if name.startswith("gemm"):
@@ -726,12 +770,9 @@ def main():
             roofline = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                         "frac": achieved / PEAK_HBM_GBPS, "traffic": None}
             per_launch = e["bytes"] / e["sampled"]
-        roofline.update({"kernel": f"{phase}/{name}", "rocprof_name": KERNEL_NAMES.get((phase, name), name),
+        roofline.update({"kernel": f"{phase}/{name}", "rocprof_name": KERNEL_NAMES[prec].get((phase, name), name),
                          "avg_launch_ms": avg_ms, "algorithmic_per_launch": per_launch,
                          "launches": e["launches"], "time_share": best[0] / total_ms if total_ms else None})
-        if name == "fused_step":
-            roofline["steps_per_launch"] = round(per_launch / fused_step_bytes(B), 3)
-            roofline["traffic"] = measured_traffic(B, roofline["steps_per_launch"])
 
     cpu = None
     if not args.no_cpu:
@@ -743,13 +784,14 @@ def main():
     if not args.no_extras:
         del words, payload, offs, eng
         torch.cuda.empty_cache()
-        if not args.no_f32_full:
-            log(f"[bench] extra: f32 mode, full size ({B} chunks x {chunk} B)")
-            extras.update(f32_full_extra(lib, X, lens_h, chunk, args.f32_warm_len))
-            log(f"[bench] extra: f32 compress {extras['f32_full_compress_MBps']:.3f} MB/s, decompress "
-                f"{extras['f32_full_decompress_MBps']:.3f} MB/s "
-                f"({extras['f32_full_decompress_step_ms']:.3f} ms per step), round trip "
-                f"{extras['f32_full_round_trip_ok']}")
+        alt = "bf16x3" if prec == "f32" else "f32"
+        if not args.no_alt_full:
+            log(f"[bench] extra: {alt} mode, full size ({B} chunks x {chunk} B)")
+            extras.update(full_pass_extra(lib, X, lens_h, chunk, args.alt_warm_len, alt))
+            log(f"[bench] extra: {alt} compress {extras[alt + '_full_compress_MBps']:.3f} MB/s, decompress "
+                f"{extras[alt + '_full_decompress_MBps']:.3f} MB/s "
+                f"({extras[alt + '_full_decompress_step_ms']:.3f} ms per step), round trip "
+                f"{extras[alt + '_full_round_trip_ok']}")
         if args.published_shape:
             log(f"[bench] extra: the published shape (d256x1L, first {args.pub_len} B of each chunk)")
             extras["published_shape"] = published_shape_extra(lib, X, lens_h, args.pub_len)
@@ -767,6 +809,9 @@ def main():
             f"{extras['config4']['decompress_MBps']:.3f} MB/s, round trip {extras['config4']['round_trip_ok']}")
 
     value = nbytes / (tc + td) / 1e6
+    positions = sum(max(v - 1, 0) for v in lens_h)
+    c_fpp = 2.0 * model_macs_per_token(256, 8) * (1.0 if prec == "f32" else 3.0)
+    c_peak = PEAK_F32_MFMA_TFLOPS if prec == "f32" else PEAK_BF16_MFMA_TFLOPS
     res = {
         "metric": METRIC,
         "value": value if ok else None,
@@ -778,18 +823,22 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16x3",
+        "dtype": "f32" if prec == "f32" else "bf16x3",
         "data": "synthetic",
         "config": {
             "workload": ("configs[2]+configs[3]: compress then decompress 64 MiB float32 records (seed 0), "
                          f"{B} chunks x {chunk} B, d256x8L Mamba random init seed 0 (fp32 weights), GEMMs in "
-                         "bf16x3 (fp32 operands split into bf16 hi+lo, three bf16 MFMA products, fp32 "
-                         "accumulation), inputs in HBM"),
+                         + ("fp32 on the matrix cores (v_mfma_f32_16x16x4_f32, fp32 operands and accumulation)"
+                            if prec == "f32" else
+                            "bf16x3 (fp32 operands split into bf16 hi+lo, three bf16 MFMA products, fp32 "
+                            "accumulation)")
+                         + f", inputs in HBM; warm-up steps over the first {wl} B of every chunk"),
             "chunks": B,
             "chunk_len": chunk,
             "payload_bytes": nbytes,
             "tile_len": args.tile_len,
-            "precision": "bf16x3",
+            "precision": prec,
+            "warmup_len": wl,
         },
         "compress_MBps": nbytes / tc / 1e6,
         "decompress_MBps": nbytes / td / 1e6,
@@ -803,6 +852,10 @@ def main():
                     "output_d2h": t_d2h_out * 1e3},
         "round_trip_ok": ok,
         "roofline": roofline,
+        "roofline_compress": {"bound": "mfma", "achieved": positions * c_fpp / tc / 1e12, "peak": c_peak,
+                              "unit": "TFLOP/s", "frac": positions * c_fpp / tc / 1e12 / c_peak,
+                              "flops_per_position": c_fpp, "positions": positions,
+                              "note": "whole compress pass (all kernels) against the MFMA peak of the mode"},
         "kernel_ms": {k: round(v, 3) for k, v in sorted(share.items(), key=lambda kv: -kv[1])},
         "cpu_baseline": cpu,
     }
