@@ -76,69 +76,89 @@ __device__ __forceinline__ int frag_of(int f0, int wave, int j, int nfrag, int r
 // groups in ascending order, the j-th MFMA of group g taking k = 16 g + 4 (l / 16) + j from lane l, which is
 // k_gemm's order.  RD groups are in flight through a register ring; the loop runs over passes of RD groups so
 // that every ring slot is fixed per unrolled position, and the last prefetches are clamped to the last group
-// (reloads, unused) instead of sitting under a branch.
-template <int NWAVE, int FPW, int K>
+// (reloads, unused) instead of sitting under a branch.  Each group's weight loads and the next group's A
+// fragment are issued together and pinned there (left to itself the scheduler sinks the loads to their uses).
+// Within a group the MFMAs go round the fragments (x of every fragment, then y, ...); each fragment's own
+// sequence is unchanged.
+// CHECK: whether some of this wave's fragments may lie past nfrag.  When the caller's shape rules that out
+// (nfrag a multiple of FPW * NWAVE, f0 a multiple of it too) there is no per-fragment condition at all: a load or
+// MFMA under a branch costs an exec-mask round trip, and an accumulator merged after a branch costs a wait for
+// the MFMA result and register copies, in every group (fp32 step 0.90 -> 0.86 ms with the other changes here).
+template <int NWAVE, int FPW, int K, int RD, bool CHECK>
 __device__ __forceinline__ void mgemm_f32(const float* A, int lda, const float* __restrict__ Wp, int f0, int nfrag,
                                           int wave, int lane, int rot, floatx4 (&acc)[FPW]) {
-    constexpr int S = K / 16, RD = 4;
+    constexpr int S = K / 16;
     static_assert(S % RD == 0, "whole passes of the register ring");
     const int kq = 4 * (lane >> 4), ar = lane & 15;
     const int fw = f0 + wave;
+    auto valid = [&](int j) { return !CHECK || fw + NWAVE * j < nfrag; };
 #pragma unroll
     for (int j = 0; j < FPW; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
     float4 bw[RD][FPW];
     auto load = [&](int g, int slot) {
 #pragma unroll
         for (int j = 0; j < FPW; ++j) {
-            if (fw + NWAVE * j < nfrag) {
+            if (valid(j)) {
                 const int f = frag_of<NWAVE>(f0, wave, j, nfrag, rot);
                 bw[slot][j] = ldg_f4(G(Wp) + ((int64_t)f * S + g) * 256 + lane * 4);
             }
         }
     };
+    const float* Ar = A + ar * lda + kq;
 #pragma unroll
     for (int i = 0; i < RD - 1; ++i) load(i, i);
+    float4 a = *reinterpret_cast<const float4*>(Ar);
 #pragma unroll 1
     for (int g0 = 0; g0 < S; g0 += RD) {
 #pragma unroll
         for (int i = 0; i < RD; ++i) {
             const int gn = g0 + i + RD - 1;
             load(gn < S ? gn : S - 1, (i + RD - 1) % RD);
-            const float4 a = *reinterpret_cast<const float4*>(A + ar * lda + 16 * (g0 + i) + kq);
+            // the next group's A fragment (the last group re-reads its own), read one group ahead
+            const int ga = g0 + i + 1 < S ? g0 + i + 1 : S - 1;
+            const float4 an = *reinterpret_cast<const float4*>(Ar + 16 * ga);
+            pin_loads();  // issued here, ahead of their use (the scheduler would sink them to it)
+            const float av[4] = {a.x, a.y, a.z, a.w};
+            a = an;
 #pragma unroll
-            for (int j = 0; j < FPW; ++j) {
-                if (fw + NWAVE * j < nfrag) {
-                    const float4 b = bw[i][j];
-                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, acc[j], 0, 0, 0);
-                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, acc[j], 0, 0, 0);
-                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, acc[j], 0, 0, 0);
-                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, acc[j], 0, 0, 0);
+            for (int e = 0; e < 4; ++e) {
+#pragma unroll
+                for (int j = 0; j < FPW; ++j) {
+                    if (valid(j)) {
+                        const float4 b = bw[i][j];
+                        const float bv[4] = {b.x, b.y, b.z, b.w};
+                        acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[e], bv[e], acc[j], 0, 0, 0);
+                    }
                 }
             }
         }
     }
 }
 
-template <int NT, int NWAVE, int FPW, int K, int D>
+// D: K steps in flight in the split forms (the fp32 form keeps 4 groups of 16 K in flight).
+template <int NT, int NWAVE, int FPW, int K, int D, bool CHECK = true>
 __device__ __forceinline__ void mgemm(const uint16_t* sAh, const uint16_t* sAl, int lda,
                                       const uint16_t* __restrict__ Wp, int f0, int nfrag, int wave, int lane,
                                       int rot, floatx4 (&acc)[FPW]) {
     if constexpr (NT == 1) {
-        mgemm_f32<NWAVE, FPW, K>(reinterpret_cast<const float*>(sAh), ld32(lda), reinterpret_cast<const float*>(Wp),
-                                 f0, nfrag, wave, lane, rot, acc);
+        mgemm_f32<NWAVE, FPW, K, 4, CHECK>(reinterpret_cast<const float*>(sAh), ld32(lda),
+                                           reinterpret_cast<const float*>(Wp), f0, nfrag, wave, lane, rot, acc);
         return;
     }
     constexpr int BLK = (NT == 3) ? 1024 : 512;
     constexpr int S = K / 32;
     const int kq = 8 * (lane >> 4), ar = lane & 15;
     const int fw = f0 + wave;
+    // The split forms keep the per-fragment condition whatever CHECK says: without it the compiler hoists the
+    // fully unrolled loop's loads together and the ring no longer spaces them (FF1 measured 40% slower).
+    auto valid = [&](int j) { return fw + NWAVE * j < nfrag; };
 #pragma unroll
     for (int j = 0; j < FPW; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
     uint4 bh[D][FPW], bl[D][FPW];
     auto load = [&](int s, int slot) {
 #pragma unroll
         for (int j = 0; j < FPW; ++j) {
-            if (fw + NWAVE * j < nfrag) {
+            if (valid(j)) {
                 const int f = frag_of<NWAVE>(f0, wave, j, nfrag, rot);
                 const gptr<uint16_t> p = G(Wp) + ((int64_t)f * S + s) * BLK + lane * 8;
                 bh[slot][j] = __builtin_bit_cast(uint4, ldg16(p));
@@ -156,7 +176,7 @@ __device__ __forceinline__ void mgemm(const uint16_t* sAh, const uint16_t* sAl, 
         const bf16x8 al = *reinterpret_cast<const bf16x8*>(sAl + ar * lda + 32 * s + kq);
 #pragma unroll
         for (int j = 0; j < FPW; ++j) {
-            if (fw + NWAVE * j < nfrag) {
+            if (valid(j)) {
                 const bf16x8 h = __builtin_bit_cast(bf16x8, bh[s % D][j]);
                 acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, h, acc[j], 0, 0, 0);
                 if constexpr (NT == 3)
@@ -222,7 +242,12 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
     constexpr int D_B = 3;         // K steps in flight, N = 1024 GEMMs
     constexpr int FPW_S = 16 / NWAVE;               // fragments per wave, N = 256 GEMMs
     constexpr int D_S = 6;         // K steps in flight, N = 256 GEMMs
+    // lane 0's SSM state is loaded before x_proj in the fp32 form, whose x_proj phase is long enough to hide it
+    constexpr bool HOIST_FIRST = NT == 1;
     static_assert(NTHR == 512 && NTHR == FDI && NWAVE * XPROJ_KB == FDI, "fused step block size: one thread per channel");
+    // every GEMM below but x_proj and head2 covers its fragments exactly (mgemm's CHECK = false)
+    static_assert((2 * FDI / 16) % (FPW_B * NWAVE) == 0 && (4 * FD / 16) % (FPW_B * NWAVE) == 0 &&
+                  (FD / 16) % (FPW_S * NWAVE) == 0, "whole passes of fragments");
     __shared__ __attribute__((aligned(16))) unsigned char lds[LDS_BYTES];
     float* sRes = reinterpret_cast<float*>(lds + OFF_RES);
     uint16_t* sAh = reinterpret_cast<uint16_t*>(lds + OFF_A);
@@ -304,7 +329,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
             float bias_j[FPW_B];  // loaded ahead of the weight ring (in-order wait counter)
 #pragma unroll
             for (int j = 0; j < FPW_B; ++j) bias_j[j] = G(w.in_b)[16 * frag_of<NWAVE>(f0, wave, j, 2 * FDI / 16, rot64) + n_of];
-            mgemm<NT, NWAVE, FPW_B, FD, D_B>(sAh, sAl, LA, w.in_p, f0, 2 * FDI / 16, wave, lane, rot64, acc);
+            mgemm<NT, NWAVE, FPW_B, FD, D_B, false>(sAh, sAl, LA, w.in_p, f0, 2 * FDI / 16, wave, lane, rot64, acc);
 #pragma unroll
             for (int j = 0; j < FPW_B; ++j) {
                 const int n = 16 * frag_of<NWAVE>(f0, wave, j, 2 * FDI / 16, rot64) + n_of;
@@ -390,12 +415,43 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
             }
         }
         __syncthreads();
+        // ---- the scan's operands that do not depend on x_proj, issued ahead of it (their memory latency then
+        //      overlaps x_proj): the channel's A row, dt_proj row, biases and lane 0's state (thread = channel)
+        const int c = tid;
+        float av[FNS], wr[FR];
+        {
+            const gptr<float> Ag = G(w.Aneg);
+#pragma unroll
+            for (int n = 0; n < FNS; n += 4) {
+                const float4 p = ldg_f4(Ag + ((int64_t)(n / 4) * FDI + c) * 4);
+                av[n] = p.x; av[n + 1] = p.y; av[n + 2] = p.z; av[n + 3] = p.w;
+            }
+#pragma unroll
+            for (int r = 0; r < FR; r += 4) {
+                const float4 q = ldg_f4(G(w.dt_w) + (int64_t)c * FR + r);
+                wr[r] = q.x; wr[r + 1] = q.y; wr[r + 2] = q.z; wr[r + 3] = q.w;
+            }
+        }
+        const float bdt = G(w.dt_b)[c], Dc = G(w.D)[c];
+        // SSM state of this workgroup's valid lanes [b0, b0 + nb): rows past the last lane read 0 and are not
+        // written (buffer range check).  No load or store is under a branch: the compiler's wait counts treat
+        // a memory operation under a branch as possibly not issued, and every row would then wait for all
+        // loads in flight.
+        const __amdgpu_buffer_rsrc_t sr =
+            buf_rsrc(a.ssm + ((int64_t)l * a.max_lanes + b0) * FDI * FNS, (uint32_t)nb * FDI * FNS * 4);
+        auto h_off = [&](int r, int n, int cq) { return (uint32_t)((r * FNS / 4 + n / 4) * FDI + cq) * 16; };
+        f32x4 h_first[FNS / 4];
+        auto load_first = [&]() {
+#pragma unroll
+            for (int n = 0; n < FNS; n += 4) h_first[n / 4] = buf_ld4(sr, h_off(0, n, c));
+        };
+        if constexpr (HOIST_FIRST) load_first();
         if constexpr (NT == 1) {
             // ---- x_proj over all 512 channels at once (fp32 mode: one ascending accumulation per output):
-            //      waves 0..2 own output fragments 0..2
-            floatx4 acc[1];
-            mgemm<NT, NWAVE, 1, FDI, 4>(sAh, sAl, LA, w.x_p, 0, FW / 16, wave, lane, 0, acc);
+            //      waves 0..2 own output fragments 0..2 (a wave-uniform condition around the whole GEMM)
             if (wave < FW / 16) {
+                floatx4 acc[1];
+                mgemm<NT, NWAVE, 1, FDI, 4, false>(sAh, sAl, LA, w.x_p, 0, FW / 16, wave, lane, 0, acc);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) sDbc[(m_of + r) * FW + 16 * wave + n_of] = acc[0][r];
             }
@@ -412,29 +468,9 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
         __syncthreads();
         // ---- dt_proj + softplus + selective scan + D + gate (thread = channel) -> y split operand
         {
-            const int c = tid;
-            float av[FNS], wr[FR];
-            const gptr<float> Ag = G(w.Aneg);
-#pragma unroll
-            for (int n = 0; n < FNS; n += 4) {
-                const float4 p = ldg_f4(Ag + ((int64_t)(n / 4) * FDI + c) * 4);
-                av[n] = p.x; av[n + 1] = p.y; av[n + 2] = p.z; av[n + 3] = p.w;
-            }
-#pragma unroll
-            for (int r = 0; r < FR; r += 4) {
-                const float4 q = ldg_f4(G(w.dt_w) + (int64_t)c * FR + r);
-                wr[r] = q.x; wr[r + 1] = q.y; wr[r + 2] = q.z; wr[r + 3] = q.w;
-            }
-            const float bdt = G(w.dt_b)[c], Dc = G(w.D)[c];
-            // SSM state of this workgroup's valid lanes [b0, b0 + nb): rows past the last lane read 0 and are not
-            // written (buffer range check).  No load or store is under a branch: the compiler's wait counts treat
-            // a memory operation under a branch as possibly not issued, and every row would then wait for all
-            // loads in flight.
-            const __amdgpu_buffer_rsrc_t sr =
-                buf_rsrc(a.ssm + ((int64_t)l * a.max_lanes + b0) * FDI * FNS, (uint32_t)nb * FDI * FNS * 4);
-            auto h_off = [&](int r, int n, int cq) { return (uint32_t)((r * FNS / 4 + n / 4) * FDI + cq) * 16; };
-            // One lane's state at a time, loaded at the top of its row (the barrier keeps the loads ahead of the
-            // row's LDS reads) and stored at its end.  The two waves of a SIMD take turns waiting on memory;
+            if constexpr (!HOIST_FIRST) load_first();
+            // One lane's state at a time, loaded at the top of its row (lane 0's before x_proj; the barrier keeps
+            // the loads ahead of the row's LDS reads) and stored at its end.  The two waves of a SIMD take turns waiting on memory;
             // loading the next lane's state one row ahead (before this row's stores) measured the same, keeping
             // 1-3 more lanes in flight per thread 2-7% slower (more registers in a kernel at its register limit).
 #pragma unroll
@@ -444,7 +480,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
                 float h[FNS];
 #pragma unroll
                 for (int n = 0; n < FNS; n += 4) {
-                    const f32x4 q = buf_ld4(sr, h_off(r, n, cq));
+                    const f32x4 q = r == 0 ? h_first[n / 4] : buf_ld4(sr, h_off(r, n, cq));
                     h[n] = q.x; h[n + 1] = q.y; h[n + 2] = q.z; h[n + 3] = q.w;
                 }
                 __builtin_amdgcn_sched_barrier(0);
@@ -463,7 +499,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
             float bias_j[FPW_S];
 #pragma unroll
             for (int j = 0; j < FPW_S; ++j) bias_j[j] = G(w.out_b)[16 * frag_of<NWAVE>(0, wave, j, FD / 16, rot16) + n_of];
-            mgemm<NT, NWAVE, FPW_S, FDI, D_S>(sAh, sAl, LA, w.out_p, 0, FD / 16, wave, lane, rot16, acc);
+            mgemm<NT, NWAVE, FPW_S, FDI, D_S, false>(sAh, sAl, LA, w.out_p, 0, FD / 16, wave, lane, rot16, acc);
 #pragma unroll
             for (int j = 0; j < FPW_S; ++j) {
                 const int n = 16 * frag_of<NWAVE>(0, wave, j, FD / 16, rot16) + n_of;
@@ -485,7 +521,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
             float bias_j[FPW_B];
 #pragma unroll
             for (int j = 0; j < FPW_B; ++j) bias_j[j] = G(w.ff1_b)[16 * frag_of<NWAVE>(f0, wave, j, 4 * FD / 16, rot64) + n_of];
-            mgemm<NT, NWAVE, FPW_B, FD, D_B>(sAh, sAl, LA, w.ff1_p, f0, 4 * FD / 16, wave, lane, rot64, acc);
+            mgemm<NT, NWAVE, FPW_B, FD, D_B, false>(sAh, sAl, LA, w.ff1_p, f0, 4 * FD / 16, wave, lane, rot64, acc);
 #pragma unroll
             for (int j = 0; j < FPW_B; ++j) {
                 const int n = 16 * frag_of<NWAVE>(f0, wave, j, 4 * FD / 16, rot64) + n_of;
@@ -501,7 +537,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
             float bias_j[FPW_S];
 #pragma unroll
             for (int j = 0; j < FPW_S; ++j) bias_j[j] = G(w.ff2_b)[16 * frag_of<NWAVE>(0, wave, j, FD / 16, rot16) + n_of];
-            mgemm<NT, NWAVE, FPW_S, 4 * FD, D_S>(sHh, sHl, LH, w.ff2_p, 0, FD / 16, wave, lane, rot16, acc);
+            mgemm<NT, NWAVE, FPW_S, 4 * FD, D_S, false>(sHh, sHl, LH, w.ff2_p, 0, FD / 16, wave, lane, rot16, acc);
 #pragma unroll
             for (int j = 0; j < FPW_S; ++j) {
                 const int n = 16 * frag_of<NWAVE>(0, wave, j, FD / 16, rot16) + n_of;
@@ -531,7 +567,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
     uint16_t* sGl = sHh + ROWS * LH1;
     {
         floatx4 acc[FPW_S];
-        mgemm<NT, NWAVE, FPW_S, FD, D_S>(sAh, sAl, LA, a.h1_p, 0, FD / 16, wave, lane, rot16, acc);
+        mgemm<NT, NWAVE, FPW_S, FD, D_S, false>(sAh, sAl, LA, a.h1_p, 0, FD / 16, wave, lane, rot16, acc);
 #pragma unroll
         for (int j = 0; j < FPW_S; ++j) {
             const int n = 16 * frag_of<NWAVE>(0, wave, j, FD / 16, rot16) + n_of;
@@ -543,7 +579,11 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
     __syncthreads();
     {
         floatx4 acc[FPW_S];
-        mgemm<NT, NWAVE, FPW_S, FD, D_S>(sGh, sGl, LH1, a.h2_p, 0, V / 16, wave, lane, 0, acc);
+        // a full 256-symbol vocabulary covers every fragment (no per-fragment condition); smaller ones check
+        if (V == FPW_S * NWAVE * 16)
+            mgemm<NT, NWAVE, FPW_S, FD, D_S, false>(sGh, sGl, LH1, a.h2_p, 0, V / 16, wave, lane, 0, acc);
+        else
+            mgemm<NT, NWAVE, FPW_S, FD, D_S>(sGh, sGl, LH1, a.h2_p, 0, V / 16, wave, lane, 0, acc);
 #pragma unroll
         for (int j = 0; j < FPW_S; ++j) {
             const int f = wave + NWAVE * j;
