@@ -135,13 +135,13 @@ __device__ __forceinline__ void mgemm_f32(const float* A, int lda, const float* 
     }
 }
 
-// D: K steps in flight in the split forms (the fp32 form keeps 4 groups of 16 K in flight).
-template <int NT, int NWAVE, int FPW, int K, int D, bool CHECK = true>
+// D: K steps in flight in the split forms; RDF: 16-K groups in flight in the fp32 form.
+template <int NT, int NWAVE, int FPW, int K, int D, bool CHECK = true, int RDF = 4>
 __device__ __forceinline__ void mgemm(const uint16_t* sAh, const uint16_t* sAl, int lda,
                                       const uint16_t* __restrict__ Wp, int f0, int nfrag, int wave, int lane,
                                       int rot, floatx4 (&acc)[FPW]) {
     if constexpr (NT == 1) {
-        mgemm_f32<NWAVE, FPW, K, 4, CHECK>(reinterpret_cast<const float*>(sAh), ld32(lda),
+        mgemm_f32<NWAVE, FPW, K, RDF, CHECK>(reinterpret_cast<const float*>(sAh), ld32(lda),
                                            reinterpret_cast<const float*>(Wp), f0, nfrag, wave, lane, rot, acc);
         return;
     }
@@ -238,7 +238,9 @@ template <int NT, int NTHR>
 __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
     constexpr int NWAVE = NTHR / 64;
     constexpr int RPW = ROWS / NWAVE;               // rows per wave (LN, decode)
-    constexpr int FPW_B = 4;                        // fragments per wave, N = 1024 GEMMs (per pass)
+    // fragments per wave and pass, N = 1024 GEMMs: 4 in the split forms; 2 in the fp32 form, whose in_proj and FF1
+    // keep 16 groups of 16 K in flight instead (the weight stream from L2 bounds them: 0.868 -> 0.840 ms per step)
+    constexpr int FPW_B = NT == 1 ? 2 : 4;
     constexpr int D_B = 3;         // K steps in flight, N = 1024 GEMMs
     constexpr int FPW_S = 16 / NWAVE;               // fragments per wave, N = 256 GEMMs
     constexpr int D_S = 6;         // K steps in flight, N = 256 GEMMs
@@ -262,7 +264,8 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
     __shared__ int sTok[ROWS];
     __shared__ int sMaxLen;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: a scalar register, not 64 vector lanes
     const int64_t b0 = (int64_t)blockIdx.x * ROWS;
     const int nb = (int)((a.B - b0) < ROWS ? (a.B - b0) : ROWS);  // valid lanes of this workgroup
     const int V = a.V;
@@ -318,6 +321,13 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
     const int s1 = p0m3 == 2 ? 0 : p0m3 + 1, s2 = p0m3 == 0 ? 2 : p0m3 - 1;
 
     for (int l = 0; l < a.L; ++l) {
+        // Lane-derived values re-derived per layer from an opaque copy of the thread index, so that the compiler
+        // does not form every phase's per-lane addresses once outside the layer loop and hold them (dozens of
+        // registers) across all phases, which leaves the GEMM phases too few registers for their weight rings.
+        int tid_o = (int)threadIdx.x;
+        __asm__ volatile("" : "+v"(tid_o));
+        const int tid = tid_o, lane = tid_o & 63;
+        const int m_of = 4 * (lane >> 4), n_of = lane & 15;
         CFusedLayer& w = layer_at(a.layers, l);
         // ---- LN1 -> split operand
         ln_rows<NT, RPW>(sRes, lnw, lnb, sAh, sAl, wave, lane);
@@ -329,7 +339,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
             float bias_j[FPW_B];  // loaded ahead of the weight ring (in-order wait counter)
 #pragma unroll
             for (int j = 0; j < FPW_B; ++j) bias_j[j] = G(w.in_b)[16 * frag_of<NWAVE>(f0, wave, j, 2 * FDI / 16, rot64) + n_of];
-            mgemm<NT, NWAVE, FPW_B, FD, D_B, false>(sAh, sAl, LA, w.in_p, f0, 2 * FDI / 16, wave, lane, rot64, acc);
+            mgemm<NT, NWAVE, FPW_B, FD, D_B, false, 16>(sAh, sAl, LA, w.in_p, f0, 2 * FDI / 16, wave, lane, rot64, acc);
 #pragma unroll
             for (int j = 0; j < FPW_B; ++j) {
                 const int n = 16 * frag_of<NWAVE>(f0, wave, j, 2 * FDI / 16, rot64) + n_of;
@@ -521,7 +531,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
             float bias_j[FPW_B];
 #pragma unroll
             for (int j = 0; j < FPW_B; ++j) bias_j[j] = G(w.ff1_b)[16 * frag_of<NWAVE>(f0, wave, j, 4 * FD / 16, rot64) + n_of];
-            mgemm<NT, NWAVE, FPW_B, FD, D_B, false>(sAh, sAl, LA, w.ff1_p, f0, 4 * FD / 16, wave, lane, rot64, acc);
+            mgemm<NT, NWAVE, FPW_B, FD, D_B, false, 16>(sAh, sAl, LA, w.ff1_p, f0, 4 * FD / 16, wave, lane, rot64, acc);
 #pragma unroll
             for (int j = 0; j < FPW_B; ++j) {
                 const int n = 16 * frag_of<NWAVE>(f0, wave, j, 4 * FD / 16, rot64) + n_of;
@@ -557,7 +567,11 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
         __syncthreads();
     }
 
-    // ---- head: Linear -> ReLU -> Linear (model.py:95, 101)
+    // ---- head: Linear -> ReLU -> Linear (model.py:95, 101); lane values from an opaque copy, as in the layer loop
+    int tid_h = (int)threadIdx.x;
+    __asm__ volatile("" : "+v"(tid_h));
+    const int tid = tid_h, lane = tid_h & 63;
+    const int m_of = 4 * (lane >> 4), n_of = lane & 15;
     for (int i = tid; i < ROWS * FD; i += NTHR) {
         const int r = i / FD, c = i % FD;
         store_op<NT, LA>(sAh, r, c, sRes[r * LRES + c]);
