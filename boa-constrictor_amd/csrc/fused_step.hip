@@ -284,8 +284,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
         }
     }
     __syncthreads();
-    const int m_of = 4 * (lane >> 4);  // first output row of this lane in a fragment
-    const int n_of = lane & 15;        // output column within a fragment
+    // (a lane's first output row in a fragment, m_of, and its column, n_of, are formed per layer and for the head)
 
     int p0m3 = a.p0m3;
 #pragma unroll 1
