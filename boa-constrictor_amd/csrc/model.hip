@@ -3101,7 +3101,7 @@ static FusedArgs fused_args(boa_ctx* x, int32_t lanes, const int32_t* tokens_in)
     a.max_lanes = x->max_lanes;
     a.emb = x->emb; a.h1_b = x->h1_b; a.h2_b = x->h2_b; a.h1_p = x->h1_w.p; a.h2_p = x->h2_w.p;
     a.ssm = x->ssm; a.hist = x->conv_hist; a.tokens_in = tokens_in;
-    a.resid = x->x; a.scr = x->xz;  // per-lane scratch rows of the d_model 512 kernel (row = lane)
+    a.scr = x->xz;  // per-lane scratch rows of the d_model 512 kernel (row = lane)
     a.nsteps = 1;
     return a;
 }

@@ -59,9 +59,8 @@ struct FusedArgs {
     int32_t* tokens_out;
     uint8_t* out;
     int64_t out_stride;
-    // d_model 512 kernel only: per-lane scratch in device memory (the context's workspace rows, row = lane):
-    // the residual stream [lanes][d_model] and the mixer's z | conv output [lanes][2 d_inner]
-    float* resid;
+    // d_model 512 kernel only: per-lane scratch in device memory (the context's workspace rows, row = lane): the
+    // mixer's z | conv output [lanes][2 d_inner]
     float* scr;
 };
 
@@ -72,7 +71,7 @@ bool fused_step_supported(int d_model, int d_state, int dt_rank, int d_conv, int
 hipError_t launch_fused_step(const FusedArgs& a, int nt, hipStream_t s);
 
 // The d_model 512 form (d_inner 1024, d_state 16, dt_rank 32, d_conv 4, vocab 256): 512 threads (8 waves) per
-// workgroup of 32 lanes, one workgroup per CU (256 VGPRs per thread, 80 KB of LDS).
+// workgroup of 32 lanes, one workgroup per CU (256 VGPRs per thread, 145 KB of LDS with the residual stream).
 bool fused_step512_supported(int d_model, int d_state, int dt_rank, int d_conv, int vocab);
 hipError_t launch_fused_step512(const FusedArgs& a, int nt, hipStream_t s);
 
