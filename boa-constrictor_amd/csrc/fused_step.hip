@@ -265,7 +265,9 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
     __shared__ int sMaxLen;
 
     const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: a scalar register, not 64 vector lanes
+    // uniform: a scalar register in the fp32 form (the split forms measured slower with it, 0.59 -> 0.67 ms per
+    // step together with the per-layer lane copies below, and keep the plain form)
+    const int wave = NT == 1 ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6;
     const int64_t b0 = (int64_t)blockIdx.x * ROWS;
     const int nb = (int)((a.B - b0) < ROWS ? (a.B - b0) : ROWS);  // valid lanes of this workgroup
     const int V = a.V;
@@ -324,7 +326,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
         // does not form every phase's per-lane addresses once outside the layer loop and hold them (dozens of
         // registers) across all phases, which leaves the GEMM phases too few registers for their weight rings.
         int tid_o = (int)threadIdx.x;
-        __asm__ volatile("" : "+v"(tid_o));
+        if constexpr (NT == 1) __asm__ volatile("" : "+v"(tid_o));
         const int tid = tid_o, lane = tid_o & 63;
         const int m_of = 4 * (lane >> 4), n_of = lane & 15;
         CFusedLayer& w = layer_at(a.layers, l);
@@ -568,7 +570,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
 
     // ---- head: Linear -> ReLU -> Linear (model.py:95, 101); lane values from an opaque copy, as in the layer loop
     int tid_h = (int)threadIdx.x;
-    __asm__ volatile("" : "+v"(tid_h));
+    if constexpr (NT == 1) __asm__ volatile("" : "+v"(tid_h));
     const int tid = tid_h, lane = tid_h & 63;
     const int m_of = 4 * (lane >> 4), n_of = lane & 15;
     for (int i = tid; i < ROWS * FD; i += NTHR) {
