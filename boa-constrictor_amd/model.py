@@ -26,10 +26,12 @@ __all__ = ["BoaConstrictor", "BoaBytePredictor", "MambaBlock", "Mixer"]
 
 DEFAULT_TILE_LEN = int(os.environ.get("BOA_TILE_LEN", "64"))
 
-# GEMM arithmetic (include/boa_hip.h BOA_PREC_*): "f32" fp32 MFMA, "bf16x3" split-bfloat16 products (default),
-# "bf16w" bfloat16 weight matrices.  Compressor and decompressor must use the same mode.
+# GEMM arithmetic (include/boa_hip.h BOA_PREC_*): "f32" fp32 MFMA (default: the reference's fp32 arithmetic),
+# "bf16x3" split-bfloat16 products (fp32 operands as bf16 hi + lo, three products: ~16 significant bits per
+# operand, about twice as fast), "bf16w" bfloat16 weight matrices.  Compressor and decompressor must use the
+# same mode.
 PRECISIONS = {"f32": _nat.BOA_PREC_F32, "bf16x3": _nat.BOA_PREC_BF16X3, "bf16w": _nat.BOA_PREC_BF16W}
-DEFAULT_PRECISION = os.environ.get("BOA_PRECISION", "bf16x3")
+DEFAULT_PRECISION = os.environ.get("BOA_PRECISION", "f32")
 
 
 class Mixer(nn.Module):

@@ -65,3 +65,13 @@ def test_cli_round_trip(gpu, tmp_path, capsys):
     assert "VERIFY: OK" in out and "compression:" in out
     assert (tmp_path / "experiments" / "exp1" / "exp1_decompressed.bin").read_bytes() == data
     assert cli.main(["-c", str(p), "--no-progress", "--decompress-only", "--verify"]) == 0
+
+
+def test_default_precision_is_fp32():
+    """The drop-in model computes in the reference's fp32 arithmetic unless a narrower mode is asked for."""
+    import os
+
+    import model
+
+    assert model.DEFAULT_PRECISION == os.environ.get("BOA_PRECISION", "f32")
+    assert model.BoaConstrictor(256, 1, 256).precision == model.DEFAULT_PRECISION

@@ -337,7 +337,9 @@ def test_wave_lanes_from_device_memory(gpu):
 
     c = N.ModelCfg(256, 2, 256, 16, 4, 2, 0)
     b = ctypes.c_int64(0)
-    N.check(gpu.boa_ctx_plan_bytes(ctypes.byref(c), N.BOA_PREC_BF16X3, 64, 64, ctypes.byref(b)))
+    import model as M
+
+    N.check(gpu.boa_ctx_plan_bytes(ctypes.byref(c), M.PRECISIONS[m.precision], 64, 64, ctypes.byref(b)))
     assert b.value == eng.device_bytes
     os.environ["BOA_GPU_STREAMS"] = "5"
     try:
@@ -346,17 +348,20 @@ def test_wave_lanes_from_device_memory(gpu):
         del os.environ["BOA_GPU_STREAMS"]
 
 
-def test_compressed_size_vs_oracle_config2(gpu, ora):
+@pytest.mark.parametrize("precision", ["f32", "bf16x3"])
+def test_compressed_size_vs_oracle_config2(gpu, ora, precision):
     """configs[2]'s own model (d256 x 8 layers, seed 0) and data (float32 records, the first 32 of its 4096
-    chunks, first 1024 B of each) in the default bf16x3 mode: compressed size within 0.5% of the reference
-    protocol run on the CPU oracle (fp32 model -> torch.softmax -> Q2 at P = 24 -> coder), and the round
-    trip byte-exact."""
+    chunks, first 1024 B of each) in the default f32 mode and in bf16x3: compressed size within 0.5% of the
+    reference protocol run on the CPU oracle (fp32 model -> torch.softmax -> Q2 at P = 24 -> coder), and the
+    round trip byte-exact."""
     import codec
     from bench import synth_records
+    import model as M
 
     lanes, L = 32, 1024
     m, blob = _model(8, seed=0)
-    assert m.precision == "bf16x3"
+    assert M.DEFAULT_PRECISION == "f32" or "BOA_PRECISION" in os.environ
+    m.precision = precision
     data = np.ascontiguousarray(synth_records(lanes * 16384, 0).reshape(lanes, 16384)[:, :L])
     chunks = [data[i] for i in range(lanes)]
     payload, nw, fb, Ls = codec.compress_payload(m, chunks)
