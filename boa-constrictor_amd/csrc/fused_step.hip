@@ -21,7 +21,8 @@
 // NT = 1 is the fp32 precision mode: the GEMM operands are fp32 in LDS (the same regions, rows 4 elements
 // shorter) and every output accumulates 16-wide K groups of four v_mfma_f32_16x16x4_f32 in ascending order,
 // lane l supplying k = 16 g + 4 (l / 16) + j to the j-th, exactly as the tiled fp32 GEMM (k_gemm) does; x_proj
-// is one ascending accumulation over all 512 channels (no K-block fold), as that GEMM computes it.
+// is the same K-block fold as in the split modes (each 64-channel partial from zero in the wave that produced
+// those channels, then P_0 + P_1 + ...), as every fp32 path computes it.
 #include "model_dev.h"
 #include "model_internal.h"
 
@@ -244,7 +245,8 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
     constexpr int D_B = 3;         // K steps in flight, N = 1024 GEMMs
     constexpr int FPW_S = 16 / NWAVE;               // fragments per wave, N = 256 GEMMs
     constexpr int D_S = 6;         // K steps in flight, N = 256 GEMMs
-    // lane 0's SSM state is loaded before x_proj in the fp32 form, whose x_proj phase is long enough to hide it
+    // lane 0's SSM state is loaded before the x_proj fold in the fp32 form (with the per-channel scan parameters,
+    // which every form loads there)
     constexpr bool HOIST_FIRST = NT == 1;
     static_assert(NTHR == 512 && NTHR == FDI && NWAVE * XPROJ_KB == FDI, "fused step block size: one thread per channel");
     // every GEMM below but x_proj and head2 covers its fragments exactly (mgemm's CHECK = false)
@@ -353,10 +355,22 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
         // ---- conv + SiLU (thread = channel): xs fp32 in place of x, split operand, history ring; then this
         //      wavefront's x_proj partial P_wave over the 64 channels it has just produced (XPROJ_KB)
         {
-            // x_proj weight blocks of this wave's K block, issued first (they do not depend on the step)
+            // x_proj weight blocks of this wave's K block, issued first (they do not depend on the step).  fp32
+            // form: blocks (f, 4 wave + g), g < 4, of the fp32 fragment-packed matrix, two per 32-wide K step (in
+            // the registers the split parts use)
             constexpr int XS = FDI / 32, XF = FW / 16, XBLK = (NT == 3) ? 1024 : 512;
             uint4 xwh[XF][2], xwl[XF][2];
-            if constexpr (NT != 1) {
+            if constexpr (NT == 1) {
+                const gptr<float> xp = G(reinterpret_cast<const float*>(w.x_p));
+#pragma unroll
+                for (int f = 0; f < XF; ++f)
+#pragma unroll
+                    for (int s = 0; s < 2; ++s) {
+                        const int g = 4 * wave + 2 * s;
+                        xwh[f][s] = __builtin_bit_cast(uint4, ldg16(xp + ((int64_t)f * (FDI / 16) + g) * 256 + lane * 4));
+                        xwl[f][s] = __builtin_bit_cast(uint4, ldg16(xp + ((int64_t)f * (FDI / 16) + g + 1) * 256 + lane * 4));
+                    }
+            } else {
 #pragma unroll
                 for (int f = 0; f < XF; ++f)
 #pragma unroll
@@ -398,21 +412,30 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
                 store_op<NT, LA>(sAh, r, cq, y);
                 buf_st1(hr3, (uint32_t)(r * 3 * FDI + p0m3 * FDI + cq) * 4, x);
             }
-            // the partial reads only split values this wavefront wrote (channels 64 wave .. 64 wave + 63 of
-            // every row); LDS operations of one wavefront complete in order
-            if constexpr (NT != 1) {
+            // the partial reads only values this wavefront wrote (channels 64 wave .. 64 wave + 63 of every row);
+            // LDS operations of one wavefront complete in order
+            {
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_wave_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-                const int ar = lane & 15, kq = 8 * (lane >> 4);
+                const int ar = lane & 15;
                 floatx4 part[XF];
 #pragma unroll
                 for (int f = 0; f < XF; ++f) part[f] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int s = 0; s < 2; ++s) {
-                    const int k0 = XPROJ_KB * wave + 32 * s;
-                    const bf16x8 ah = *reinterpret_cast<const bf16x8*>(sAh + ar * LA + k0 + kq);
-                    const bf16x8 al = *reinterpret_cast<const bf16x8*>(sAl + ar * LA + k0 + kq);
+                    bf16x8 ah, al;
+                    if constexpr (NT == 1) {
+                        // fp32 rows: lane l's 4 values of groups 4 wave + 2 s and + 1 (k = 16 g + 4 (l / 16) + j)
+                        const float* r32 = reinterpret_cast<const float*>(sAh) + ar * ld32(LA) + XPROJ_KB * wave +
+                                           32 * s + 4 * (lane >> 4);
+                        ah = __builtin_bit_cast(bf16x8, *reinterpret_cast<const float4*>(r32));
+                        al = __builtin_bit_cast(bf16x8, *reinterpret_cast<const float4*>(r32 + 16));
+                    } else {
+                        const int k0 = XPROJ_KB * wave + 32 * s, kq = 8 * (lane >> 4);
+                        ah = *reinterpret_cast<const bf16x8*>(sAh + ar * LA + k0 + kq);
+                        al = *reinterpret_cast<const bf16x8*>(sAl + ar * LA + k0 + kq);
+                    }
 #pragma unroll
                     for (int f = 0; f < XF; ++f)
                         part[f] = mfma_split_step<NT>(part[f], ah, al, __builtin_bit_cast(bf16x8, xwh[f][s]),
@@ -457,24 +480,13 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
             for (int n = 0; n < FNS; n += 4) h_first[n / 4] = buf_ld4(sr, h_off(0, n, c));
         };
         if constexpr (HOIST_FIRST) load_first();
-        if constexpr (NT == 1) {
-            // ---- x_proj over all 512 channels at once (fp32 mode: one ascending accumulation per output):
-            //      waves 0..2 own output fragments 0..2 (a wave-uniform condition around the whole GEMM)
-            if (wave < FW / 16) {
-                floatx4 acc[1];
-                mgemm<NT, NWAVE, 1, FDI, 4, false>(sAh, sAl, LA, w.x_p, 0, FW / 16, wave, lane, 0, acc);
+        // ---- x_proj fold: dbc = P_0 + P_1 + ... + P_7, in place of P_0 (element i is read and written by one
+        //      thread only)
+        for (int i = tid; i < ROWS * FW; i += NTHR) {
+            float v = sPart[i];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) sDbc[(m_of + r) * FW + 16 * wave + n_of] = acc[0][r];
-            }
-        } else {
-            // ---- x_proj fold: dbc = P_0 + P_1 + ... + P_7, in place of P_0 (element i is read and written by
-            //      one thread only)
-            for (int i = tid; i < ROWS * FW; i += NTHR) {
-                float v = sPart[i];
-#pragma unroll
-                for (int q = 1; q < FDI / XPROJ_KB; ++q) v = v + sPart[q * (ROWS * FW) + i];
-                sDbc[i] = v;
-            }
+            for (int q = 1; q < FDI / XPROJ_KB; ++q) v = v + sPart[q * (ROWS * FW) + i];
+            sDbc[i] = v;
         }
         __syncthreads();
         // ---- dt_proj + softplus + selective scan + D + gate (thread = channel) -> y split operand

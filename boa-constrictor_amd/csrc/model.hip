@@ -731,6 +731,51 @@ __global__ void __launch_bounds__(256) k_xproj(const float* __restrict__ xs, int
         }
 }
 
+// x_proj in the fp32 mode for the layer-by-layer path: one wavefront per 16 rows computes all NF output fragments
+// from xs [M][di] and the fp32 weight matrix W [N][di] (row-major, as in the weight blob), with the K-block fold of
+// XPROJ_KB: P_q accumulates the four 16-K groups of channels 64 q .. 64 q + 63 from zero through
+// v_mfma_f32_16x16x4_f32 (lane l supplies k = 16 g + 4 (l / 16) + j to the j-th MFMA of group g, as every fp32
+// kernel does), then dbc = P_0 + P_1 + ....  A position's dbc row is therefore the one the fused fp32 compress
+// (k_mixin<1>) and decode (k_fused_step<1, 512>) kernels compute.  Row m of the output depends on row m of xs only.
+template <int NF>
+__global__ void __launch_bounds__(256) k_xproj_f32(const float* __restrict__ xs, int64_t M, int di,
+                                                  const float* __restrict__ W, float* __restrict__ dbc, int ldd) {
+    const int lane = threadIdx.x & 63;
+    const int64_t m0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 16;
+    if (m0 >= M) return;
+    const int ar = lane & 15, kq = 4 * (lane >> 4);
+    const bool ok = m0 + ar < M;
+    floatx4 acc[NF];
+    for (int q = 0; q < di / XPROJ_KB; ++q) {
+        floatx4 part[NF];
+#pragma unroll
+        for (int f = 0; f < NF; ++f) part[f] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int g = 0; g < XPROJ_KB / 16; ++g) {
+            const int k0 = XPROJ_KB * q + 16 * g + kq;
+            float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (ok) a = *reinterpret_cast<const float4*>(xs + (m0 + ar) * di + k0);
+#pragma unroll
+            for (int f = 0; f < NF; ++f) {
+                const float4 b = *reinterpret_cast<const float4*>(W + (int64_t)(16 * f + ar) * di + k0);
+                part[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, part[f], 0, 0, 0);
+                part[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, part[f], 0, 0, 0);
+                part[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, part[f], 0, 0, 0);
+                part[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, part[f], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int f = 0; f < NF; ++f) acc[f] = q == 0 ? part[f] : acc[f] + part[f];
+    }
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t row = m0 + 4 * (lane >> 4) + r;
+            if (row < M) dbc[row * ldd + 16 * f + ar] = acc[f][r];
+        }
+}
+
 // ================================================================================================
 // Feed-forward half of a block in one kernel (split modes, d_model 256, d_ff 1024), for row tiles:
 //   x <- x + FF2(GELU(FF1(LN2(mm))))        (model.py:60-65: Linear -> GELU -> Linear, then the block residual)
@@ -1474,19 +1519,9 @@ __global__ void __launch_bounds__(256, 2) k_mixin(const float* __restrict__ x, c
             buf_st1(hw, (uint32_t)(e2 * DI + c) * 4, xv[18]);
         }
         __syncthreads();
-        // x_proj partial over this chunk's 64 channels (K block k): rows 16 wave .. + 15, fragments 0..2.  The
-        // fp32 mode accumulates straight into dbc instead (chunks in ascending channel order: one ascending K
-        // accumulation, as the tiled fp32 GEMM computes x_proj).
-        if constexpr (NT == 1) {
-#pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                const int o = x_off(16 * wave + ar, 32 * s + kq);
-                const bf16x8 ah = *reinterpret_cast<const bf16x8*>(&sXh[o]);
-                const bf16x8 al = *reinterpret_cast<const bf16x8*>(&sXl[o]);
-#pragma unroll
-                for (int j = 0; j < 3; ++j) dacc[j] = mfma_split_step<NT>(dacc[j], ah, al, xwh[s][j], xwl[s][j]);
-            }
-        } else {
+        // x_proj partial over this chunk's 64 channels (K block k, from zero): rows 16 wave .. + 15, fragments
+        // 0..2, folded into dbc in ascending block order (XPROJ_KB; every mode)
+        {
             floatx4 part[3];
 #pragma unroll
             for (int j = 0; j < 3; ++j) part[j] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -1705,6 +1740,16 @@ __global__ void __launch_bounds__(512, 2) k_mixin512(const float* __restrict__ x
     for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) GM(dbc)[(m0 + 16 * xr + m_of + r) * FW + 16 * (xf + j) + ar] = dacc[j][r];
+}
+
+// fp32 mode: the K-block fold over the fp32 weight matrix (k_xproj_f32)
+static int launch_xproj_f32(const float* xs, int64_t M, int di, const float* W, float* dbc, int ldd, hipStream_t s) {
+    const unsigned grid = (unsigned)((M + 63) / 64);
+    if (di % XPROJ_KB != 0) return boa_fail(BOA_ERR_ARG, "internal: d_inner %d not a multiple of %d", di, XPROJ_KB);
+    if (ldd == 48) hipLaunchKernelGGL((k_xproj_f32<3>), dim3(grid), dim3(256), 0, s, xs, M, di, W, dbc, ldd);
+    else if (ldd == 64) hipLaunchKernelGGL((k_xproj_f32<4>), dim3(grid), dim3(256), 0, s, xs, M, di, W, dbc, ldd);
+    else return boa_fail(BOA_ERR_ARG, "internal: x_proj width %d not supported (48 or 64)", ldd);
+    return BOA_OK;
 }
 
 static int launch_xproj(const float* xs, int64_t M, int di, const uint16_t* Wh, const uint16_t* Wl, float* dbc, int ldd,
@@ -2874,10 +2919,9 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc, int part = 7) {
                             hist, w.conv_w, w.conv_b, x->xs, di, Tc, (int)(x->pos % 3)));
     // x_proj -> dbc [M][R+2NS]
     {
-        GemmArgs g = gemm_args(x->xs, di, w.x_w, nullptr, x->dbc, R + 2 * NS, M, R + 2 * NS, di);
         PROF(PC_XPROJ, gemm_flops(M, R + 2 * NS, di), gemm_bytes(M, R + 2 * NS, di),
              rc = split ? launch_xproj(x->xs, M, di, w.x_w.h, w.x_w.l, x->dbc, R + 2 * NS, s)
-                        : (launch_gemm_f32_cfg<64, 64, 0, EPI_NONE>(g, s)));
+                        : launch_xproj_f32(x->xs, M, di, w.x_w.f, x->dbc, R + 2 * NS, s));
         if (rc) return rc;
     }
     }

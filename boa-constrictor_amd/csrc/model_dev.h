@@ -185,11 +185,12 @@ __device__ __forceinline__ floatx4 mfma_split_step_t(floatx4 acc, bf16x8 ah, bf1
 // no longer hides any latency.
 __device__ __forceinline__ void pin_loads() { asm volatile("" ::: "memory"); }
 
-// x_proj (d_inner -> dt_rank + 2 d_state) in the split modes is a sum of K-block partials:
+// x_proj (d_inner -> dt_rank + 2 d_state) is a sum of K-block partials in every precision mode:
 //   dbc = P_0 + P_1 + ... + P_{d_inner/64 - 1}   (left to right, fp32 adds)
-// where P_q accumulates the two 32-wide K steps of channels 64q .. 64q + 63 from zero.  The fused decode
-// kernel computes P_q in the wavefront that produced those channels' conv outputs, so x_proj starts without
-// a workgroup barrier; the compress and per-layer decode paths compute the same partials and the same fold.
+// where P_q accumulates the two 32-wide K steps (four 16-K groups in the fp32 mode) of channels 64q .. 64q + 63
+// from zero.  The fused decode kernels compute P_q in the wavefront that produced those channels' conv outputs,
+// so x_proj starts without a workgroup barrier; the compress and per-layer paths compute the same partials and
+// the same fold.
 constexpr int XPROJ_KB = 64;
 
 // Activations on the hardware transcendental units (v_exp_f32 = 2^x, v_log_f32 = log2 x, v_rcp_f32 = 1/x,
