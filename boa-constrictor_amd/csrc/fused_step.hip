@@ -96,12 +96,20 @@ __device__ __forceinline__ void mgemm_f32(const float* A, int lda, const float* 
 #pragma unroll
     for (int j = 0; j < FPW; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
     float4 bw[RD][FPW];
+    // Weight loads through a buffer descriptor: a fragment's lane offset sits in the vector operand (formed once per
+    // pass), the group's offset (g KB) in the scalar one, so a load costs no vector address arithmetic.  (With
+    // 64-bit global addresses, two VALU adds per load competed with the MFMAs for issue: an isolated in_proj phase
+    // took 18.8-20 us against 15.1-15.3 us with this form.)
+    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(Wp, (uint32_t)nfrag * S * 1024u);
+    uint32_t voff[FPW];
+#pragma unroll
+    for (int j = 0; j < FPW; ++j) voff[j] = (uint32_t)(frag_of<NWAVE>(f0, wave, j, nfrag, rot) * S * 1024 + lane * 16);
     auto load = [&](int g, int slot) {
 #pragma unroll
         for (int j = 0; j < FPW; ++j) {
             if (valid(j)) {
-                const int f = frag_of<NWAVE>(f0, wave, j, nfrag, rot);
-                bw[slot][j] = ldg_f4(G(Wp) + ((int64_t)f * S + g) * 256 + lane * 4);
+                const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, voff[j], g * 1024, 0));
+                bw[slot][j] = make_float4(v.x, v.y, v.z, v.w);
             }
         }
     };
@@ -239,9 +247,10 @@ template <int NT, int NTHR>
 __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
     constexpr int NWAVE = NTHR / 64;
     constexpr int RPW = ROWS / NWAVE;               // rows per wave (LN, decode)
-    // fragments per wave and pass, N = 1024 GEMMs: 4 in the split forms; 2 in the fp32 form, whose in_proj and FF1
-    // keep 16 groups of 16 K in flight instead (the weight stream from L2 bounds them: 0.868 -> 0.840 ms per step)
-    constexpr int FPW_B = NT == 1 ? 2 : 4;
+    // fragments per wave and pass, N = 1024 GEMMs: 4 in the split forms; 8 in the fp32 form (one pass for in_proj,
+    // two for FF1), with 2 groups of 16 K in flight (the widest fragment set with the buffer-loaded weights measured
+    // best: 0.79 ms per step against 0.80 with 2 fragments and 16 groups in flight, 0.82 with 4 and 4)
+    constexpr int FPW_B = NT == 1 ? 8 : 4;
     constexpr int D_B = 3;         // K steps in flight, N = 1024 GEMMs
     constexpr int FPW_S = 16 / NWAVE;               // fragments per wave, N = 256 GEMMs
     constexpr int D_S = 6;         // K steps in flight, N = 256 GEMMs
@@ -342,7 +351,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
             float bias_j[FPW_B];  // loaded ahead of the weight ring (in-order wait counter)
 #pragma unroll
             for (int j = 0; j < FPW_B; ++j) bias_j[j] = G(w.in_b)[16 * frag_of<NWAVE>(f0, wave, j, 2 * FDI / 16, rot64) + n_of];
-            mgemm<NT, NWAVE, FPW_B, FD, D_B, false, 16>(sAh, sAl, LA, w.in_p, f0, 2 * FDI / 16, wave, lane, rot64, acc);
+            mgemm<NT, NWAVE, FPW_B, FD, D_B, false, 2>(sAh, sAl, LA, w.in_p, f0, 2 * FDI / 16, wave, lane, rot64, acc);
 #pragma unroll
             for (int j = 0; j < FPW_B; ++j) {
                 const int n = 16 * frag_of<NWAVE>(f0, wave, j, 2 * FDI / 16, rot64) + n_of;
@@ -544,7 +553,7 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
             float bias_j[FPW_B];
 #pragma unroll
             for (int j = 0; j < FPW_B; ++j) bias_j[j] = G(w.ff1_b)[16 * frag_of<NWAVE>(f0, wave, j, 4 * FD / 16, rot64) + n_of];
-            mgemm<NT, NWAVE, FPW_B, FD, D_B, false, 16>(sAh, sAl, LA, w.ff1_p, f0, 4 * FD / 16, wave, lane, rot64, acc);
+            mgemm<NT, NWAVE, FPW_B, FD, D_B, false, 2>(sAh, sAl, LA, w.ff1_p, f0, 4 * FD / 16, wave, lane, rot64, acc);
 #pragma unroll
             for (int j = 0; j < FPW_B; ++j) {
                 const int n = 16 * frag_of<NWAVE>(f0, wave, j, 4 * FD / 16, rot64) + n_of;
