@@ -247,8 +247,8 @@ template <int NT, int NTHR>
 __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
     constexpr int NWAVE = NTHR / 64;
     constexpr int RPW = ROWS / NWAVE;               // rows per wave (LN, decode)
-    // fragments per wave and pass, N = 1024 GEMMs: 4 in the split forms; 8 in the fp32 form (one pass for in_proj,
-    // two for FF1), with 2 groups of 16 K in flight (the widest fragment set with the buffer-loaded weights measured
+    // fragments per wave and pass, N = 1024 GEMMs (in_proj, FF1): 4 in the split forms (two passes); 8 in the fp32
+    // form (one pass), with 2 groups of 16 K in flight (the widest fragment set with the buffer-loaded weights measured
     // best: 0.79 ms per step against 0.80 with 2 fragments and 16 groups in flight, 0.82 with 4 and 4)
     constexpr int FPW_B = NT == 1 ? 8 : 4;
     constexpr int D_B = 3;         // K steps in flight, N = 1024 GEMMs

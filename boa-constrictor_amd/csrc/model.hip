@@ -842,14 +842,14 @@ __global__ void __launch_bounds__(512, 4) k_ffn(const float* __restrict__ mm, co
     };
     if constexpr (OUTP) {
         constexpr int KO = 2 * D, KC = D, NKS = KO / 32, BLKO = two_part_blocks<NT>() ? 1024 : 512, RO = 4;
-        const gptr<uint16_t> wop = G(Wop);
+        const __amdgpu_buffer_rsrc_t wop = wbuf(Wop);
         u32x4 oh[RO], ol[RO];
         // block i (W_out fragment 2 wave + i % 2, K step i / 2) into ring slot i % RO
         auto issue_o = [&](int i) {
-            const gptr<uint16_t> q = wop + ((int64_t)(2 * wave + (i & 1)) * NKS + (i >> 1)) * BLKO + lane * 8;
-            oh[i % RO] = ldg16(q);
+            const uint32_t bo = (uint32_t)(((2 * wave + (i & 1)) * NKS + (i >> 1)) * BLKO * 2);
+            oh[i % RO] = wbuf_ld16(wop, lane * 16, bo);
             ol[i % RO] = oh[i % RO];
-            if constexpr (two_part_blocks<NT>()) ol[i % RO] = ldg16(q + 512);
+            if constexpr (two_part_blocks<NT>()) ol[i % RO] = wbuf_ld16(wop, lane * 16, bo + 1024);
         };
 #pragma unroll
         for (int i = 0; i < RO; ++i) issue_o(i);
@@ -946,18 +946,18 @@ __global__ void __launch_bounds__(512, 4) k_ffn(const float* __restrict__ mm, co
     __syncthreads();
     const int ar = lane & 15, kq = 8 * (lane >> 4), m_of = 4 * (lane >> 4);
     constexpr int BLK = two_part_blocks<NT>() ? 1024 : 512;
-    const gptr<uint16_t> w1p = G(W1p), w2p = G(W2p);
+    const __amdgpu_buffer_rsrc_t w1p = wbuf(W1p), w2p = wbuf(W2p);
     const int rh = wave & 1, cf = wave >> 1;
     constexpr int NBC = 12, R = 4;
     static_assert(NBC % R == 0, "ring slots divide the blocks of a chunk");
     u32x4 rhh[R], rll[R];
     auto issue = [&](int c, int i) {
-        const int64_t blk = i < 8 ? (int64_t)(4 * c + cf) * (D / 32) + i
-                                  : (int64_t)(2 * wave + ((i - 8) & 1)) * (DF / 32) + 2 * c + ((i - 8) >> 1);
-        const gptr<uint16_t> q = (i < 8 ? w1p : w2p) + blk * BLK + lane * 8;
-        rhh[i % R] = ldg16(q);
+        const int blk = i < 8 ? (4 * c + cf) * (D / 32) + i
+                              : (2 * wave + ((i - 8) & 1)) * (DF / 32) + 2 * c + ((i - 8) >> 1);
+        const __amdgpu_buffer_rsrc_t wr = i < 8 ? w1p : w2p;
+        rhh[i % R] = wbuf_ld16(wr, lane * 16, (uint32_t)(blk * BLK * 2));
         rll[i % R] = rhh[i % R];
-        if constexpr (two_part_blocks<NT>()) rll[i % R] = ldg16(q + 512);
+        if constexpr (two_part_blocks<NT>()) rll[i % R] = wbuf_ld16(wr, lane * 16, (uint32_t)(blk * BLK * 2 + 1024));
     };
     auto refill = [&](int c, int cn, int i) {
         if (i + R < NBC) issue(c, i + R);
@@ -1398,7 +1398,7 @@ __global__ void __launch_bounds__(256, 2) k_mixin(const float* __restrict__ x, c
     __syncthreads();
 
     const int ar = lane & 15, kq = 8 * (lane >> 4), m_of = 4 * (lane >> 4);
-    const gptr<uint16_t> wip = G(Wip), wxp = G(Wxp);
+    const __amdgpu_buffer_rsrc_t wip = wbuf(Wip), wxp = wbuf(Wxp);
     // in_proj chunk k (columns CH k .. CH k + 63; chunks 0..7 are x, 8..15 are z): wave w computes columns
     // CH k + 16 w .. + 15 for all 64 rows, with the weight block (fragment 4 k + w, K step s) as the A operand
     // (mfma_split_step_t): lane l holds columns 16 w + m_of + r of row 16 i + ar.  The 8 blocks of a chunk
@@ -1408,10 +1408,10 @@ __global__ void __launch_bounds__(256, 2) k_mixin(const float* __restrict__ x, c
     auto chunk_of = [](int i) { return i < NCH / 2 ? NCH / 2 + i : i - NCH / 2; };  // i-th chunk processed
     u32x4 r1h[R1], r1l[R1];
     auto issue_w = [&](int k, int s) {  // block (fragment 4 k + wave, K step s) into slot s
-        const gptr<uint16_t> q = wip + ((int64_t)((CH / 16) * k + wave) * (D / 32) + s) * BLK + lane * 8;
-        r1h[s] = ldg16(q);
+        const uint32_t bo = (uint32_t)((((CH / 16) * k + wave) * (D / 32) + s) * BLK * 2);
+        r1h[s] = wbuf_ld16(wip, lane * 16, bo);
         r1l[s] = r1h[s];
-        if constexpr (two_part_blocks<NT>()) r1l[s] = ldg16(q + 512);
+        if constexpr (two_part_blocks<NT>()) r1l[s] = wbuf_ld16(wip, lane * 16, bo + 1024);
     };
 #pragma unroll
     for (int s = 0; s < R1; ++s) issue_w(chunk_of(0), s);
@@ -1480,10 +1480,11 @@ __global__ void __launch_bounds__(256, 2) k_mixin(const float* __restrict__ x, c
             for (int s = 0; s < 2; ++s)
 #pragma unroll
                 for (int j = 0; j < 3; ++j) {
-                    const gptr<uint16_t> q = wxp + ((int64_t)j * (DI / 32) + 2 * k + s) * BLK + lane * 8;
-                    const u32x4 bh = ldg16(q);
+                    const uint32_t bo = (uint32_t)((j * (DI / 32) + 2 * k + s) * BLK * 2);
+                    const u32x4 bh = wbuf_ld16(wxp, lane * 16, bo);
                     xwh[s][j] = __builtin_bit_cast(bf16x8, bh);
-                    xwl[s][j] = two_part_blocks<NT>() ? __builtin_bit_cast(bf16x8, ldg16(q + 512)) : xwh[s][j];
+                    xwl[s][j] = two_part_blocks<NT>() ? __builtin_bit_cast(bf16x8, wbuf_ld16(wxp, lane * 16, bo + 1024))
+                                                      : xwh[s][j];
                 }
             pin_loads();
             float xv[19];
@@ -2023,18 +2024,17 @@ __global__ void __launch_bounds__(512, (D == 256) ? 4 : 2) k_head_xq(const float
     const int ar = lane & 15, m_of = 4 * (lane >> 4);
     __syncthreads();
     constexpr int BLK = two_part_blocks<NT>() ? 1024 : 512;
-    const gptr<uint16_t> w1p = G(W1p), w2p = G(W2p);
+    const __amdgpu_buffer_rsrc_t w1p = wbuf(W1p), w2p = wbuf(W2p);
     const int rh = wave & 1, cf = wave >> 1;
     constexpr int KS = D / 32, NBC = KS + 4, R = 4, NC = D / HC;
     static_assert(NBC % R == 0 && KS % R == 0, "ring slots divide the blocks of a chunk");
     u32x4 rhh[R], rll[R];
     auto issue = [&](int c, int i) {
-        const int64_t blk = i < KS ? (int64_t)(4 * c + cf) * KS + i
-                                   : (int64_t)(2 * wave + ((i - KS) & 1)) * KS + 2 * c + ((i - KS) >> 1);
-        const gptr<uint16_t> q = (i < KS ? w1p : w2p) + blk * BLK + lane * 8;
-        rhh[i % R] = ldg16(q);
+        const int blk = i < KS ? (4 * c + cf) * KS + i : (2 * wave + ((i - KS) & 1)) * KS + 2 * c + ((i - KS) >> 1);
+        const __amdgpu_buffer_rsrc_t wr = i < KS ? w1p : w2p;
+        rhh[i % R] = wbuf_ld16(wr, lane * 16, (uint32_t)(blk * BLK * 2));
         rll[i % R] = rhh[i % R];
-        if constexpr (two_part_blocks<NT>()) rll[i % R] = ldg16(q + 512);
+        if constexpr (two_part_blocks<NT>()) rll[i % R] = wbuf_ld16(wr, lane * 16, (uint32_t)(blk * BLK * 2 + 1024));
     };
     auto refill = [&](int c, int cn, int i) {
         if (i + R < NBC) issue(c, i + R);
