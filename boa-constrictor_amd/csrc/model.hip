@@ -1083,7 +1083,17 @@ namespace ffn5 {
 constexpr int BM = 64, D = 512, DF = 2048, HC = 64;
 // 16-byte chunks XOR-swizzled by row (low 4 bits of the chunk index), so 16-row fragment reads spread over banks
 __device__ __forceinline__ int a_off(int r, int k) { return r * D + (((k >> 3) ^ (r & 15)) << 3) + (k & 7); }
-__device__ __forceinline__ int h_off(int r, int k) { return r * HC + (((k >> 3) ^ (r >> 1)) & 7) * 8 + (k & 7); }
+// the hidden chunk [64][HW] (HW = 64: 8 chunks of 16 bytes per row, swizzled by row / 2; HW = 128: 16 per row,
+// swizzled by row)
+template <int HW>
+__device__ __forceinline__ int h_off(int r, int k) {
+    if constexpr (HW == 64) return r * HW + (((k >> 3) ^ (r >> 1)) & 7) * 8 + (k & 7);
+    else return r * HW + (((k >> 3) ^ r) & 15) * 8 + (k & 7);
+}
+// W1 fragments per wave and hidden chunk: 2 with bf16 weights (chunks of 128 hidden units: each LN2 operand
+// fragment read from LDS feeds two weight blocks), 1 with bf16x3 weights (no registers to spare)
+template <int NT>
+constexpr int ffn_groups() { return NT == 2 ? 2 : 1; }
 }  // namespace ffn5
 
 // OUTP: the out_proj GEMM runs first, inside this kernel (decode step and compress tiles at d_model 512): mm =
@@ -1100,7 +1110,7 @@ __global__ void __launch_bounds__(512, 2) k_ffn512(const float* __restrict__ mm,
                                                    const uint16_t* __restrict__ Wop, const float* __restrict__ bo) {
     using namespace ffn5;
     __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * D];
-    __shared__ __attribute__((aligned(16))) uint16_t sH[2][BM * HC];
+    __shared__ __attribute__((aligned(16))) uint16_t sH[2][BM * HC * ffn_groups<NT>()];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int64_t m0 = (int64_t)blockIdx.x * BM;
@@ -1224,15 +1234,15 @@ __global__ void __launch_bounds__(512, 2) k_ffn512(const float* __restrict__ mm,
     constexpr int BLK = (NT == 3) ? 1024 : 512;
     const gptr<uint16_t> w1p = G(W1p), w2p = G(W2p);
     const int rh = wave & 1, cf = wave >> 1;
-    constexpr int NB1 = D / 32, NBC = NB1 + 8, R = 6;
+    constexpr int FG = ffn_groups<NT>(), HW = FG * HC, NB1 = D / 32, NF1 = FG * NB1, NBC = NF1 + HW / 8, R = 6;
     static_assert(NBC % R == 0, "ring slots divide the blocks of a chunk");
     u32x4 rhh[R], rll[R];
-    // block i of chunk c: i < 16: W1 fragment 4 c + cf, K step i; else W2 fragment 4 wave + (i - 16) % 4,
-    // K step 2 c + (i - 16) / 4
+    // block i of chunk c: i < NF1: W1 fragment (4 c + cf) FG + i % FG, K step i / FG; else W2 fragment
+    // 4 wave + (i - NF1) % 4, K step (HW / 32) c + (i - NF1) / 4
     auto issue = [&](int c, int i) {
-        const int64_t blk = i < NB1 ? (int64_t)(4 * c + cf) * (D / 32) + i
-                                    : (int64_t)(4 * wave + ((i - NB1) & 3)) * (DF / 32) + 2 * c + ((i - NB1) >> 2);
-        const gptr<uint16_t> q = (i < NB1 ? w1p : w2p) + blk * BLK + lane * 8;
+        const int64_t blk = i < NF1 ? (int64_t)((4 * c + cf) * FG + i % FG) * (D / 32) + i / FG
+                                    : (int64_t)(4 * wave + ((i - NF1) & 3)) * (DF / 32) + (HW / 32) * c + ((i - NF1) >> 2);
+        const gptr<uint16_t> q = (i < NF1 ? w1p : w2p) + blk * BLK + lane * 8;
         rhh[i % R] = ldg16(q);
         rll[i % R] = rhh[i % R];
         if constexpr (NT == 3) rll[i % R] = ldg16(q + 512);
@@ -1249,55 +1259,81 @@ __global__ void __launch_bounds__(512, 2) k_ffn512(const float* __restrict__ mm,
 #pragma unroll
     for (int i = 0; i < R; ++i) issue(0, i);
 #pragma unroll 1
-    for (int c = 0; c < DF / HC; ++c) {
-        const int cn = c + 1 < DF / HC ? c + 1 : c;
-        const float4 bias = ldg_f4(G(b1) + HC * c + 16 * cf + m_of);
-        floatx4 hacc[2];
+    for (int c = 0; c < DF / HW; ++c) {
+        const int cn = c + 1 < DF / HW ? c + 1 : c;
+        float4 bias[FG];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) hacc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int g = 0; g < FG; ++g) bias[g] = ldg_f4(G(b1) + HW * c + 16 * (FG * cf + g) + m_of);
+        floatx4 hacc[FG][2];
 #pragma unroll
-        for (int s = 0; s < NB1; ++s) {
-            bf16x8 ah[2], al[2];
+        for (int g = 0; g < FG; ++g)
+#pragma unroll
+            for (int i = 0; i < 2; ++i) hacc[g][i] = floatx4{0.f, 0.f, 0.f, 0.f};
+        // the LN2 operand fragments of K step s into register slot u; with bf16 weights (NT 2) one K step ahead of
+        // their MFMAs, so the LDS read latency is not exposed at every step (NT 3 has no registers to spare)
+        constexpr int AS = NT == 2 ? 2 : 1;
+        bf16x8 ah[AS][2], al[AS][2];
+        auto lda = [&](int s, int u) {
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 const int o = a_off(32 * rh + 16 * i + ar, 32 * s + kq);
-                ah[i] = *reinterpret_cast<const bf16x8*>(&sA[0][o]);
-                al[i] = *reinterpret_cast<const bf16x8*>(&sA[1][o]);
+                ah[u][i] = *reinterpret_cast<const bf16x8*>(&sA[0][o]);
+                al[u][i] = *reinterpret_cast<const bf16x8*>(&sA[1][o]);
             }
+        };
+        if constexpr (AS == 2) lda(0, 0);
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
-                hacc[i] = mfma_split_step_t<NT>(hacc[i], ah[i], al[i], __builtin_bit_cast(bf16x8, rhh[s % R]),
-                                                __builtin_bit_cast(bf16x8, rll[s % R]));
-            refill(c, cn, s);
+        for (int s = 0; s < NB1; ++s) {
+            if constexpr (AS == 2) {
+                if (s + 1 < NB1) lda(s + 1, (s + 1) & 1);
+                __builtin_amdgcn_sched_barrier(0);
+            } else {
+                lda(s, 0);
+            }
+            const int u = AS == 2 ? (s & 1) : 0;
+#pragma unroll
+            for (int g = 0; g < FG; ++g) {
+                const int bi = FG * s + g;
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                    hacc[g][i] = mfma_split_step_t<NT>(hacc[g][i], ah[u][i], al[u][i],
+                                                       __builtin_bit_cast(bf16x8, rhh[bi % R]),
+                                                       __builtin_bit_cast(bf16x8, rll[bi % R]));
+                refill(c, cn, bi);
+            }
             pin_loads();
+            // nothing crosses a step boundary or the reads above: without the fences the scheduler moves each step's
+            // MFMAs up to their operand reads, and the reads are back in front of their uses
+            if constexpr (AS == 2) __builtin_amdgcn_sched_barrier(0);
         }
-        {
-            const float bv[4] = {bias.x, bias.y, bias.z, bias.w};
+#pragma unroll
+        for (int g = 0; g < FG; ++g) {
+            const float bv[4] = {bias[g].x, bias[g].y, bias[g].z, bias[g].w};
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                float g[4];
+                float h[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) g[r] = epi_value<EPI_GELU>(hacc[i][r], bv[r]);
+                for (int r = 0; r < 4; ++r) h[r] = epi_value<EPI_GELU>(hacc[g][i][r], bv[r]);
                 uint2 hp, lp;
-                split4(g[0], g[1], g[2], g[3], hp, lp);
-                const int o = h_off(32 * rh + 16 * i + ar, 16 * cf + m_of);
+                split4(h[0], h[1], h[2], h[3], hp, lp);
+                const int o = h_off<HW>(32 * rh + 16 * i + ar, 16 * (FG * cf + g) + m_of);
                 *reinterpret_cast<uint2*>(&sH[0][o]) = hp;
                 *reinterpret_cast<uint2*>(&sH[1][o]) = lp;
             }
         }
         __syncthreads();
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+        for (int t = 0; t < HW / 32; ++t) {
             bf16x8 ah[4], al[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int o = h_off(16 * i + ar, 32 * t + kq);
+                const int o = h_off<HW>(16 * i + ar, 32 * t + kq);
                 ah[i] = *reinterpret_cast<const bf16x8*>(&sH[0][o]);
                 al[i] = *reinterpret_cast<const bf16x8*>(&sH[1][o]);
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int bi = NB1 + 4 * t + j;
+                const int bi = NF1 + 4 * t + j;
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     out[i][j] = mfma_split_step<NT>(out[i][j], ah[i], al[i], __builtin_bit_cast(bf16x8, rhh[bi % R]),
