@@ -1871,17 +1871,28 @@ __global__ void __launch_bounds__(256) k_scan(float* __restrict__ xs_y, const fl
     float* hp = ssm + b * di * NS + 4 * c;
     scan_load_channel<NS, R>(c, di, hp, Aneg, dt_w, h, a, wr);
     const float bdt = dt_b[c], Dc = Dp[c];
-    float xn = xs_y[row0 * di + c];
-    float zn = xz[row0 * ldxz + di + c];
-    for (int t = 0; t < Tc; ++t) {
-        const int64_t m = row0 + t;
-        const float x = xn, z = zn;
-        // next position's inputs in flight while this one computes (the last position reloads its own: no
-        // load under a branch, and a loop the register allocator keeps free of copies)
-        const int64_t mn = t + 1 < Tc ? m + 1 : m;
-        xn = xs_y[mn * di + c];
-        zn = xz[mn * ldxz + di + c];
-        scan_store_y<OUTS>(xs_y, yh, yl, m * di + c, scan_position<NS, R>(dbc + m * ldd, wr, bdt, a, Dc, x, z, h));
+    // x and z of positions t + 1 and t + 2 in flight while position t computes: a ring of three register slots,
+    // position t in slot t % 3 (the loop unrolled by three), reloaded with position t + 3 once used; loads past
+    // the tile repeat its last position (read before that position's y is written over it, and unused)
+    float xr[3], zr[3];
+    auto ld = [&](int t, int u) {
+        const int64_t m = row0 + (t < Tc ? t : Tc - 1);
+        xr[u] = xs_y[m * di + c];
+        zr[u] = xz[m * ldxz + di + c];
+    };
+    ld(0, 0);
+    ld(1, 1);
+    for (int t0 = 0; t0 < Tc; t0 += 3) {
+#pragma unroll
+        for (int u = 0; u < 3; ++u) {
+            const int t = t0 + u;
+            if (t < Tc) {
+                ld(t + 2, (u + 2) % 3);
+                const int64_t m = row0 + t;
+                scan_store_y<OUTS>(xs_y, yh, yl, m * di + c,
+                                   scan_position<NS, R, true>(dbc + m * ldd, wr, bdt, a, Dc, xr[u], zr[u], h));
+            }
+        }
     }
     scan_store_channel<NS>(hp, di, h);
 }

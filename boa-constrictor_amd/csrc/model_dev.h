@@ -268,7 +268,15 @@ __device__ __forceinline__ float scan_dt(const float* row, const float (&wr)[R],
     dt = dt + bdt;
     return hw_softplus(dt);
 }
-template <int NS, int R>
+// INPLACE: the state update as one v_fma_f32 whose result overwrites h_n's own register (the same fused
+// multiply-add).  In a loop over positions the compiler otherwise accumulates into dBx's register (v_fmac), so
+// the new h_n lands in another register than the old and the loop rotates all NS of them with moves each
+// position.  dA comes from v_exp_f32, a transcendental: the hardware needs one wait state before a VALU
+// instruction reads a transcendental's result, which the compiler inserts before its own instructions but not
+// before inline assembly, hence the s_nop 0 (without it the v_fma_f32 reads a stale dA).  (Pairs of updates in
+// one block with the exponentials two instructions ahead, and exponentials computed 4, 8 or 16 states ahead,
+// measured 2-4% slower in the compress scan at d_model 512.)
+template <int NS, int R, bool INPLACE = false>
 __device__ __forceinline__ float scan_update(const float* row, float dt, const float (&a)[NS], float Dc, float x, float z,
                                              float (&h)[NS]) {
     float y = 0.0f;
@@ -277,16 +285,17 @@ __device__ __forceinline__ float scan_update(const float* row, float dt, const f
     for (int n = 0; n < NS; ++n) {
         const float dA = __builtin_amdgcn_exp2f(dt * a[n]);  // v_exp_f32
         const float dBx = row[R + n] * dtx;
-        h[n] = __builtin_fmaf(dA, h[n], dBx);
+        if constexpr (INPLACE) __asm__("s_nop 0\n\tv_fma_f32 %0, %1, %0, %2" : "+v"(h[n]) : "v"(dA), "v"(dBx));
+        else h[n] = __builtin_fmaf(dA, h[n], dBx);
         y = __builtin_fmaf(h[n], row[R + NS + n], y);
     }
     y = __builtin_fmaf(Dc, x, y);
     return y * hw_silu(z);
 }
-template <int NS, int R>
+template <int NS, int R, bool INPLACE = false>
 __device__ __forceinline__ float scan_position(const float* row, const float (&wr)[R], float bdt, const float (&a)[NS],
                                                float Dc, float x, float z, float (&h)[NS]) {
-    return scan_update<NS, R>(row, scan_dt<R>(row, wr, bdt), a, Dc, x, z, h);
+    return scan_update<NS, R, INPLACE>(row, scan_dt<R>(row, wr, bdt), a, Dc, x, z, h);
 }
 
 // Logits of one lane (a V-wide row) as held by one wavefront: lane j gets elements 4j .. 4j + 3 (0 beyond V).
