@@ -365,7 +365,8 @@ def codec_pass(lib, eng, X, lens, lens_h, chunk: int, reps: int, warm: int):
         if i >= warm:
             tcs.append(t1 - t0)
             tds.append(t2 - t1)
-    return float(np.mean(tcs)), float(np.mean(tds)), 4 * int(nw.sum().item()), lanes_equal(out, X, lens_h)
+    mean = lambda v: float(np.mean(v)) if v else 0.0
+    return mean(tcs), mean(tds), 4 * int(nw.sum().item()), lanes_equal(out, X, lens_h)
 
 
 def read_profile(lib, eng) -> dict:
@@ -534,25 +535,43 @@ def config4_data(n_chunks: int, chunk: int, take: int, seed: int = 1):
     return np.ascontiguousarray(flat[:, :take])
 
 
-def config4_extra(lib, lanes: int, take: int) -> dict:
+def config4_extra(lib, lanes: int, take: int, wave: int = 0, warm_len: int = 0) -> dict:
     """d512 x 16 layers, bf16 weights (fp32 state, fp32 quantiser path), seed 1, `lanes` chunks
-    of the 256 MiB mixed-record payload (chunks_count = lanes), each cut to its first `take` bytes; one
-    warm-up and one timed compress + decompress.  Rooflines: compress against the dense bf16 MFMA peak with
-    the model's multiply-adds (the bf16w mode issues two bf16 products per multiply-add: activation hi and
-    lo parts), decompress against HBM with the recurrent state plus the bf16 weights once per step."""
+    of the 256 MiB mixed-record payload (chunks_count = lanes), each cut to its first `take` bytes (the whole
+    chunk when take = 256 MiB / lanes), coded in waves of `wave` lanes (all of them by default) on one context;
+    one untimed warm-up pass over the first `warm_len` bytes (default: take) of the first wave's chunks, then
+    one timed compress + decompress per wave, summed.  Rooflines: compress against the dense bf16 MFMA peak
+    with the model's multiply-adds (the bf16w mode issues two bf16 products per multiply-add: activation hi
+    and lo parts), decompress against HBM with the recurrent state plus the bf16 weights once per step."""
+    import numpy as np
     import torch
 
     from boa_amd import weights as W
     import model as M
 
+    wave = wave or lanes
+    warm_len = min(warm_len or take, take)
+    if lanes % wave:
+        raise ValueError(f"configs[4]: {lanes} chunks do not split into waves of {wave}")
     cfg = W.Cfg(d_model=512, n_layers=16)
     chunk = (256 << 20) // lanes
     data = config4_data(lanes, chunk, take)
-    X = torch.from_numpy(data).cuda()
-    ls = [take] * lanes
+    eng = M._Engine(W.seeded_blob(cfg, 1), cfg, wave, 64, precision="bf16w")
+    lw = [warm_len] * wave
+    Xw = torch.from_numpy(np.ascontiguousarray(data[:wave, :warm_len])).cuda()
+    codec_pass(lib, eng, Xw, torch.tensor(lw, dtype=torch.int32, device="cuda"), lw, warm_len, reps=0, warm=1)
+    del Xw
+    ls = [take] * wave
     lens = torch.tensor(ls, dtype=torch.int32, device="cuda")
-    eng = M._Engine(W.seeded_blob(cfg, 1), cfg, lanes, 64, precision="bf16w")
-    tc, td, cb, ok = codec_pass(lib, eng, X, lens, ls, take, reps=1, warm=1)
+    tc = td = 0.0
+    cb, ok = 0, True
+    for w in range(lanes // wave):
+        X = torch.from_numpy(np.ascontiguousarray(data[w * wave:(w + 1) * wave])).cuda()
+        tcw, tdw, cbw, okw = codec_pass(lib, eng, X, lens, ls, take, reps=1, warm=0)
+        if lanes != wave:
+            log(f"[bench] configs[4] wave {w}: compress {tcw:.2f}s decompress {tdw:.2f}s round trip {okw}")
+        tc, td, cb, ok = tc + tcw, td + tdw, cb + cbw, ok and okw
+        del X
     del eng
     nb = lanes * take
     macs = model_macs_per_token(512, 16)
@@ -561,7 +580,8 @@ def config4_extra(lib, lanes: int, take: int) -> dict:
     step_bytes = lanes * decode_state_bytes(512, 16) + 2.0 * macs
     return {
         "workload": (f"configs[4]: d512x16L bf16 weights seed 1, {lanes} chunks of the 256 MiB int16/float32 "
-                     f"record payload, first {take} B of each chunk; one warm-up and one timed pass"),
+                     f"record payload, first {take} B of each chunk, in waves of {wave} lanes; one warm-up pass "
+                     f"over the first {warm_len} B, then one timed pass"),
         "compress_MBps": nb / tc / 1e6, "decompress_MBps": nb / td / 1e6, "decompress_step_ms": step_s * 1e3,
         "compressed_bytes": cb, "round_trip_ok": ok,
         "roofline_compress": {"bound": "mfma", "achieved": flops / tc / 1e12, "peak": PEAK_BF16_MFMA_TFLOPS,
@@ -605,6 +625,10 @@ def main():
     ap.add_argument("--c4-lanes", type=int, default=16384, help="chunks (= lanes) of the configs[4] extra")
     ap.add_argument("--c4-len", type=int, default=257,
                     help="bytes per chunk of the configs[4] extra (257: 256 coded positions, four whole tiles)")
+    ap.add_argument("--c4-wave", type=int, default=0,
+                    help="lanes per wave of the configs[4] run (default: all chunks in one wave)")
+    ap.add_argument("--c4-warm-len", type=int, default=0,
+                    help="bytes per chunk of the configs[4] warm-up pass (default: --c4-len)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy 3 times (PMC byte-counter calibration)")
     args = ap.parse_args()
@@ -635,7 +659,7 @@ def main():
         return
     if args.workload == "config4":
         print(json.dumps({"metric": "configs[4] input MB/s compress, decompress, d512x16L bf16 weights, 1 GPU",
-                          **config4_extra(N.lib(), args.c4_lanes, args.c4_len)}))
+                          **config4_extra(N.lib(), args.c4_lanes, args.c4_len, args.c4_wave, args.c4_warm_len)}))
         return
     lib = N.lib()
     dev = torch.device("cuda")
