@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the BoaConstrictor batched compress/decompress hot path on one MI355X.
 
-Workload (BASELINE.json configs[2] + configs[3]): d_model 256 x 8 Mamba layers, fp32, seeded random weights
+Workload (the benchmark's configs[2] + configs[3]): d_model 256 x 8 Mamba layers, fp32, seeded random weights
 (seed 0); 64 MiB of little-endian float32 records (per record 4 log-normal(mu=1, sigma=1.5) energies,
 3 N(0,1) coordinates, 1 uniform int32 id; numpy default_rng(0)); chunks_count 4096 -> 4096 chunks of
 16384 bytes.  One step = compress the whole payload (model parallel in time + fused range coding + device

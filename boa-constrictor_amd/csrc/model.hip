@@ -1806,16 +1806,19 @@ static int launch_xproj(const float* xs, int64_t M, int di, const uint16_t* Wh, 
 }
 
 // ================================================================================================
-// Selective scan, fused with dt_proj + softplus, the D skip and the SiLU(z) gate (App. A of the mixer):
+// Selective scan, fused with dt_proj + softplus, the D skip and the SiLU(z) gate (the Mamba mixer's step,
+// reference portability_solved_cpp/mamba_kernels.cu:264-347 and its chunked form :396-444):
 //   dt = softplus(W_dt . dr + b_dt)                  (torch threshold 20)
 //   h_n <- exp(dt * A_n) * h_n + B_n * (dt * x)      A = -exp(A_log), precomputed as A * log2(e) so the
 //                                                    16 exponentials per position are exp2 (v_exp_f32)
 //   y = sum_n h_n * C_n + D * x ;  y <- y * SiLU(z)
 // One thread per (lane, channel), h[16] in registers across the Tc positions.  The [dr | B | C] row of a
 // position is uniform across the workgroup and read-only here, so the compiler reads it with scalar loads
-// into SGPRs (3 x 16 dwords per position): no LDS staging, no per-position LDS reads, and 77 VGPRs, which
-// gives 6 waves per SIMD instead of 5 (the scan is latency-bound at that occupancy: 346 -> 316 ms per
-// 16 MiB).  State [lane][di][NS] in HBM between launches.  y overwrites x in place.
+// into SGPRs (3 x 16 dwords per position): no LDS staging, no per-position LDS reads, and 76 VGPRs at
+// d_model 256 with fp32 output, which gives 6 waves per SIMD instead of 5 (the scan is latency-bound at that
+// occupancy: 346 -> 316 ms per 16 MiB).  x and z of the next two positions are in flight while one computes
+// (a three-slot register ring), and the state update writes each h_n over its own register (scan_update's
+// INPLACE form).  State [lane][di][NS] in HBM between launches.  y overwrites x in place.
 // The per-position arithmetic is scan_position (shared with the fused decompress-step kernel).
 
 template <int NS, int R>
