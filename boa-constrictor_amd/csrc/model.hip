@@ -1067,18 +1067,21 @@ __global__ void __launch_bounds__(512, 4) k_ffn(const float* __restrict__ mm, co
 // ================================================================================================
 // The same feed-forward half for d_model 512 (d_ff 2048; configs[4]'s shape):
 //   x <- x + FF2(GELU(FF1(LN2(mm))))
-// A workgroup of 512 threads owns 64 rows (one workgroup per CU: the LN2 operand is 128 KB).  Per 64-wide chunk
-// of the hidden layer: FF1 (+bias, GELU, split) into LDS, then FF2 accumulates the chunk into registers, so the
-// hidden activations never leave the chip.  The arithmetic of every value is that of the layer-by-layer path
+// A workgroup of 512 threads owns 64 rows (one workgroup per CU: the LN2 operand is 128 KB).  Per chunk of the
+// hidden layer (64 units wide, 128 with bf16 weights): FF1 (+bias, GELU, split) into LDS, then FF2 accumulates
+// the chunk into registers, so the hidden activations never leave the chip.  The arithmetic of every value is that of the layer-by-layer path
 // (ln_stats_row / ln_apply / split2; FF1 outputs accumulate their 16 K steps in ascending order through
 // mfma_split_step_t, then epi_value<GELU>; FF2 outputs accumulate all 64 K steps in ascending order, chunk by
 // chunk, then x + epi_value<RESID>), so rows equal those of the GEMM kernels bit for bit.  Used by the compress
 // tiles (64 positions of one lane) and by the per-layer decode step (64 lanes of one position).
-//   FF1: wave w computes rows 32 (w & 1) .. + 31 x hidden units 16 (w >> 1) .. + 15 of the chunk, the W1 block as
-//        the MFMA A operand (a lane's 4 outputs are 4 consecutive hidden units, one 8-byte store per part).
+//   FF1: wave w computes rows 32 (w & 1) .. + 31 x FG fragments of 16 hidden units of the chunk (fragments
+//        FG (w >> 1) ..; FG = ffn_groups), the W1 block as the MFMA A operand (a lane's 4 outputs are 4
+//        consecutive hidden units, one 8-byte store per part).  With bf16 weights the LN2 operand fragments of the
+//        next K step are read before the current step's MFMAs, with scheduling fences around each step (without
+//        them the compiler moves each MFMA up to its own operand read, and every MFMA waits for LDS).
 //   FF2: wave w owns outputs 64 w .. + 63 (4 fragments) of all 64 rows: 16 accumulators.
-// Per chunk a wave uses 24 weight blocks (16 of W1, then 8 of W2) through a ring of R register slots in use
-// order, running on into the next chunk, so R blocks are always in flight.
+// Per chunk a wave uses 24 FG weight blocks (16 FG of W1, then 8 FG of W2) through a ring of R register slots in
+// use order, running on into the next chunk, so R blocks are always in flight.
 namespace ffn5 {
 constexpr int BM = 64, D = 512, DF = 2048, HC = 64;
 // 16-byte chunks XOR-swizzled by row (low 4 bits of the chunk index), so 16-row fragment reads spread over banks
