@@ -515,9 +515,22 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
                     const f32x4 q = r == 0 ? h_first[n / 4] : buf_ld4(sr, h_off(r, n, cq));
                     h[n] = q.x; h[n + 1] = q.y; h[n + 2] = q.z; h[n + 3] = q.w;
                 }
+                // the row's [dr | B | C] (uniform across the workgroup) into registers, all 12 reads issued together:
+                // read where they are used, each waited for its own LDS round trip
+                float dbc[FW];
+                // the rows' LDS base in a register (opaque zero), so the 12 reads take immediate offsets instead of a
+                // constant address materialised for each
+                int zb = 0;
+                __asm__ volatile("" : "+v"(zb));
+                const float* rowp = sDbc + zb + r * FW;
+#pragma unroll
+                for (int i = 0; i < FW; i += 4) {
+                    const float4 v = *reinterpret_cast<const float4*>(rowp + i);
+                    dbc[i] = v.x; dbc[i + 1] = v.y; dbc[i + 2] = v.z; dbc[i + 3] = v.w;
+                }
                 __builtin_amdgcn_sched_barrier(0);
                 const float x = sX[r * LXZ + cq], z = sX[r * LXZ + FDI + cq];
-                const float y = scan_position<FNS, FR>(sDbc + r * FW, wr, bdt, av, Dc, x, z, h);
+                const float y = scan_position<FNS, FR>(dbc, wr, bdt, av, Dc, x, z, h);
                 store_op<NT, LA>(sAh, r, cq, y);
 #pragma unroll
                 for (int n = 0; n < FNS; n += 4)
