@@ -501,10 +501,17 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
         // ---- dt_proj + softplus + selective scan + D + gate (thread = channel) -> y split operand
         {
             if constexpr (!HOIST_FIRST) load_first();
-            // One lane's state at a time, loaded at the top of its row (lane 0's before x_proj; the barrier keeps
-            // the loads ahead of the row's LDS reads) and stored at its end.  The two waves of a SIMD take turns waiting on memory;
-            // loading the next lane's state one row ahead (before this row's stores) measured the same, keeping
-            // 1-3 more lanes in flight per thread 2-7% slower (more registers in a kernel at its register limit).
+            // One lane's state at a time (lane 0's loaded before x_proj), stored at the end of its row.  The two waves
+            // of a SIMD take turns waiting on memory.  In the split forms each row's state is loaded at the top of
+            // the row (the barrier keeps the loads ahead of the row's LDS reads); keeping 1-3 more lanes in flight
+            // per thread measured 2-7% slower there (more registers in a kernel at its register limit).
+            // AHEAD (fp32 form, which has the registers): the next lane's state is loaded at the top of this row,
+            // before this row's stores, so waiting for it (one in-order counter for loads and stores) does not wait
+            // for those stores (0.3% per step; the same in the split forms)
+            constexpr bool AHEAD = NT == 1;
+            f32x4 hn[FNS / 4];
+#pragma unroll
+            for (int n = 0; n < FNS; n += 4) hn[n / 4] = h_first[n / 4];
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) {
                 int cq = c;  // opaque per lane: offsets formed here, not held across the loop (see the conv)
@@ -512,8 +519,14 @@ __global__ void __launch_bounds__(NTHR) k_fused_step(FusedArgs a) {
                 float h[FNS];
 #pragma unroll
                 for (int n = 0; n < FNS; n += 4) {
-                    const f32x4 q = r == 0 ? h_first[n / 4] : buf_ld4(sr, h_off(r, n, cq));
+                    const f32x4 q = AHEAD ? hn[n / 4] : (r == 0 ? h_first[n / 4] : buf_ld4(sr, h_off(r, n, cq)));
                     h[n] = q.x; h[n + 1] = q.y; h[n + 2] = q.z; h[n + 3] = q.w;
+                }
+                if constexpr (AHEAD) {
+                    if (r + 1 < ROWS) {
+#pragma unroll
+                        for (int n = 0; n < FNS; n += 4) hn[n / 4] = buf_ld4(sr, h_off(r + 1, n, cq));
+                    }
                 }
                 // the row's [dr | B | C] (uniform across the workgroup) into registers, all 12 reads issued together:
                 // read where they are used, each waited for its own LDS round trip
