@@ -350,15 +350,15 @@ def test_wave_lanes_from_device_memory(gpu):
 
 @pytest.mark.parametrize("precision", ["f32", "bf16x3"])
 def test_compressed_size_vs_oracle_config2(gpu, ora, precision):
-    """configs[2]'s own model (d256 x 8 layers, seed 0) and data (float32 records, the first 32 of its 4096
-    chunks, first 1024 B of each) in the default f32 mode and in bf16x3: compressed size within 0.5% of the
-    reference protocol run on the CPU oracle (fp32 model -> torch.softmax -> Q2 at P = 24 -> coder), and the
-    round trip byte-exact."""
+    """configs[2]'s own model (d256 x 8 layers, seed 0) and data (float32 records: in the default f32 mode the
+    first 256 of its 4096 chunks, first 2048 B of each, 1/128 of the payload; in bf16x3 the first 32 chunks x
+    1024 B): compressed size within 0.5% of the reference protocol run on the CPU oracle (fp32 model ->
+    torch.softmax -> Q2 at P = 24 -> coder), and the round trip byte-exact."""
     import codec
     from bench import synth_records
     import model as M
 
-    lanes, L = 32, 1024
+    lanes, L = (256, 2048) if precision == "f32" else (32, 1024)
     m, blob = _model(8, seed=0)
     assert M.DEFAULT_PRECISION == "f32" or "BOA_PRECISION" in os.environ
     m.precision = precision
