@@ -7,6 +7,7 @@
 - Teacher-forced logits of configs[2]'s model and records (d256 x 8 layers, seed 0) over 2048 positions, and
   of configs[4]'s model (d512 x 16 layers, bf16 weights, seed 1) over 512 positions, against the oracle at
   every position: the recurrent state's error must not grow past the bar deep into a chunk.
+- configs[4]'s compressed size within 0.5% of the oracle pipeline's on 8 chunks x 1024 B (same bf16 weights).
 
 Tolerance (floating point), per position t: max |logits_gpu[:, t] - logits_ref[:, t]| <= 1e-4 *
 max |logits_ref[:, t]| (the north-star bar "logits match the reference's fp32 Mamba step within 1e-4
@@ -123,5 +124,30 @@ def test_config0_full_size_round_trip_and_size(gpu, ora, precision):
     ref_words = sum(len(O.encode_probs_q2(24, probs[b], X[b, 1:].numpy().astype(np.int32))) for b in range(lanes))
     gpu_words = int(snw.sum())
     print(f"configs[0] sample {lanes}x{L}: gpu words {gpu_words}  oracle words {ref_words}", flush=True)
+    assert abs(gpu_words - ref_words) <= 0.005 * ref_words
+    m.release_engines()
+
+
+def test_config4_compressed_size_vs_oracle(gpu, ora):
+    """configs[4]'s model (d512 x 16 layers, bf16 weights, seed 1) on 8 chunks of its int16 / float32 records x
+    their first 1024 B: byte-exact round trip, and the GPU's compressed size within 0.5% of the reference
+    protocol run on the CPU oracle with the same bf16-rounded weights (fp32 model -> torch.softmax -> Q2 at
+    P = 24 -> coder)."""
+    import codec
+    from bench import config4_data
+    from oracle import ora as O
+
+    m, ref = _models(512, 16, 1, "bf16w")
+    lanes, L = 8, 1024
+    data = np.ascontiguousarray(config4_data(lanes, 16384, L))
+    chunks = [data[i] for i in range(lanes)]
+    payload, nw, fb, Ls = codec.compress_payload(m, chunks)
+    out = codec.decompress_payload(m, payload, nw, Ls, fb)
+    assert np.array_equal(out, data)
+    X = torch.from_numpy(data.astype(np.int64))
+    probs = torch.softmax(ref.forward(X[:, :-1]), dim=-1).to(torch.float32).numpy()
+    ref_words = sum(len(O.encode_probs_q2(24, probs[b], X[b, 1:].numpy().astype(np.int32))) for b in range(lanes))
+    gpu_words = int(nw.sum())
+    print(f"configs[4] sample {lanes}x{L}: gpu words {gpu_words}  oracle words {ref_words}", flush=True)
     assert abs(gpu_words - ref_words) <= 0.005 * ref_words
     m.release_engines()
