@@ -182,11 +182,15 @@ class BoaFile:
         fb_at = at + len(self.IDX)
         first = list(blob[fb_at:fb_at + n])
         fields = _uvarints(blob, fb_at + n, len(blob) - _CRC.size, 2 * n)
-        starts = np.cumsum(fields[:n])
-        sizes = fields[n:]
+        deltas, sizes = fields[:n], fields[n:]
+        starts = np.cumsum(deltas)
         room = at - body
-        if n and (int((starts + sizes).max()) > room or bool((sizes & 3).any())):
-            raise ValueError("BOA2 payload out of range")  # boa.cpp:240's check; the Python reader has none
+        # boa.cpp:240's check (the Python reader has none): every stream inside the payload, in whole words.  With
+        # each delta at most the payload's size, a running offset that wraps 2^64 shows as a decrease; with the
+        # last (largest) offset inside the payload, start + size cannot wrap either.
+        if n and (int(deltas.max()) > room or bool((starts[1:] < starts[:-1]).any()) or int(starts[-1]) > room
+                  or int(sizes.max()) > room or int((starts + sizes).max()) > room or bool((sizes & 3).any())):
+            raise ValueError("BOA2 payload out of range")
         view = memoryview(blob)[body:at]
         self.compressed_data = [bytes(view[s:s + z]) for s, z in zip(starts.tolist(), sizes.tolist())]
         self.first_bytes = first

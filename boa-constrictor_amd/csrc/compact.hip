@@ -39,8 +39,16 @@ constexpr int kScanBlock = kScanBlockLanes;
 constexpr int kMaxScanBlocks = kStaticScanBlocks;  // also the smallest allocation of boa_compact's scratch
 constexpr int kMaxDevices = 64;
 
-__device__ __forceinline__ int64_t lane_words(const int32_t* nwords, int n, int i) {
-    return i < n ? (int64_t)max(nwords[i], 0) : (int64_t)0;
+// A lane's word count must lie in [0, pitch].  An invalid one counts as 0 words and marks its scan workgroup's
+// partial with kBadBlock, which the one-workgroup scan turns into a negative total: the host then reports the
+// error and launches no gather (which would read past the lane's row).
+constexpr int64_t kBadBlock = -1;
+
+__device__ __forceinline__ int64_t lane_words(const int32_t* nwords, int n, int64_t pitch, int i, int& bad) {
+    if (i >= n) return 0;
+    const int32_t w = nwords[i];
+    bad = (w < 0 || w > pitch) ? 1 : 0;
+    return bad ? (int64_t)0 : (int64_t)w;
 }
 
 // Inclusive prefix sum over a 1024-thread workgroup (16 wavefronts): wavefront shuffles, then the 16
@@ -67,40 +75,49 @@ __device__ __forceinline__ int64_t block_incl_scan(int64_t v, int64_t* sw) {
     return wave ? v + sw[wave - 1] : v;
 }
 
-// Kernel 1: sums[w] = words of lanes [1024 w, 1024 w + 1024).
-__global__ void __launch_bounds__(kScanBlock) k_block_sums(const int32_t* __restrict__ nwords, int n,
+// Kernel 1: sums[w] = words of lanes [1024 w, 1024 w + 1024), or kBadBlock if one of them has an invalid count.
+__global__ void __launch_bounds__(kScanBlock) k_block_sums(const int32_t* __restrict__ nwords, int n, int64_t pitch,
                                                           int64_t* __restrict__ sums) {
     __shared__ int64_t sw[kScanBlock / 64];
     const int i = blockIdx.x * kScanBlock + threadIdx.x;
-    const int64_t incl = block_incl_scan(lane_words(nwords, n, i), sw);
-    if (threadIdx.x == kScanBlock - 1) sums[blockIdx.x] = incl;
+    int bad = 0;
+    const int64_t incl = block_incl_scan(lane_words(nwords, n, pitch, i, bad), sw);
+    const int any_bad = __syncthreads_or(bad);
+    if (threadIdx.x == kScanBlock - 1) sums[blockIdx.x] = any_bad ? kBadBlock : incl;
 }
 
-// Kernel 2 (one workgroup): sums[0..nb) -> exclusive prefix sums in place; *total = their sum.  Each thread
-// takes a contiguous run of ceil(nb / 1024) entries.
+// Kernel 2 (one workgroup): sums[0..nb) -> exclusive prefix sums in place; *total = their sum, or kBadBlock if
+// any partial is.  Each thread takes a contiguous run of ceil(nb / 1024) entries.
 __global__ void __launch_bounds__(kScanBlock) k_scan_block_sums(int64_t* __restrict__ sums, int nb,
                                                                int64_t* __restrict__ total) {
     __shared__ int64_t sw[kScanBlock / 64];
     const int per = (nb + kScanBlock - 1) / kScanBlock;
     const int lo = threadIdx.x * per, hi = min(nb, lo + per);
     int64_t s = 0;
-    for (int i = lo; i < hi; ++i) s += sums[i];
+    int bad = 0;
+    for (int i = lo; i < hi; ++i) {
+        const int64_t v = sums[i];
+        bad |= v < 0 ? 1 : 0;
+        s += v;
+    }
+    const int any_bad = __syncthreads_or(bad);
     int64_t run = block_incl_scan(s, sw) - s;
     for (int i = lo; i < hi; ++i) {
         const int64_t v = sums[i];
         sums[i] = run;
         run += v;
     }
-    if (threadIdx.x == kScanBlock - 1) *total = run;
+    if (threadIdx.x == kScanBlock - 1) *total = any_bad ? kBadBlock : run;
 }
 
-// Kernel 3: off[i] = exclusive prefix of the words of lanes < i.
-__global__ void __launch_bounds__(kScanBlock) k_lane_offsets(const int32_t* __restrict__ nwords, int n,
+// Kernel 3: off[i] = exclusive prefix of the words of lanes < i (meaningless when the total is kBadBlock).
+__global__ void __launch_bounds__(kScanBlock) k_lane_offsets(const int32_t* __restrict__ nwords, int n, int64_t pitch,
                                                             const int64_t* __restrict__ sums,
                                                             int64_t* __restrict__ off) {
     __shared__ int64_t sw[kScanBlock / 64];
     const int i = blockIdx.x * kScanBlock + threadIdx.x;
-    const int64_t v = lane_words(nwords, n, i);
+    int bad = 0;
+    const int64_t v = lane_words(nwords, n, pitch, i, bad);
     const int64_t incl = block_incl_scan(v, sw);
     if (i < n) off[i] = sums[blockIdx.x] + incl - v;
 }
@@ -111,7 +128,7 @@ __global__ void __launch_bounds__(256) k_gather_words(const uint32_t* __restrict
                                                      const int64_t* __restrict__ off,
                                                      uint32_t* __restrict__ payload) {
     const int b = blockIdx.x;
-    const int32_t nw = max(nwords[b], 0);
+    const int64_t nw = min((int64_t)max(nwords[b], 0), pitch);  // counts are checked before this launch
     const uint32_t* src = words + (int64_t)b * pitch;
     uint32_t* dst = payload + off[b];
     for (int i = threadIdx.x; i < nw; i += blockDim.x) dst[i] = src[i];
@@ -125,13 +142,19 @@ int compact_with(const char* who, int64_t* sc, const uint32_t* d_words, int64_t 
                  int32_t lanes, int64_t* d_word_off, uint32_t* d_payload, int64_t payload_cap, int64_t* h_total,
                  hipStream_t s) {
     const int nb = scan_blocks(lanes);
-    hipLaunchKernelGGL(k_block_sums, dim3(nb), dim3(kScanBlock), 0, s, d_nwords, lanes, sc + 1);
+    hipLaunchKernelGGL(k_block_sums, dim3(nb), dim3(kScanBlock), 0, s, d_nwords, lanes, pitch_words, sc + 1);
     hipLaunchKernelGGL(k_scan_block_sums, dim3(1), dim3(kScanBlock), 0, s, sc + 1, nb, sc);
-    hipLaunchKernelGGL(k_lane_offsets, dim3(nb), dim3(kScanBlock), 0, s, d_nwords, lanes, sc + 1, d_word_off);
+    hipLaunchKernelGGL(k_lane_offsets, dim3(nb), dim3(kScanBlock), 0, s, d_nwords, lanes, pitch_words, sc + 1,
+                       d_word_off);
     BOA_HIP_TRY(hipGetLastError());
     int64_t total = 0;
     BOA_HIP_TRY(hipMemcpyAsync(&total, sc, sizeof(int64_t), hipMemcpyDeviceToHost, s));
     BOA_HIP_TRY(hipStreamSynchronize(s));
+    if (total < 0) {
+        *h_total = 0;
+        return boa_fail(BOA_ERR_ARG, "%s: a lane's word count lies outside [0, pitch_words = %lld]", who,
+                        (long long)pitch_words);
+    }
     *h_total = total;
     if (total > payload_cap)
         return boa_fail(BOA_ERR_OVERFLOW, "%s: payload needs %lld words, capacity %lld", who, (long long)total,
@@ -166,7 +189,7 @@ int current_device(const char* who, int* dev) {
 extern "C" int boa_compact(const uint32_t* d_words, int64_t pitch_words, const int32_t* d_nwords, int32_t lanes,
                            int64_t* d_word_off, uint32_t* d_payload, int64_t payload_cap, int64_t* h_total_words,
                            void* stream) {
-    if (!d_words || !d_nwords || !d_word_off || lanes < 0 || !h_total_words)
+    if (!d_words || !d_nwords || !d_word_off || lanes < 0 || pitch_words < 0 || !h_total_words)
         return boa_fail(BOA_ERR_ARG, "boa_compact: bad arguments");
     *h_total_words = 0;
     if (lanes == 0) return BOA_OK;
@@ -202,7 +225,7 @@ extern "C" int boa_compact(const uint32_t* d_words, int64_t pitch_words, const i
 extern "C" int boa_compact_noalloc(const uint32_t* d_words, int64_t pitch_words, const int32_t* d_nwords,
                                    int32_t lanes, int64_t* d_word_off, uint32_t* d_payload, int64_t payload_cap,
                                    int64_t* h_total_words, void* stream) {
-    if (!d_words || !d_nwords || !d_word_off || lanes < 0 || !h_total_words)
+    if (!d_words || !d_nwords || !d_word_off || lanes < 0 || pitch_words < 0 || !h_total_words)
         return boa_fail(BOA_ERR_ARG, "boa_compact_noalloc: bad arguments");
     *h_total_words = 0;
     if (lanes > BOA_COMPACT_NOALLOC_MAX_LANES)

@@ -143,6 +143,8 @@ int boa_xq_cdf(const float* d_logits, int64_t rows, int32_t vocab, int32_t preci
 
 /* Bitstream compaction: exclusive prefix sum of d_nwords into d_word_off (int64 [lanes]) and a gather of
  * each lane's words from the pitched buffer into the contiguous d_payload (capacity payload_cap words).
+ * Every d_nwords[i] must lie in [0, pitch_words]: otherwise BOA_ERR_ARG, with nothing gathered (the check
+ * runs on the device, in the scan).
  * *h_total_words receives the total; this call synchronizes the stream.  The scan's partial sums live in a
  * buffer the library allocates on the first call per device and stream (and enlarges for a larger wave).
  * Replaces the per-lane D2H copy of the full pitch (gpu_range_coder.py:278-292; boa.cpp:388-395).      */

@@ -94,6 +94,39 @@ def test_reader_rejects_out_of_range_payload(tmp_path):
         boa.BoaFile(str(p), object())._read_file()
 
 
+def _write_boa2_index(path, payload, first, deltas, sizes):
+    """A BOA2 file whose index holds the given offset deltas and stream sizes as they are (any values)."""
+    import boa
+
+    with open(path, "wb") as f:
+        f.write(b"BOA2" + struct.pack("<IIQIII", 1, 0, 100, 50, len(first), 50) + struct.pack("<B", 0))
+        f.write(payload)
+        idx = bytearray(b"IDX1") + bytes(first)
+        for v in list(deltas) + list(sizes):
+            idx += boa.uvarint_encode(v)
+        f.write(idx + struct.pack("<I", zlib.crc32(idx) & 0xFFFFFFFF))
+
+
+def test_reader_rejects_wrapping_offsets(tmp_path):
+    """Offset deltas whose running sum wraps 2^64 (stream 0 at 2^64 - 4, stream 1 back at 0) are rejected, as are
+    a running offset past the payload and a single delta past it; a well-formed index of the same payload reads."""
+    import boa
+
+    payload = np.arange(3, dtype="<u4").tobytes()  # 12 bytes
+    p = tmp_path / "w.boa"
+    bad = [([(1 << 64) - 4, 4], [8, 4]),   # starts [2^64 - 4, 0]: each start + size wraps below 12
+           ([4, 12], [4, 0]),              # starts [4, 16]: stream 1 starts past the payload
+           ([13, 0], [0, 0])]              # one delta past the payload
+    for deltas, sizes in bad:
+        _write_boa2_index(p, payload, [1, 2], deltas, sizes)
+        with pytest.raises(ValueError, match="out of range"):
+            boa.BoaFile(str(p), object())._read_file()
+    _write_boa2_index(p, payload, [1, 2], [0, 4], [4, 8])
+    f = boa.BoaFile(str(p), object())
+    f._read_file()
+    assert f.compressed_data == [payload[:4], payload[4:]]
+
+
 def test_chunking_formula():
     import boa
 

@@ -309,6 +309,40 @@ def test_range_coder_batch_errors(gpu):
         b.load_compressed_list([np.zeros(5, np.uint32)] * N)
 
 
+@pytest.mark.parametrize("bad_lane,bad_count", [(1500, 17), (7, -3), (2999, 17)])
+def test_compaction_rejects_counts_outside_pitch(gpu, bad_lane, bad_count):
+    """A lane's word count outside [0, pitch] is reported as an argument error and nothing is gathered (the check
+    runs in the device scan, in whichever scan workgroup holds the lane).  The words buffer has a spare row and the
+    capacity covers the stated counts, so nothing would be touched out of bounds even without the check."""
+    from boa_amd import _native as N
+
+    lanes, pitch = 3000, 16
+    rng = np.random.default_rng(12)
+    nw = rng.integers(0, pitch + 1, lanes).astype(np.int32)
+    nw[bad_lane] = bad_count
+    words = rng.integers(0, 1 << 31, (lanes + 1, pitch)).astype(np.int32)
+    d_words, d_nw = _dev(words), _dev(nw)
+    d_off = torch.empty(lanes, dtype=torch.int64, device="cuda")
+    cap = int(np.clip(nw, 0, None).astype(np.int64).sum())
+    d_pl = torch.full((cap,), 7, dtype=torch.int32, device="cuda")
+    got = ctypes.c_int64(-1)
+    rc = gpu.boa_compact(N.ptr(d_words), pitch, N.ptr(d_nw), lanes, N.ptr(d_off), N.ptr(d_pl), cap,
+                         ctypes.byref(got), N.stream_ptr())
+    assert rc == N.BOA_ERR_ARG and b"pitch_words = 16" in gpu.boa_last_error()
+    assert got.value == 0 and bool((d_pl == 7).all())
+    # the same buffers with the count made valid compact normally (the scratch carries nothing over)
+    nw[bad_lane] = pitch
+    d_nw = _dev(nw)
+    total = int(nw.sum())
+    d_pl = torch.zeros(total, dtype=torch.int32, device="cuda")
+    N.check(gpu.boa_compact(N.ptr(d_words), pitch, N.ptr(d_nw), lanes, N.ptr(d_off), N.ptr(d_pl), total,
+                            ctypes.byref(got), N.stream_ptr()))
+    assert got.value == total
+    ref = np.concatenate([words[i, :nw[i]] for i in range(lanes)])
+    assert (d_pl.cpu().numpy() == ref).all()
+    assert (d_off.cpu().numpy() == np.concatenate([[0], np.cumsum(nw)[:-1]])).all()
+
+
 @pytest.mark.parametrize("lanes,pitch", [(1, 8), (1024, 16), (1025, 16), (3000, 64), (70000, 4)])
 def test_compaction(gpu, lanes, pitch):
     """Multi-workgroup scan (1024 lanes per workgroup) + gather vs numpy, at one and several workgroups."""

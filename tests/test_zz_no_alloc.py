@@ -1,6 +1,7 @@
 """boa_compact_noalloc (compaction with the scan scratch in a fixed device array, no allocation) gives the
-same offsets, payload and total as boa_compact, on two calls in a row, the second with fewer lanes; and
-rejects a wave beyond its static maximum before touching the GPU."""
+same offsets, payload and total as boa_compact, on two calls in a row, the second with fewer lanes; rejects a
+wave beyond its static maximum before touching the GPU; and reports a payload capacity below the total or a word
+count beyond the pitch without writing anything."""
 import ctypes
 
 import numpy as np
@@ -61,3 +62,15 @@ def test_noalloc_limits(gpu):
     rc = gpu.boa_compact_noalloc(N.ptr(d_words), 8, N.ptr(d_nw), 300, N.ptr(d_off), N.ptr(small), 4,
                                  ctypes.byref(got), N.stream_ptr())
     assert rc == N.BOA_ERR_OVERFLOW and got.value == int(nw.sum())
+    # a word count beyond the pitch is an argument error, nothing gathered; the next valid call is unaffected
+    bad = nw.copy()
+    bad[150] = 9
+    d_bad = torch.from_numpy(bad).cuda()
+    cap = int(bad.sum())
+    d_pl = torch.full((cap,), 7, dtype=torch.int32, device="cuda")
+    rc = gpu.boa_compact_noalloc(N.ptr(d_words), 8, N.ptr(d_bad), 300, N.ptr(d_off), N.ptr(d_pl), cap,
+                                 ctypes.byref(got), N.stream_ptr())
+    assert rc == N.BOA_ERR_ARG and got.value == 0 and bool((d_pl == 7).all())
+    t_ref, off_ref, pl_ref = _run(gpu, "boa_compact", nw, words, 8)
+    t_new, off_new, pl_new = _run(gpu, "boa_compact_noalloc", nw, words, 8)
+    assert t_new == t_ref and np.array_equal(off_new, off_ref) and np.array_equal(pl_new, pl_ref)
