@@ -548,6 +548,16 @@ __global__ void __launch_bounds__(256) k_ln_split(const float* __restrict__ A, i
 
 // ================================================================================================
 // Embedding gathers.  One wavefront per row; lane j copies elements 4j.. of each 256-wide slab.
+// The model input of lane b at position p of a compress pass: its byte inside the chunk, 0 past its end.  The
+// byte is read whatever the length (p < max_len <= stride for every position a compress tile covers), so the two
+// loads are independent.
+__device__ __forceinline__ int byte_token(const uint8_t* bytes, int64_t stride, const int32_t* lens, int64_t b, int p,
+                                          int V) {
+    const int raw = (int)bytes[b * stride + p];
+    const int tok = (p < lens[b]) ? raw : 0;
+    return tok < V ? tok : V - 1;  // bytes >= vocab are not codable; keep the gather in bounds
+}
+
 __global__ void __launch_bounds__(256) k_embed_bytes(const uint8_t* __restrict__ bytes, int64_t stride,
                                                     const int32_t* __restrict__ lens, int t0, int Tc,
                                                     int64_t rows, const float* __restrict__ emb, int d, int V,
@@ -557,12 +567,22 @@ __global__ void __launch_bounds__(256) k_embed_bytes(const uint8_t* __restrict__
     if (m >= rows) return;
     const int64_t b = m / Tc;
     const int t = (int)(m - b * Tc);
-    const int p = t0 + t;
-    int tok = (p < lens[b]) ? (int)bytes[b * stride + p] : 0;
-    tok = tok < V ? tok : V - 1;  // bytes >= vocab are not codable; keep the gather in bounds
+    const int tok = byte_token(bytes, stride, lens, b, t0 + t, V);
     for (int c = 4 * lane; c < d; c += 256)
         *reinterpret_cast<float4*>(x + m * d + c) = *reinterpret_cast<const float4*>(emb + (int64_t)tok * d + c);
 }
+
+// Layer 0 of a full compress tile reads its input rows straight from the embedding table in the LN1 prologue of
+// the mixer-input kernel (k_mixin, k_mixin512), which also writes them to x, the residual stream the feed-forward
+// kernel adds to; the separate embedding pass (k_embed_bytes) and its HBM round trip are skipped.  bytes null: the
+// kernel reads x as written by an embedding pass or the previous layer.
+struct EmbedIn {
+    const uint8_t* bytes = nullptr;  // the group's bytes [lanes][stride]
+    int64_t stride = 0;
+    const int32_t* lens = nullptr;   // the group's chunk lengths
+    const float* emb = nullptr;      // [V][d]
+    int t0 = 0, V = 0;               // the tile's first position; vocab
+};
 
 __global__ void __launch_bounds__(256) k_embed_tokens(const int32_t* __restrict__ tokens, int64_t tok_stride,
                                                      int t0, int Tc, int64_t rows, const float* __restrict__ emb,
@@ -1395,12 +1415,13 @@ __device__ __forceinline__ int sx_off(int r, int c) { return r * CH + ((((c >> 2
 }  // namespace mixin
 
 template <int NT>
-__global__ void __launch_bounds__(256, 2) k_mixin(const float* __restrict__ x, const float* __restrict__ ln_w,
+__global__ void __launch_bounds__(256, 2) k_mixin(float* __restrict__ x, const float* __restrict__ ln_w,
                                                  const float* __restrict__ ln_b, const uint16_t* __restrict__ Wip,
                                                  const float* __restrict__ bin, const float* __restrict__ conv_w,
                                                  const float* __restrict__ conv_b, const uint16_t* __restrict__ Wxp,
                                                  float* __restrict__ xz, float* __restrict__ xs,
-                                                 float* __restrict__ dbc, float* __restrict__ hist, int p0m3) {
+                                                 float* __restrict__ dbc, float* __restrict__ hist, int p0m3,
+                                                 EmbedIn e) {
     using namespace mixin;
     constexpr int BLK = two_part_blocks<NT>() ? 1024 : 512;
     __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * D];  // LN1 output (hi, lo)
@@ -1410,13 +1431,20 @@ __global__ void __launch_bounds__(256, 2) k_mixin(const float* __restrict__ x, c
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int64_t b = blockIdx.x, m0 = b * BM;
-    // ---- LN1
+    // ---- LN1 (layer 0 of a compress tile: of the embedding rows, which are also written to x at the end; lane q
+    //      of a wave reads the token of its row q, handed to every lane by readlane)
+    const int tokv = e.bytes ? byte_token(e.bytes, e.stride, e.lens, b, e.t0 + 16 * wave + (lane & 15), e.V) : 0;
     {
         const float4 wv = ldg_f4(G(ln_w) + 4 * lane), bv = ldg_f4(G(ln_b) + 4 * lane);
 #pragma unroll 4
         for (int q = 0; q < BM / 4; ++q) {
             const int r = 16 * wave + q;
-            const float4 u = ldg_f4(G(x) + (m0 + r) * D + 4 * lane);
+            float4 u;
+            if (e.bytes) {
+                u = ldg_f4(G(e.emb) + (int64_t)__builtin_amdgcn_readlane(tokv, q) * D + 4 * lane);
+            } else {
+                u = ldg_f4(G(x) + (m0 + r) * D + 4 * lane);
+            }
             const float v[4] = {u.x, u.y, u.z, u.w};
             float mu, rs;
             ln_stats_row<1>(v, mu, rs);
@@ -1583,6 +1611,14 @@ __global__ void __launch_bounds__(256, 2) k_mixin(const float* __restrict__ x, c
     for (int j = 0; j < 3; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) GM(dbc)[(m0 + 16 * wave + m_of + r) * FW + 16 * j + ar] = dacc[j][r];
+    // layer 0 of a compress tile: the embedding rows to x (the residual stream), gathered again from the table
+    // (L2) and stored last: stored in the prologue, the weight loads behind them waited for their completion
+    if (e.bytes) {
+#pragma unroll 4
+        for (int q = 0; q < BM / 4; ++q)
+            *reinterpret_cast<float4*>(x + (m0 + 16 * wave + q) * D + 4 * lane) =
+                ldg_f4(G(e.emb) + (int64_t)__builtin_amdgcn_readlane(tokv, q) * D + 4 * lane);
+    }
 }
 
 // The mixer's input half for d_model 512 (d_inner 1024, dt_rank 32, x_proj width 64; configs[4]'s shape), one
@@ -1602,12 +1638,13 @@ constexpr int BM = 64, D = 512, DI = 1024, CH = 64, FW = 64;
 }  // namespace mixin5
 
 template <int NT>
-__global__ void __launch_bounds__(512, 2) k_mixin512(const float* __restrict__ x, const float* __restrict__ ln_w,
+__global__ void __launch_bounds__(512, 2) k_mixin512(float* __restrict__ x, const float* __restrict__ ln_w,
                                                      const float* __restrict__ ln_b, const uint16_t* __restrict__ Wip,
                                                      const float* __restrict__ bin, const float* __restrict__ conv_w,
                                                      const float* __restrict__ conv_b, const uint16_t* __restrict__ Wxp,
                                                      float* __restrict__ xz, float* __restrict__ xs,
-                                                     float* __restrict__ dbc, float* __restrict__ hist, int p0m3) {
+                                                     float* __restrict__ dbc, float* __restrict__ hist, int p0m3,
+                                                     EmbedIn e) {
     using namespace mixin5;
     using mixin::sx_off;
     using mixin::x_off;
@@ -1619,7 +1656,9 @@ __global__ void __launch_bounds__(512, 2) k_mixin512(const float* __restrict__ x
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int64_t b = blockIdx.x, m0 = b * BM;
-    // ---- LN1: 8 rows per wave
+    // ---- LN1: 8 rows per wave (layer 0 of a compress tile: of the embedding rows, which are also written to x at
+    //      the end; lane q of a wave reads the token of its row q, handed to every lane by readlane)
+    const int tokv = e.bytes ? byte_token(e.bytes, e.stride, e.lens, b, e.t0 + 8 * wave + (lane & 7), e.V) : 0;
     {
         const float4 w0 = ldg_f4(G(ln_w) + 4 * lane), w1 = ldg_f4(G(ln_w) + 256 + 4 * lane);
         const float4 c0 = ldg_f4(G(ln_b) + 4 * lane), c1 = ldg_f4(G(ln_b) + 256 + 4 * lane);
@@ -1628,8 +1667,15 @@ __global__ void __launch_bounds__(512, 2) k_mixin512(const float* __restrict__ x
 #pragma unroll 2
         for (int q = 0; q < BM / 8; ++q) {
             const int r = 8 * wave + q;
-            const float4 u0 = ldg_f4(G(x) + (m0 + r) * D + 4 * lane);
-            const float4 u1 = ldg_f4(G(x) + (m0 + r) * D + 256 + 4 * lane);
+            float4 u0, u1;
+            if (e.bytes) {
+                const gptr<float> er = G(e.emb) + (int64_t)__builtin_amdgcn_readlane(tokv, q) * D + 4 * lane;
+                u0 = ldg_f4(er);
+                u1 = ldg_f4(er + 256);
+            } else {
+                u0 = ldg_f4(G(x) + (m0 + r) * D + 4 * lane);
+                u1 = ldg_f4(G(x) + (m0 + r) * D + 256 + 4 * lane);
+            }
             const float v[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
             float mu, rs;
             ln_stats_row<2>(v, mu, rs);
@@ -1780,6 +1826,16 @@ __global__ void __launch_bounds__(512, 2) k_mixin512(const float* __restrict__ x
     for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) GM(dbc)[(m0 + 16 * xr + m_of + r) * FW + 16 * (xf + j) + ar] = dacc[j][r];
+    // layer 0 of a compress tile: the embedding rows to x, gathered again and stored last (as in k_mixin)
+    if (e.bytes) {
+#pragma unroll 2
+        for (int q = 0; q < BM / 8; ++q) {
+            const gptr<float> er = G(e.emb) + (int64_t)__builtin_amdgcn_readlane(tokv, q) * D + 4 * lane;
+            float* xr_ = x + (m0 + 8 * wave + q) * D + 4 * lane;
+            *reinterpret_cast<float4*>(xr_) = ldg_f4(er);
+            *reinterpret_cast<float4*>(xr_ + 256) = ldg_f4(er + 256);
+        }
+    }
 }
 
 // fp32 mode: the K-block fold over the fp32 weight matrix (k_xproj_f32)
@@ -2363,6 +2419,13 @@ struct boa_ctx {
     int decode_halves = 2;
     bool ffn_outp = true;  // out_proj inside the feed-forward kernel (BOA_FFN_OUTP=0: separate GEMM)
     bool head_xq = true;   // compress tiles: head + quantiser in one kernel (BOA_HEAD_XQ=0: head GEMMs + k_encode_tile)
+    // full compress tiles: layer 0's mixer-input kernel gathers the embedding rows itself (BOA_EMBED_LN1=1) instead
+    // of the separate embedding pass.  Off by default: with it the compress pass measured 0.8% slower at d_model
+    // 256 (f32; the feed-forward kernels 4% slower beside the other lane group's kernels, the mixer kernel
+    // unchanged) and 0.3% at d_model 512 (bf16w).  emb_src is the current tile's (set only around its layer-0
+    // launch).
+    bool embed_ln1 = false;
+    EmbedIn emb_src;
     // compress in groups of the lanes on their own streams (BOA_COMPRESS_HALVES=0: one stream; BOA_COMPRESS_GROUPS:
     // 2 or 3 groups, default 2)
     bool compress_halves = true;
@@ -2791,6 +2854,7 @@ extern "C" int boa_ctx_create(const boa_model_cfg* cfg, const void* h_weights, i
     if (const char* v = getenv("BOA_DECODE_HALVES")) x->decode_halves = atoi(v) == 1 ? 1 : 2;
     if (const char* v = getenv("BOA_FFN_OUTP")) x->ffn_outp = atoi(v) != 0;
     if (const char* v = getenv("BOA_HEAD_XQ")) x->head_xq = atoi(v) != 0;
+    if (const char* v = getenv("BOA_EMBED_LN1")) x->embed_ln1 = atoi(v) != 0;
     if (const char* v = getenv("BOA_COMPRESS_HALVES")) x->compress_halves = atoi(v) != 0;
     if (const char* v = getenv("BOA_COMPRESS_GROUPS")) x->compress_groups = atoi(v) == 3 ? 3 : 2;
     if ((!x->fused && x->decode_halves == 2) || x->compress_halves) {
@@ -2884,19 +2948,50 @@ static void launch_scan(boa_ctx* x, const LayerW& w, float* ssm, int B, int Tc) 
 //   1: LN1 + in_proj;  2: conv + x_proj + scan (the state traffic);  4: out_proj + LN2 + feed-forward.
 // Where a fused compress-tile kernel (k_mixin, k_mixin512) covers LN1 through x_proj, bit 1 launches it and
 // bit 2 the scan alone.
+// Whether a layer of a Tc-position tile runs LN1 through x_proj as one mixer-input kernel: k_mixin512 (d_model
+// 512, split modes) or k_mixin (d_model 256, every mode), on full tiles with fragment-packed weights.
+static bool mixin512_layer(const boa_ctx* x, const LayerW& w, int Tc) {
+    return x->prec != BOA_PREC_F32 && x->d == mixin5::D && x->di == mixin5::DI && x->R + 2 * x->NS == mixin5::FW &&
+           Tc == mixin5::BM && w.in_w.p && w.x_w.p;
+}
+static bool mixin_layer(const boa_ctx* x, const LayerW& w, int Tc) {
+    return !mixin512_layer(x, w, Tc) && x->d == mixin::D && x->di == mixin::DI && x->R + 2 * x->NS == mixin::FW &&
+           Tc == mixin::BM && w.in_w.p && w.x_w.p;
+}
+// Whether a compress tile of Tc positions skips the embedding pass: its layer 0 gathers the rows (EmbedIn).
+static bool embed_in_mixin(const boa_ctx* x, int Tc) {
+    return x->embed_ln1 && x->L > 0 && (mixin512_layer(x, x->layers[0], Tc) || mixin_layer(x, x->layers[0], Tc));
+}
+
+// Sets the context's embedding source for one layer-0 launch sequence of a compress tile and clears it after.
+struct EmbedFromBytes {
+    boa_ctx* x;
+    EmbedFromBytes(boa_ctx* c, bool on, const uint8_t* bytes, int64_t stride, const int32_t* lens, int t0) : x(c) {
+        x->emb_src = EmbedIn{};
+        if (on) {
+            x->emb_src.bytes = bytes; x->emb_src.stride = stride; x->emb_src.lens = lens;
+            x->emb_src.emb = x->emb; x->emb_src.t0 = t0; x->emb_src.V = x->V;
+        }
+    }
+    ~EmbedFromBytes() { x->emb_src = EmbedIn{}; }
+};
+
 static int run_layer(boa_ctx* x, int l, int B, int Tc, int part = 7) {
     const LayerW& w = x->layers[l];
     const int d = x->d, di = x->di, NS = x->NS, R = x->R;
     const int64_t M = (int64_t)B * Tc;
     hipStream_t s = x->stream;
     const bool split = x->prec != BOA_PREC_F32;
+    // layer 0 of a tile whose embedding pass was skipped: the mixer-input kernel gathers the rows
+    const EmbedIn ein = (l == 0) ? x->emb_src : EmbedIn{};
+    if (ein.bytes && !((mixin512_layer(x, w, Tc) || mixin_layer(x, w, Tc)) && (part & 1)))
+        return boa_fail(BOA_ERR_STATE, "run_layer: no embedding pass for a tile without the mixer-input kernel");
     // FF hidden activations (split): two bf16 arrays in the memory of xz (dead after the scan)
     uint16_t* gh = reinterpret_cast<uint16_t*>(x->xz);
     uint16_t* gl = gh + M * 4 * d;
     int rc = 0;
     float* hist = x->conv_hist + ((int64_t)l * x->max_lanes + x->lane0) * 3 * di;
-    const bool mix5 = split && d == mixin5::D && di == mixin5::DI && R + 2 * NS == mixin5::FW && Tc == mixin5::BM &&
-                      w.in_w.p && w.x_w.p;
+    const bool mix5 = mixin512_layer(x, w, Tc);
     if (mix5 && (part & 1)) {
         // LN1 + in_proj + conv + SiLU + x_proj in one kernel per lane tile, d_model 512
         const double flops = gemm_flops(M, 2 * di, d) + gemm_flops(M, R + 2 * NS, di) + 8.0 * M * di;
@@ -2905,16 +3000,15 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc, int part = 7) {
             PROF(PC_MIXIN, flops, bytes,
                  hipLaunchKernelGGL((k_mixin512<3>), dim3((unsigned)B), dim3(512), 0, s, x->x, w.ln1_w, w.ln1_b,
                                     w.in_w.p, w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs, x->dbc, hist,
-                                    (int)(x->pos % 3)));
+                                    (int)(x->pos % 3), ein));
         else
             PROF(PC_MIXIN, flops, bytes,
                  hipLaunchKernelGGL((k_mixin512<2>), dim3((unsigned)B), dim3(512), 0, s, x->x, w.ln1_w, w.ln1_b,
                                     w.in_w.p, w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs, x->dbc, hist,
-                                    (int)(x->pos % 3)));
+                                    (int)(x->pos % 3), ein));
     }
     // (fp32 mode included: its fragment-packed weights exist at d_model 256)
-    const bool mix = !mix5 && d == mixin::D && di == mixin::DI && R + 2 * NS == mixin::FW && Tc == mixin::BM &&
-                     w.in_w.p && w.x_w.p;
+    const bool mix = mixin_layer(x, w, Tc);
     if (mix && (part & 1)) {
         // LN1 + in_proj + conv + SiLU + x_proj in one kernel per lane tile
         const double flops = gemm_flops(M, 2 * di, d) + gemm_flops(M, R + 2 * NS, di) + 8.0 * M * di;
@@ -2922,15 +3016,18 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc, int part = 7) {
         if (x->prec == BOA_PREC_F32)
             PROF(PC_MIXIN, flops, bytes,
                  hipLaunchKernelGGL((k_mixin<1>), dim3((unsigned)B), dim3(256), 0, s, x->x, w.ln1_w, w.ln1_b, w.in_w.p,
-                                    w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs, x->dbc, hist, (int)(x->pos % 3)));
+                                    w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs, x->dbc, hist, (int)(x->pos % 3),
+                                    ein));
         else if (w.in_w.l)
             PROF(PC_MIXIN, flops, bytes,
                  hipLaunchKernelGGL((k_mixin<3>), dim3((unsigned)B), dim3(256), 0, s, x->x, w.ln1_w, w.ln1_b, w.in_w.p,
-                                    w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs, x->dbc, hist, (int)(x->pos % 3)));
+                                    w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs, x->dbc, hist, (int)(x->pos % 3),
+                                    ein));
         else
             PROF(PC_MIXIN, flops, bytes,
                  hipLaunchKernelGGL((k_mixin<2>), dim3((unsigned)B), dim3(256), 0, s, x->x, w.ln1_w, w.ln1_b, w.in_w.p,
-                                    w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs, x->dbc, hist, (int)(x->pos % 3)));
+                                    w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs, x->dbc, hist, (int)(x->pos % 3),
+                                    ein));
     } else if (!mix5 && !mix) {
     // LN1 + in_proj -> xz [M][2di]
     if (part & 1) {
@@ -3326,7 +3423,8 @@ extern "C" int boa_compress(boa_ctx* x, const uint8_t* d_bytes, int64_t byte_str
         for (int g = 1; g < G; ++g) BOA_HIP_TRY(hipStreamWaitEvent(gs[g], join[0], 0));
         for (int t0 = 0; t0 < positions; t0 += x->tile_len) {
             const int Tc = std::min(x->tile_len, positions - t0);
-            for (int g = 0; g < G; ++g) {
+            const bool fuse_emb = embed_in_mixin(x, Tc);
+            for (int g = 0; g < G && !fuse_emb; ++g) {
                 LaneView v(x, (int64_t)lo[g] * x->tile_len, lo[g], gs[g]);
                 const int64_t b0 = x->lane0, rows = (int64_t)(lo[g + 1] - lo[g]) * Tc;
                 PROF(PC_EMBED, 0.0, 4.0 * rows * x->d,
@@ -3337,6 +3435,8 @@ extern "C" int boa_compress(boa_ctx* x, const uint8_t* d_bytes, int64_t byte_str
             for (int l = 0; l < L; ++l) {
                 for (int g = 0; g < G; ++g) {
                     LaneView v(x, (int64_t)lo[g] * x->tile_len, lo[g], gs[g]);
+                    const int64_t b0 = x->lane0;
+                    EmbedFromBytes eb(x, fuse_emb && l == 0, d_bytes + b0 * byte_stride, byte_stride, d_lens + b0, t0);
                     rc = run_layer(x, l, lo[g + 1] - lo[g], Tc);
                     if (rc) return rc;
                 }
@@ -3372,12 +3472,17 @@ extern "C" int boa_compress(boa_ctx* x, const uint8_t* d_bytes, int64_t byte_str
     for (int t0 = 0; !halves && t0 < positions; t0 += x->tile_len) {
         const int Tc = std::min(x->tile_len, positions - t0);
         const int64_t rows = (int64_t)lanes * Tc;
-        PROF(PC_EMBED, 0.0, 4.0 * rows * x->d,
-             hipLaunchKernelGGL(k_embed_bytes, dim3(row_blocks(rows)), dim3(256), 0, s, d_bytes, byte_stride, d_lens,
-                                t0, Tc, rows, x->emb, x->d, x->V, x->x));
+        const bool fuse_emb = embed_in_mixin(x, Tc);
+        if (!fuse_emb)
+            PROF(PC_EMBED, 0.0, 4.0 * rows * x->d,
+                 hipLaunchKernelGGL(k_embed_bytes, dim3(row_blocks(rows)), dim3(256), 0, s, d_bytes, byte_stride, d_lens,
+                                    t0, Tc, rows, x->emb, x->d, x->V, x->x));
         if (head_xq_ok(x, Tc)) {
             // layers, then head + quantiser in one kernel (logits on chip) and the sequential coder
-            for (int l = 0; l < x->L && !rc; ++l) rc = run_layer(x, l, lanes, Tc);
+            for (int l = 0; l < x->L && !rc; ++l) {
+                EmbedFromBytes eb(x, fuse_emb && l == 0, d_bytes, byte_stride, d_lens, t0);
+                rc = run_layer(x, l, lanes, Tc);
+            }
             x->pos += Tc;
             if (rc) return rc;
             uint2* lf = reinterpret_cast<uint2*>(x->logits);  // (lo, width) per position: 8 of the row's V * 4 bytes
@@ -3388,7 +3493,10 @@ extern "C" int boa_compress(boa_ctx* x, const uint8_t* d_bytes, int64_t byte_str
                                     d_words, pitch_words));
             continue;
         }
-        rc = run_model(x, lanes, Tc, x->logits);
+        {
+            EmbedFromBytes eb(x, fuse_emb, d_bytes, byte_stride, d_lens, t0);  // used by layer 0 only
+            rc = run_model(x, lanes, Tc, x->logits);
+        }
         x->pos += Tc;
         if (rc) return rc;
         PROF(PC_ENCODE, 0.0, 4.0 * rows * x->V + (double)rows,

@@ -407,6 +407,21 @@ def test_fused_compress_kernels_match_separate_kernels(gpu, d_model, precision, 
     chip, (lo, width) pairs, sequential coder) against the head GEMMs + per-lane encode kernel; BOA_FFN_OUTP:
     out_proj inside the feed-forward kernel against the separate out_proj GEMM: identical words for every chunk,
     including chunks that end inside a tile, length-1 chunks and the partial last tile; and the stream decodes."""
+    _compress_with_and_without(d_model, precision, flag)
+
+
+@pytest.mark.parametrize("groups", ["1", "2"])
+@pytest.mark.parametrize("d_model,precision", [(256, "f32"), (256, "bf16x3"), (256, "bf16w"), (512, "bf16w"),
+                                               (512, "bf16x3")])
+def test_embedding_gathered_in_ln1_matches_embedding_pass(gpu, d_model, precision, groups):
+    """BOA_EMBED_LN1: layer 0 of a full compress tile gathers its embedding rows in the mixer-input kernel's LN1
+    prologue (and writes them to x for the residual) instead of reading the rows an embedding pass wrote: identical
+    words with and without, on one stream and (groups "2": 512 lanes) on two lane groups, whose byte and length
+    pointers start at the second group's first lane; partial tiles keep the embedding pass in both runs."""
+    _compress_with_and_without(d_model, precision, "BOA_EMBED_LN1", wide=groups == "2")
+
+
+def _compress_with_and_without(d_model, precision, flag, wide=False):
     import codec
     from boa_amd import weights as W
 
@@ -415,6 +430,8 @@ def test_fused_compress_kernels_match_separate_kernels(gpu, d_model, precision, 
     m = M.BoaConstrictor(d_model, 2, 256).load_blob(W.seeded_blob(W.Cfg(d_model=d_model, n_layers=2), 5))
     m.precision = precision
     lens = [1, 2, 63, 64, 65, 66, 129, 200, 191, 130]
+    if wide:  # enough lanes for the compress groups (two streams from 512 lanes), ragged in both groups
+        lens = (lens * 52)[:512]
     chunks = [_markov(L, seed=40 + i) for i, L in enumerate(lens)]
     res = []
     for val in ("1", "0"):
