@@ -548,13 +548,10 @@ __global__ void __launch_bounds__(256) k_ln_split(const float* __restrict__ A, i
 
 // ================================================================================================
 // Embedding gathers.  One wavefront per row; lane j copies elements 4j.. of each 256-wide slab.
-// The model input of lane b at position p of a compress pass: its byte inside the chunk, 0 past its end.  The
-// byte is read whatever the length (p < max_len <= stride for every position a compress tile covers), so the two
-// loads are independent.
+// The model input of lane b at position p of a compress pass: its byte inside the chunk, 0 past its end.
 __device__ __forceinline__ int byte_token(const uint8_t* bytes, int64_t stride, const int32_t* lens, int64_t b, int p,
                                           int V) {
-    const int raw = (int)bytes[b * stride + p];
-    const int tok = (p < lens[b]) ? raw : 0;
+    const int tok = (p < lens[b]) ? (int)bytes[b * stride + p] : 0;
     return tok < V ? tok : V - 1;  // bytes >= vocab are not codable; keep the gather in bounds
 }
 
@@ -581,6 +578,7 @@ struct EmbedIn {
     int64_t stride = 0;
     const int32_t* lens = nullptr;   // the group's chunk lengths
     const float* emb = nullptr;      // [V][d]
+    float* xout = nullptr;           // x, where the gathered rows are written for the residual
     int t0 = 0, V = 0;               // the tile's first position; vocab
 };
 
@@ -1414,8 +1412,8 @@ __device__ __forceinline__ int x_off(int r, int k) { return r * CH + (((k >> 3) 
 __device__ __forceinline__ int sx_off(int r, int c) { return r * CH + ((((c >> 2) ^ r) & 15) << 2) + (c & 3); }
 }  // namespace mixin
 
-template <int NT>
-__global__ void __launch_bounds__(256, 2) k_mixin(float* __restrict__ x, const float* __restrict__ ln_w,
+template <int NT, bool EMB>
+__global__ void __launch_bounds__(256, 2) k_mixin(const float* __restrict__ x, const float* __restrict__ ln_w,
                                                  const float* __restrict__ ln_b, const uint16_t* __restrict__ Wip,
                                                  const float* __restrict__ bin, const float* __restrict__ conv_w,
                                                  const float* __restrict__ conv_b, const uint16_t* __restrict__ Wxp,
@@ -1433,18 +1431,15 @@ __global__ void __launch_bounds__(256, 2) k_mixin(float* __restrict__ x, const f
     const int64_t b = blockIdx.x, m0 = b * BM;
     // ---- LN1 (layer 0 of a compress tile: of the embedding rows, which are also written to x at the end; lane q
     //      of a wave reads the token of its row q, handed to every lane by readlane)
-    const int tokv = e.bytes ? byte_token(e.bytes, e.stride, e.lens, b, e.t0 + 16 * wave + (lane & 15), e.V) : 0;
+    const int tokv = EMB ? byte_token(e.bytes, e.stride, e.lens, b, e.t0 + 16 * wave + (lane & 15), e.V) : 0;
     {
         const float4 wv = ldg_f4(G(ln_w) + 4 * lane), bv = ldg_f4(G(ln_b) + 4 * lane);
 #pragma unroll 4
         for (int q = 0; q < BM / 4; ++q) {
             const int r = 16 * wave + q;
             float4 u;
-            if (e.bytes) {
-                u = ldg_f4(G(e.emb) + (int64_t)__builtin_amdgcn_readlane(tokv, q) * D + 4 * lane);
-            } else {
-                u = ldg_f4(G(x) + (m0 + r) * D + 4 * lane);
-            }
+            if constexpr (EMB) u = ldg_f4(G(e.emb) + (int64_t)__builtin_amdgcn_readlane(tokv, q) * D + 4 * lane);
+            else u = ldg_f4(G(x) + (m0 + r) * D + 4 * lane);
             const float v[4] = {u.x, u.y, u.z, u.w};
             float mu, rs;
             ln_stats_row<1>(v, mu, rs);
@@ -1613,10 +1608,10 @@ __global__ void __launch_bounds__(256, 2) k_mixin(float* __restrict__ x, const f
         for (int r = 0; r < 4; ++r) GM(dbc)[(m0 + 16 * wave + m_of + r) * FW + 16 * j + ar] = dacc[j][r];
     // layer 0 of a compress tile: the embedding rows to x (the residual stream), gathered again from the table
     // (L2) and stored last: stored in the prologue, the weight loads behind them waited for their completion
-    if (e.bytes) {
+    if constexpr (EMB) {
 #pragma unroll 4
         for (int q = 0; q < BM / 4; ++q)
-            *reinterpret_cast<float4*>(x + (m0 + 16 * wave + q) * D + 4 * lane) =
+            *reinterpret_cast<float4*>(e.xout + (m0 + 16 * wave + q) * D + 4 * lane) =
                 ldg_f4(G(e.emb) + (int64_t)__builtin_amdgcn_readlane(tokv, q) * D + 4 * lane);
     }
 }
@@ -1637,8 +1632,8 @@ namespace mixin5 {
 constexpr int BM = 64, D = 512, DI = 1024, CH = 64, FW = 64;
 }  // namespace mixin5
 
-template <int NT>
-__global__ void __launch_bounds__(512, 2) k_mixin512(float* __restrict__ x, const float* __restrict__ ln_w,
+template <int NT, bool EMB>
+__global__ void __launch_bounds__(512, 2) k_mixin512(const float* __restrict__ x, const float* __restrict__ ln_w,
                                                      const float* __restrict__ ln_b, const uint16_t* __restrict__ Wip,
                                                      const float* __restrict__ bin, const float* __restrict__ conv_w,
                                                      const float* __restrict__ conv_b, const uint16_t* __restrict__ Wxp,
@@ -1658,7 +1653,7 @@ __global__ void __launch_bounds__(512, 2) k_mixin512(float* __restrict__ x, cons
     const int64_t b = blockIdx.x, m0 = b * BM;
     // ---- LN1: 8 rows per wave (layer 0 of a compress tile: of the embedding rows, which are also written to x at
     //      the end; lane q of a wave reads the token of its row q, handed to every lane by readlane)
-    const int tokv = e.bytes ? byte_token(e.bytes, e.stride, e.lens, b, e.t0 + 8 * wave + (lane & 7), e.V) : 0;
+    const int tokv = EMB ? byte_token(e.bytes, e.stride, e.lens, b, e.t0 + 8 * wave + (lane & 7), e.V) : 0;
     {
         const float4 w0 = ldg_f4(G(ln_w) + 4 * lane), w1 = ldg_f4(G(ln_w) + 256 + 4 * lane);
         const float4 c0 = ldg_f4(G(ln_b) + 4 * lane), c1 = ldg_f4(G(ln_b) + 256 + 4 * lane);
@@ -1668,7 +1663,7 @@ __global__ void __launch_bounds__(512, 2) k_mixin512(float* __restrict__ x, cons
         for (int q = 0; q < BM / 8; ++q) {
             const int r = 8 * wave + q;
             float4 u0, u1;
-            if (e.bytes) {
+            if constexpr (EMB) {
                 const gptr<float> er = G(e.emb) + (int64_t)__builtin_amdgcn_readlane(tokv, q) * D + 4 * lane;
                 u0 = ldg_f4(er);
                 u1 = ldg_f4(er + 256);
@@ -1827,11 +1822,11 @@ __global__ void __launch_bounds__(512, 2) k_mixin512(float* __restrict__ x, cons
 #pragma unroll
         for (int r = 0; r < 4; ++r) GM(dbc)[(m0 + 16 * xr + m_of + r) * FW + 16 * (xf + j) + ar] = dacc[j][r];
     // layer 0 of a compress tile: the embedding rows to x, gathered again and stored last (as in k_mixin)
-    if (e.bytes) {
+    if constexpr (EMB) {
 #pragma unroll 2
         for (int q = 0; q < BM / 8; ++q) {
             const gptr<float> er = G(e.emb) + (int64_t)__builtin_amdgcn_readlane(tokv, q) * D + 4 * lane;
-            float* xr_ = x + (m0 + 8 * wave + q) * D + 4 * lane;
+            float* xr_ = e.xout + (m0 + 8 * wave + q) * D + 4 * lane;
             *reinterpret_cast<float4*>(xr_) = ldg_f4(er);
             *reinterpret_cast<float4*>(xr_ + 256) = ldg_f4(er + 256);
         }
@@ -2419,12 +2414,10 @@ struct boa_ctx {
     int decode_halves = 2;
     bool ffn_outp = true;  // out_proj inside the feed-forward kernel (BOA_FFN_OUTP=0: separate GEMM)
     bool head_xq = true;   // compress tiles: head + quantiser in one kernel (BOA_HEAD_XQ=0: head GEMMs + k_encode_tile)
-    // full compress tiles: layer 0's mixer-input kernel gathers the embedding rows itself (BOA_EMBED_LN1=1) instead
-    // of the separate embedding pass.  Off by default: with it the compress pass measured 0.8% slower at d_model
-    // 256 (f32; the feed-forward kernels 4% slower beside the other lane group's kernels, the mixer kernel
-    // unchanged) and 0.3% at d_model 512 (bf16w).  emb_src is the current tile's (set only around its layer-0
+    // full compress tiles: layer 0's mixer-input kernel gathers the embedding rows itself instead of the separate
+    // embedding pass (BOA_EMBED_LN1=0: the pass).  emb_src is the current tile's (set only around its layer-0
     // launch).
-    bool embed_ln1 = false;
+    bool embed_ln1 = true;
     EmbedIn emb_src;
     // compress in groups of the lanes on their own streams (BOA_COMPRESS_HALVES=0: one stream; BOA_COMPRESS_GROUPS:
     // 2 or 3 groups, default 2)
@@ -2970,7 +2963,7 @@ struct EmbedFromBytes {
         x->emb_src = EmbedIn{};
         if (on) {
             x->emb_src.bytes = bytes; x->emb_src.stride = stride; x->emb_src.lens = lens;
-            x->emb_src.emb = x->emb; x->emb_src.t0 = t0; x->emb_src.V = x->V;
+            x->emb_src.emb = x->emb; x->emb_src.t0 = t0; x->emb_src.V = x->V;  // xout: the launch's x
         }
     }
     ~EmbedFromBytes() { x->emb_src = EmbedIn{}; }
@@ -2983,7 +2976,9 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc, int part = 7) {
     hipStream_t s = x->stream;
     const bool split = x->prec != BOA_PREC_F32;
     // layer 0 of a tile whose embedding pass was skipped: the mixer-input kernel gathers the rows
-    const EmbedIn ein = (l == 0) ? x->emb_src : EmbedIn{};
+    EmbedIn ein = (l == 0) ? x->emb_src : EmbedIn{};
+    ein.xout = x->x;
+    const bool emb = ein.bytes != nullptr;
     if (ein.bytes && !((mixin512_layer(x, w, Tc) || mixin_layer(x, w, Tc)) && (part & 1)))
         return boa_fail(BOA_ERR_STATE, "run_layer: no embedding pass for a tile without the mixer-input kernel");
     // FF hidden activations (split): two bf16 arrays in the memory of xz (dead after the scan)
@@ -2998,14 +2993,20 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc, int part = 7) {
         const double bytes = 4.0 * M * (d + di + di + R + 2 * NS) + 4.0 * 6 * B * di;
         if (w.in_w.l)
             PROF(PC_MIXIN, flops, bytes,
-                 hipLaunchKernelGGL((k_mixin512<3>), dim3((unsigned)B), dim3(512), 0, s, x->x, w.ln1_w, w.ln1_b,
-                                    w.in_w.p, w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs, x->dbc, hist,
-                                    (int)(x->pos % 3), ein));
+                 if (emb) hipLaunchKernelGGL((k_mixin512<3, true>), dim3((unsigned)B), dim3(512), 0, s, x->x, w.ln1_w,
+                                           w.ln1_b, w.in_w.p, w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs,
+                                           x->dbc, hist, (int)(x->pos % 3), ein);
+                 else hipLaunchKernelGGL((k_mixin512<3, false>), dim3((unsigned)B), dim3(512), 0, s, x->x, w.ln1_w,
+                                           w.ln1_b, w.in_w.p, w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs,
+                                           x->dbc, hist, (int)(x->pos % 3), ein));
         else
             PROF(PC_MIXIN, flops, bytes,
-                 hipLaunchKernelGGL((k_mixin512<2>), dim3((unsigned)B), dim3(512), 0, s, x->x, w.ln1_w, w.ln1_b,
-                                    w.in_w.p, w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs, x->dbc, hist,
-                                    (int)(x->pos % 3), ein));
+                 if (emb) hipLaunchKernelGGL((k_mixin512<2, true>), dim3((unsigned)B), dim3(512), 0, s, x->x, w.ln1_w,
+                                           w.ln1_b, w.in_w.p, w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs,
+                                           x->dbc, hist, (int)(x->pos % 3), ein);
+                 else hipLaunchKernelGGL((k_mixin512<2, false>), dim3((unsigned)B), dim3(512), 0, s, x->x, w.ln1_w,
+                                           w.ln1_b, w.in_w.p, w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs,
+                                           x->dbc, hist, (int)(x->pos % 3), ein));
     }
     // (fp32 mode included: its fragment-packed weights exist at d_model 256)
     const bool mix = mixin_layer(x, w, Tc);
@@ -3015,19 +3016,28 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc, int part = 7) {
         const double bytes = 4.0 * M * (d + di + di + R + 2 * NS) + 4.0 * 6 * B * di;
         if (x->prec == BOA_PREC_F32)
             PROF(PC_MIXIN, flops, bytes,
-                 hipLaunchKernelGGL((k_mixin<1>), dim3((unsigned)B), dim3(256), 0, s, x->x, w.ln1_w, w.ln1_b, w.in_w.p,
-                                    w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs, x->dbc, hist, (int)(x->pos % 3),
-                                    ein));
+                 if (emb) hipLaunchKernelGGL((k_mixin<1, true>), dim3((unsigned)B), dim3(256), 0, s, x->x, w.ln1_w,
+                                           w.ln1_b, w.in_w.p, w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs,
+                                           x->dbc, hist, (int)(x->pos % 3), ein);
+                 else hipLaunchKernelGGL((k_mixin<1, false>), dim3((unsigned)B), dim3(256), 0, s, x->x, w.ln1_w,
+                                           w.ln1_b, w.in_w.p, w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs,
+                                           x->dbc, hist, (int)(x->pos % 3), ein));
         else if (w.in_w.l)
             PROF(PC_MIXIN, flops, bytes,
-                 hipLaunchKernelGGL((k_mixin<3>), dim3((unsigned)B), dim3(256), 0, s, x->x, w.ln1_w, w.ln1_b, w.in_w.p,
-                                    w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs, x->dbc, hist, (int)(x->pos % 3),
-                                    ein));
+                 if (emb) hipLaunchKernelGGL((k_mixin<3, true>), dim3((unsigned)B), dim3(256), 0, s, x->x, w.ln1_w,
+                                           w.ln1_b, w.in_w.p, w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs,
+                                           x->dbc, hist, (int)(x->pos % 3), ein);
+                 else hipLaunchKernelGGL((k_mixin<3, false>), dim3((unsigned)B), dim3(256), 0, s, x->x, w.ln1_w,
+                                           w.ln1_b, w.in_w.p, w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs,
+                                           x->dbc, hist, (int)(x->pos % 3), ein));
         else
             PROF(PC_MIXIN, flops, bytes,
-                 hipLaunchKernelGGL((k_mixin<2>), dim3((unsigned)B), dim3(256), 0, s, x->x, w.ln1_w, w.ln1_b, w.in_w.p,
-                                    w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs, x->dbc, hist, (int)(x->pos % 3),
-                                    ein));
+                 if (emb) hipLaunchKernelGGL((k_mixin<2, true>), dim3((unsigned)B), dim3(256), 0, s, x->x, w.ln1_w,
+                                           w.ln1_b, w.in_w.p, w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs,
+                                           x->dbc, hist, (int)(x->pos % 3), ein);
+                 else hipLaunchKernelGGL((k_mixin<2, false>), dim3((unsigned)B), dim3(256), 0, s, x->x, w.ln1_w,
+                                           w.ln1_b, w.in_w.p, w.in_b, w.conv_w, w.conv_b, w.x_w.p, x->xz, x->xs,
+                                           x->dbc, hist, (int)(x->pos % 3), ein));
     } else if (!mix5 && !mix) {
     // LN1 + in_proj -> xz [M][2di]
     if (part & 1) {
