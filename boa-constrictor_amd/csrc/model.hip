@@ -570,9 +570,9 @@ __global__ void __launch_bounds__(256) k_embed_bytes(const uint8_t* __restrict__
 }
 
 // Layer 0 of a full compress tile reads its input rows straight from the embedding table in the LN1 prologue of
-// the mixer-input kernel (k_mixin, k_mixin512), which also writes them to x, the residual stream the feed-forward
-// kernel adds to; the separate embedding pass (k_embed_bytes) and its HBM round trip are skipped.  bytes null: the
-// kernel reads x as written by an embedding pass or the previous layer.
+// the mixer-input kernel (k_mixin, k_mixin512: template parameter EMB), which also writes them to x, the residual
+// stream the feed-forward kernel adds to; the separate embedding pass (k_embed_bytes) and its HBM round trip are
+// skipped.  Without EMB the kernels read x as written by an embedding pass or the previous layer, and ignore this.
 struct EmbedIn {
     const uint8_t* bytes = nullptr;  // the group's bytes [lanes][stride]
     int64_t stride = 0;
@@ -1607,7 +1607,7 @@ __global__ void __launch_bounds__(256, 2) k_mixin(const float* __restrict__ x, c
 #pragma unroll
         for (int r = 0; r < 4; ++r) GM(dbc)[(m0 + 16 * wave + m_of + r) * FW + 16 * j + ar] = dacc[j][r];
     // layer 0 of a compress tile: the embedding rows to x (the residual stream), gathered again from the table
-    // (L2) and stored last: stored in the prologue, the weight loads behind them waited for their completion
+    // (an L2 hit) and stored after the tile's other work (stored in the prologue instead: the same time)
     if constexpr (EMB) {
 #pragma unroll 4
         for (int q = 0; q < BM / 4; ++q)
@@ -2932,15 +2932,6 @@ static void launch_scan(boa_ctx* x, const LayerW& w, float* ssm, int B, int Tc) 
                            (int64_t)2 * di, w.dt_w, w.dt_b, w.Aneg, w.D, ssm, di, Tc, x->ah, x->al);
 }
 
-// One block of the model over B lanes x Tc positions, in place on ctx->x.
-//   fp32 mode:  LN stats -> in_proj(LN on load) -> conv -> x_proj -> scan (y in place of xs) -> out_proj ->
-//               LN stats -> FF1(LN on load, GELU) into xz -> FF2(+residual) into x
-//   split modes: LN+split -> in_proj -> conv -> x_proj -> scan (y split) -> out_proj -> LN+split ->
-//               FF1(GELU, split output into xz's memory) -> FF2(+residual) into x
-// part selects which of three consecutive groups of the layer to launch (bits, 7 = the whole layer):
-//   1: LN1 + in_proj;  2: conv + x_proj + scan (the state traffic);  4: out_proj + LN2 + feed-forward.
-// Where a fused compress-tile kernel (k_mixin, k_mixin512) covers LN1 through x_proj, bit 1 launches it and
-// bit 2 the scan alone.
 // Whether a layer of a Tc-position tile runs LN1 through x_proj as one mixer-input kernel: k_mixin512 (d_model
 // 512, split modes) or k_mixin (d_model 256, every mode), on full tiles with fragment-packed weights.
 static bool mixin512_layer(const boa_ctx* x, const LayerW& w, int Tc) {
@@ -2969,6 +2960,15 @@ struct EmbedFromBytes {
     ~EmbedFromBytes() { x->emb_src = EmbedIn{}; }
 };
 
+// One block of the model over B lanes x Tc positions, in place on ctx->x.
+//   fp32 mode:  LN stats -> in_proj(LN on load) -> conv -> x_proj -> scan (y in place of xs) -> out_proj ->
+//               LN stats -> FF1(LN on load, GELU) into xz -> FF2(+residual) into x
+//   split modes: LN+split -> in_proj -> conv -> x_proj -> scan (y split) -> out_proj -> LN+split ->
+//               FF1(GELU, split output into xz's memory) -> FF2(+residual) into x
+// part selects which of three consecutive groups of the layer to launch (bits, 7 = the whole layer):
+//   1: LN1 + in_proj;  2: conv + x_proj + scan (the state traffic);  4: out_proj + LN2 + feed-forward.
+// Where a fused compress-tile kernel (k_mixin, k_mixin512) covers LN1 through x_proj, bit 1 launches it and
+// bit 2 the scan alone.
 static int run_layer(boa_ctx* x, int l, int B, int Tc, int part = 7) {
     const LayerW& w = x->layers[l];
     const int d = x->d, di = x->di, NS = x->NS, R = x->R;
@@ -2979,7 +2979,7 @@ static int run_layer(boa_ctx* x, int l, int B, int Tc, int part = 7) {
     EmbedIn ein = (l == 0) ? x->emb_src : EmbedIn{};
     ein.xout = x->x;
     const bool emb = ein.bytes != nullptr;
-    if (ein.bytes && !((mixin512_layer(x, w, Tc) || mixin_layer(x, w, Tc)) && (part & 1)))
+    if (emb && !((mixin512_layer(x, w, Tc) || mixin_layer(x, w, Tc)) && (part & 1)))
         return boa_fail(BOA_ERR_STATE, "run_layer: no embedding pass for a tile without the mixer-input kernel");
     // FF hidden activations (split): two bf16 arrays in the memory of xz (dead after the scan)
     uint16_t* gh = reinterpret_cast<uint16_t*>(x->xz);
