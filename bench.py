@@ -601,7 +601,7 @@ def main():
     ap.add_argument("--payload-mib", type=int, default=64)
     ap.add_argument("--chunks", type=int, default=4096)
     ap.add_argument("--tile-len", type=int, default=int(os.environ.get("BOA_TILE_LEN", "64")))
-    ap.add_argument("--cpu-steps", type=int, default=300, help="coded positions per chunk in the CPU sample")
+    ap.add_argument("--cpu-steps", type=int, default=500, help="coded positions per chunk in the CPU sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--workload", choices=["codec", "coder", "config4"], default="codec",
                     help="codec: configs[2]+[3] (the metric); coder: configs[1], the range coder alone; config4: "
